@@ -1,0 +1,125 @@
+// Device-side helpers shared by the gfx950 kernels of libcascade_hip.
+//
+// Conventions used throughout the library:
+//   * bf16 tensors travel as raw uint16_t; arithmetic is fp32.
+//   * float -> bf16 rounding is round-to-nearest-even (the hardware
+//     v_cvt_pk_bf16_f32 conversion), the same rounding torch uses for
+//     Tensor.to(torch.bfloat16).
+//   * One wavefront is 64 lanes. A 16-byte load (u32x4) carries 8 bf16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cascade {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Value of f after a round trip through bf16 (models a torch bf16 result).
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+__device__ __forceinline__ float lo_bf16(uint32_t pair) {
+  return __uint_as_float(pair << 16);
+}
+
+__device__ __forceinline__ float hi_bf16(uint32_t pair) {
+  return __uint_as_float(pair & 0xffff0000u);
+}
+
+// Reinterprets one packed dword as two bf16.  The dword is taken by value:
+// hipcc (ROCm 7.2) miscompiles __builtin_bit_cast applied directly to an
+// ext_vector element expression such as v.y (it reads element 0 instead).
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) {
+  return __builtin_bit_cast(bf16x2_t, v);
+}
+
+// acc + sum_{i<8} a[i] * b[i] for two 8 x bf16 vectors, fp32 accumulation
+// (v_dot2_f32_bf16: two products per instruction).
+__device__ __forceinline__ float dot8_bf16(u32x4 a, u32x4 b, float acc) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t ae = a[e];
+    const uint32_t be = b[e];
+    acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(ae), as_bf16x2(be), acc,
+                                          false);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15).
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
+    uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
+    uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k keys. A (value, index) pair maps to one uint64 whose unsigned order
+// is "value descending, then index ascending", so selecting the k largest
+// keys is an exact, deterministic top-k with lower-index-first tie breaking.
+// -0.0 is folded into +0.0 and every NaN into one positive quiet NaN, which
+// sorts above +inf (torch.topk also ranks NaN highest). Key 0 never encodes
+// a real candidate and serves as the empty sentinel.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ordered_bits(float v) {
+  uint32_t u = __float_as_uint(v);
+  if (v == 0.0f) u = 0u;
+  if (v != v) u = 0x7fc00000u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float from_ordered_bits(uint32_t o) {
+  uint32_t u = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t index) {
+  return (static_cast<uint64_t>(ordered_bits(v)) << 32) |
+         static_cast<uint64_t>(0xffffffffu - index);
+}
+
+__device__ __forceinline__ float key_value(uint64_t key) {
+  return from_ordered_bits(static_cast<uint32_t>(key >> 32));
+}
+
+__device__ __forceinline__ int64_t key_index(uint64_t key) {
+  return static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key));
+}
+
+}  // namespace cascade

@@ -1,0 +1,534 @@
+// M=1 bf16 GEMV family for the batch=1 decode path on gfx950.
+//
+// One wavefront owns a tile of R weight rows and the whole reduction
+// dimension K.  Lane l reads 16-byte pieces l, l+64, l+128, ... of each row,
+// so every load instruction of a wave covers 1 KiB of one row, fully
+// coalesced.  All loads of a tile are issued before the workgroup builds its
+// copy of the (optionally RMS-normalised) input vector in LDS, so the
+// prologue hides under HBM latency.  Products use v_dot2_f32_bf16 (two bf16
+// products accumulated into fp32 per instruction); the row sums are reduced
+// across the wave and finished by an epilogue that reproduces the reference's
+// bf16 rounding points:
+//   plain     y = bf16(acc)                          F.linear
+//   residual  y = bf16(res + bf16(acc))              residual + F.linear
+//   qkv_rope  rows (d, d+64) of one head per tile -> RoPE in bf16, then the
+//             q buffer or the layer's KV cache       llama31.py:206-218
+//   swiglu    gate row i and up row i per tile ->
+//             bf16(bf16(silu(bf16(g))) * bf16(u))    llama31.py:264-275
+//   silu / mul  the matrix-granularity halves of swiglu.
+#include "cascade_device.h"
+#include "cascade_internal.h"
+
+namespace cascade {
+
+enum GemvEpilogue : int {
+  kPlain = 0,
+  kResidual = 1,
+  kQkvRope = 2,
+  kSwiglu = 3,
+  kSilu = 4,
+  kMul = 5,
+};
+
+struct GemvArgs {
+  const uint16_t *w0;  // plain/residual/silu/mul: W; qkv: Wq; swiglu: Wgate
+  const uint16_t *w1;  // qkv: Wk; swiglu: Wup
+  const uint16_t *w2;  // qkv: Wv
+  int64_t n0, n1, n2;  // rows of w0 / w1 / w2 (swiglu: n0 = n_half)
+  int64_t k;
+  const uint16_t *x;
+  const uint16_t *norm_w;  // nullable: RMSNorm weight applied to x first
+  float eps;
+  uint16_t *y;
+  const uint16_t *aux;  // residual (kResidual) or gate (kMul)
+  const uint16_t *rope_cos;
+  const uint16_t *rope_sin;
+  uint16_t *k_out;
+  uint16_t *v_out;
+  int64_t kv_head_stride;
+  int64_t n_tiles;
+};
+
+constexpr int kHeadDim = 128;
+constexpr int kHalfHead = 64;
+
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+
+// Builds the GEMV input vector in LDS.  With a norm weight it applies
+// _rms_norm (llama31.py:21-25): fp32 mean of squares, 1/sqrt(var + eps),
+// x * r rounded to bf16, times the bf16 weight rounded to bf16.
+template <int THREADS>
+__device__ void stage_input(const GemvArgs &a, u32x4 *xs) {
+  const int64_t nvec = a.k >> 3;
+  const u32x4 *xg = reinterpret_cast<const u32x4 *>(a.x);
+  if (a.norm_w == nullptr) {
+    for (int64_t j = threadIdx.x; j < nvec; j += THREADS) xs[j] = xg[j];
+    return;
+  }
+  __shared__ float red[THREADS / kWave];
+  float ss = 0.0f;
+  for (int64_t j = threadIdx.x; j < nvec; j += THREADS) {
+    const u32x4 v = xg[j];
+    xs[j] = v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = lo_bf16(v[e]);
+      const float hi = hi_bf16(v[e]);
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < THREADS / kWave; ++i) total += red[i];
+  const float variance = total * (1.0f / static_cast<float>(a.k));
+  const float r = 1.0f / __builtin_sqrtf(variance + a.eps);
+  const u32x4 *wg = reinterpret_cast<const u32x4 *>(a.norm_w);
+  for (int64_t j = threadIdx.x; j < nvec; j += THREADS) {
+    const u32x4 v = xs[j];
+    const u32x4 w = wg[j];
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float nlo = round_bf16(lo_bf16(v[e]) * r);
+      const float nhi = round_bf16(hi_bf16(v[e]) * r);
+      const uint32_t olo = f32_to_bf16(lo_bf16(w[e]) * nlo);
+      const uint32_t ohi = f32_to_bf16(hi_bf16(w[e]) * nhi);
+      o[e] = olo | (ohi << 16);
+    }
+    xs[j] = o;
+  }
+}
+
+__device__ __forceinline__ float silu_f32(float g) {
+  return g / (1.0f + expf(-g));
+}
+
+// Row addressing of one tile.  Returns, per tile row, the row's weight
+// pointer and whether the row exists.
+template <int EPI, int R>
+__device__ __forceinline__ void tile_rows(const GemvArgs &a, int64_t tile,
+                                          bool tile_ok,
+                                          const uint16_t *(&wrow)[R],
+                                          bool (&ok)[R]) {
+  if constexpr (EPI == kQkvRope) {
+    constexpr int P = R / 2;
+    constexpr int kTilesPerHead = kHalfHead / P;
+    const int64_t head = tile / kTilesPerHead;
+    const int d0 = static_cast<int>(tile % kTilesPerHead) * P;
+    const int64_t hq = a.n0 / kHeadDim, hk = a.n1 / kHeadDim;
+    const uint16_t *base;
+    int64_t lh;
+    if (head < hq) {
+      base = a.w0;
+      lh = head;
+    } else if (head < hq + hk) {
+      base = a.w1;
+      lh = head - hq;
+    } else {
+      base = a.w2;
+      lh = head - hq - hk;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int d = d0 + (r % P) + (r >= P ? kHalfHead : 0);
+      ok[r] = tile_ok;
+      wrow[r] = tile_ok ? base + (lh * kHeadDim + d) * a.k : a.w0;
+    }
+  } else if constexpr (EPI == kSwiglu) {
+    constexpr int P = R / 2;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t i = tile * P + (r % P);
+      ok[r] = tile_ok && i < a.n0;
+      wrow[r] = ok[r] ? (r < P ? a.w0 : a.w1) + i * a.k : a.w0;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = tile * R + r;
+      ok[r] = tile_ok && row < a.n0;
+      wrow[r] = ok[r] ? a.w0 + row * a.k : a.w0;
+    }
+  }
+}
+
+template <int EPI, int R>
+__device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
+                                         const float (&acc)[R],
+                                         const bool (&ok)[R]) {
+  if constexpr (EPI == kQkvRope) {
+    constexpr int P = R / 2;
+    constexpr int kTilesPerHead = kHalfHead / P;
+    const int64_t head = tile / kTilesPerHead;
+    const int d0 = static_cast<int>(tile % kTilesPerHead) * P;
+    const int64_t hq = a.n0 / kHeadDim, hk = a.n1 / kHeadDim;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int d = d0 + p;
+      const float xa = round_bf16(acc[p]);      // element d of the head
+      const float xb = round_bf16(acc[p + P]);  // element d + 64
+      uint16_t oa, ob;
+      if (head < hq + hk) {
+        // apply_rotary_pos_emb: x*cos + rotate_half(x)*sin, every product
+        // and the sum rounded to bf16; cos/sin are bf16 and identical for
+        // d and d + 64 (emb = cat(freqs, freqs)).
+        const float c = bf16_to_f32(a.rope_cos[d]);
+        const float s = bf16_to_f32(a.rope_sin[d]);
+        oa = f32_to_bf16(round_bf16(xa * c) + round_bf16(-xb * s));
+        ob = f32_to_bf16(round_bf16(xb * c) + round_bf16(xa * s));
+      } else {
+        oa = f32_to_bf16(xa);
+        ob = f32_to_bf16(xb);
+      }
+      if (head < hq) {
+        a.y[head * kHeadDim + d] = oa;
+        a.y[head * kHeadDim + d + kHalfHead] = ob;
+      } else if (head < hq + hk) {
+        uint16_t *dst = a.k_out + (head - hq) * a.kv_head_stride;
+        dst[d] = oa;
+        dst[d + kHalfHead] = ob;
+      } else {
+        uint16_t *dst = a.v_out + (head - hq - hk) * a.kv_head_stride;
+        dst[d] = oa;
+        dst[d + kHalfHead] = ob;
+      }
+    }
+  } else if constexpr (EPI == kSwiglu) {
+    constexpr int P = R / 2;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (!ok[p]) continue;
+      const float g = round_bf16(acc[p]);
+      const float u = round_bf16(acc[p + P]);
+      const float s = round_bf16(silu_f32(g));
+      a.y[tile * P + p] = f32_to_bf16(s * u);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (!ok[r]) continue;
+      const int64_t row = tile * R + r;
+      const float v = round_bf16(acc[r]);
+      float out;
+      if constexpr (EPI == kPlain) {
+        out = v;
+      } else if constexpr (EPI == kResidual) {
+        out = bf16_to_f32(a.aux[row]) + v;
+      } else if constexpr (EPI == kSilu) {
+        out = silu_f32(v);
+      } else {  // kMul
+        out = bf16_to_f32(a.aux[row]) * v;
+      }
+      a.y[row] = f32_to_bf16(out);
+    }
+  }
+}
+
+// KC > 0: K == KC * 512, loads fully unrolled and issued up front.
+// KC == 0: any K that is a multiple of 8 (loop over 16-byte pieces).
+template <int KC, int R, int WAVES, int EPI>
+__global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
+  extern __shared__ u32x4 xs[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
+  const bool tile_ok = tile < a.n_tiles;
+
+  const uint16_t *wrow[R];
+  bool ok[R];
+  tile_rows<EPI, R>(a, tile, tile_ok, wrow, ok);
+
+  float acc[R];
+  if constexpr (KC > 0) {
+    u32x4 wv[R][KC];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        wv[r][c] = ok[r] ? load16(wrow[r] + (c * kWave + lane) * 8)
+                         : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    stage_input<WAVES * kWave>(a, xs);
+    __syncthreads();
+    float acc2[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      acc[r] = 0.0f;
+      acc2[r] = 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const u32x4 xv = xs[c * kWave + lane];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (c & 1)
+          acc2[r] = dot8_bf16(wv[r][c], xv, acc2[r]);
+        else
+          acc[r] = dot8_bf16(wv[r][c], xv, acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] += acc2[r];
+  } else {
+    stage_input<WAVES * kWave>(a, xs);
+    __syncthreads();
+    const int64_t nvec = a.k >> 3;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int64_t j = lane; j < nvec; j += kWave) {
+      const u32x4 xv = xs[j];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (ok[r]) acc[r] = dot8_bf16(load16(wrow[r] + j * 8), xv, acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane == 0 && tile_ok) epilogue<EPI, R>(a, tile, acc, ok);
+}
+
+template <int KC, int R, int WAVES, int EPI>
+static hipError_t launch_gemv(const GemvArgs &a, hipStream_t stream) {
+  const int64_t blocks = (a.n_tiles + WAVES - 1) / WAVES;
+  const size_t lds = static_cast<size_t>(a.k) * 2;
+  hipLaunchKernelGGL((gemv_kernel<KC, R, WAVES, EPI>), dim3(blocks),
+                     dim3(WAVES * kWave), lds, stream, a);
+  return hipGetLastError();
+}
+
+// Shape policy: K = 4096 rows are 8 KiB (8 loads per lane), K = 14336 rows
+// are 28 KiB (28 loads per lane); other K use the looped kernel.
+template <int R, int EPI>
+static hipError_t dispatch_gemv(const GemvArgs &a, hipStream_t stream) {
+  if (a.k == 4096) return launch_gemv<8, R, 4, EPI>(a, stream);
+  if constexpr (R == 1) {
+    if (a.k == 14336) return launch_gemv<28, 1, 4, EPI>(a, stream);
+  }
+  return launch_gemv<0, R, 4, EPI>(a, stream);
+}
+
+static int check_common(const void *w, const void *x, int64_t n, int64_t k) {
+  if (w == nullptr || x == nullptr || n <= 0 || k <= 0) return CASCADE_EINVAL;
+  if ((k & 7) != 0 || !aligned16(w) || !aligned16(x)) return CASCADE_EALIGN;
+  if (k * 2 > kMaxGemvLdsBytes) return CASCADE_ESHAPE;
+  return 0;
+}
+
+}  // namespace cascade
+
+using namespace cascade;
+
+extern "C" int cascade_gemv_bf16(const void *w, const void *x, void *y,
+                                 int64_t n, int64_t k, void *stream) {
+  if (int e = check_common(w, x, n, k)) return e;
+  if (y == nullptr) return CASCADE_EINVAL;
+  GemvArgs a{};
+  a.w0 = static_cast<const uint16_t *>(w);
+  a.n0 = n;
+  a.k = k;
+  a.x = static_cast<const uint16_t *>(x);
+  a.y = static_cast<uint16_t *>(y);
+  a.n_tiles = (n + 1) / 2;
+  return dispatch_gemv<2, kPlain>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_gemv_residual_bf16(const void *w, const void *x,
+                                          const void *residual, void *y,
+                                          int64_t n, int64_t k, void *stream) {
+  if (int e = check_common(w, x, n, k)) return e;
+  if (y == nullptr || residual == nullptr) return CASCADE_EINVAL;
+  GemvArgs a{};
+  a.w0 = static_cast<const uint16_t *>(w);
+  a.n0 = n;
+  a.k = k;
+  a.x = static_cast<const uint16_t *>(x);
+  a.y = static_cast<uint16_t *>(y);
+  a.aux = static_cast<const uint16_t *>(residual);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (k == 4096) {
+    a.n_tiles = (n + 1) / 2;
+    return dispatch_gemv<2, kResidual>(a, s);
+  }
+  a.n_tiles = n;
+  return dispatch_gemv<1, kResidual>(a, s);
+}
+
+extern "C" int cascade_qkv_rope_bf16(const void *wq, const void *wk,
+                                     const void *wv, int64_t nq, int64_t nk,
+                                     int64_t nv, int64_t k, const void *x,
+                                     const void *norm_weight, float eps,
+                                     const void *rope_cos,
+                                     const void *rope_sin, void *q_out,
+                                     void *k_out, void *v_out,
+                                     int64_t kv_head_stride, void *stream) {
+  if (nq < 0 || nk < 0 || nv < 0) return CASCADE_EINVAL;
+  if ((nq % kHeadDim) || (nk % kHeadDim) || (nv % kHeadDim))
+    return CASCADE_ESHAPE;
+  const int64_t total = nq + nk + nv;
+  if (total == 0 || x == nullptr || k <= 0) return CASCADE_EINVAL;
+  if ((k & 7) != 0 || !aligned16(x) || !aligned16(norm_weight))
+    return CASCADE_EALIGN;
+  if (k * 2 > kMaxGemvLdsBytes) return CASCADE_ESHAPE;
+  if (nq && (wq == nullptr || q_out == nullptr || !aligned16(wq)))
+    return wq == nullptr || q_out == nullptr ? CASCADE_EINVAL : CASCADE_EALIGN;
+  if (nk && (wk == nullptr || k_out == nullptr || !aligned16(wk)))
+    return wk == nullptr || k_out == nullptr ? CASCADE_EINVAL : CASCADE_EALIGN;
+  if (nv && (wv == nullptr || v_out == nullptr || !aligned16(wv)))
+    return wv == nullptr || v_out == nullptr ? CASCADE_EINVAL : CASCADE_EALIGN;
+  if ((nq || nk) && (rope_cos == nullptr || rope_sin == nullptr))
+    return CASCADE_EINVAL;
+  if ((nk || nv) && kv_head_stride < kHeadDim) return CASCADE_EINVAL;
+  GemvArgs a{};
+  a.w0 = static_cast<const uint16_t *>(wq);
+  a.w1 = static_cast<const uint16_t *>(wk);
+  a.w2 = static_cast<const uint16_t *>(wv);
+  a.n0 = nq;
+  a.n1 = nk;
+  a.n2 = nv;
+  a.k = k;
+  a.x = static_cast<const uint16_t *>(x);
+  a.norm_w = static_cast<const uint16_t *>(norm_weight);
+  a.eps = eps;
+  a.y = static_cast<uint16_t *>(q_out);
+  a.rope_cos = static_cast<const uint16_t *>(rope_cos);
+  a.rope_sin = static_cast<const uint16_t *>(rope_sin);
+  a.k_out = static_cast<uint16_t *>(k_out);
+  a.v_out = static_cast<uint16_t *>(v_out);
+  a.kv_head_stride = kv_head_stride;
+  a.n_tiles = total / 2;  // two rows (d, d + 64) per tile
+  return dispatch_gemv<2, kQkvRope>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_gate_up_swiglu_bf16(const void *w_gate,
+                                           const void *w_up, int64_t n_half,
+                                           int64_t k, const void *x,
+                                           const void *norm_weight, float eps,
+                                           void *y, void *stream) {
+  if (int e = check_common(w_gate, x, n_half, k)) return e;
+  if (w_up == nullptr || y == nullptr) return CASCADE_EINVAL;
+  if (!aligned16(w_up) || !aligned16(norm_weight)) return CASCADE_EALIGN;
+  GemvArgs a{};
+  a.w0 = static_cast<const uint16_t *>(w_gate);
+  a.w1 = static_cast<const uint16_t *>(w_up);
+  a.n0 = n_half;
+  a.k = k;
+  a.x = static_cast<const uint16_t *>(x);
+  a.norm_w = static_cast<const uint16_t *>(norm_weight);
+  a.eps = eps;
+  a.y = static_cast<uint16_t *>(y);
+  a.n_tiles = n_half;  // one gate row + one up row per tile
+  return dispatch_gemv<2, kSwiglu>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_gate_silu_bf16(const void *w_gate, int64_t n, int64_t k,
+                                      const void *x, const void *norm_weight,
+                                      float eps, void *y, void *stream) {
+  if (int e = check_common(w_gate, x, n, k)) return e;
+  if (y == nullptr) return CASCADE_EINVAL;
+  if (!aligned16(norm_weight)) return CASCADE_EALIGN;
+  GemvArgs a{};
+  a.w0 = static_cast<const uint16_t *>(w_gate);
+  a.n0 = n;
+  a.k = k;
+  a.x = static_cast<const uint16_t *>(x);
+  a.norm_w = static_cast<const uint16_t *>(norm_weight);
+  a.eps = eps;
+  a.y = static_cast<uint16_t *>(y);
+  a.n_tiles = (n + 1) / 2;
+  return dispatch_gemv<2, kSilu>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_up_mul_bf16(const void *w_up, int64_t n, int64_t k,
+                                   const void *x, const void *norm_weight,
+                                   float eps, const void *gate, void *y,
+                                   void *stream) {
+  if (int e = check_common(w_up, x, n, k)) return e;
+  if (y == nullptr || gate == nullptr) return CASCADE_EINVAL;
+  if (!aligned16(norm_weight)) return CASCADE_EALIGN;
+  GemvArgs a{};
+  a.w0 = static_cast<const uint16_t *>(w_up);
+  a.n0 = n;
+  a.k = k;
+  a.x = static_cast<const uint16_t *>(x);
+  a.norm_w = static_cast<const uint16_t *>(norm_weight);
+  a.eps = eps;
+  a.y = static_cast<uint16_t *>(y);
+  a.aux = static_cast<const uint16_t *>(gate);
+  a.n_tiles = (n + 1) / 2;
+  return dispatch_gemv<2, kMul>(a, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Standalone RMSNorm, one workgroup per row (the final norm before the LM
+// head, llama31.py:325-329, and any caller that wants the normalised vector).
+namespace cascade {
+
+constexpr int kNormThreads = 256;
+
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
+    const uint16_t *x, const uint16_t *w, uint16_t *y, int64_t n, float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * n);
+  const u32x4 *wr = reinterpret_cast<const u32x4 *>(w);
+  u32x4 *yr = reinterpret_cast<u32x4 *>(y + row * n);
+  const int64_t nvec = n >> 3;
+  float ss = 0.0f;
+  for (int64_t j = threadIdx.x; j < nvec; j += kNormThreads) {
+    const u32x4 v = xr[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = lo_bf16(v[e]);
+      const float hi = hi_bf16(v[e]);
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / kWave; ++i) total += red[i];
+  const float r =
+      1.0f / __builtin_sqrtf(total * (1.0f / static_cast<float>(n)) + eps);
+  for (int64_t j = threadIdx.x; j < nvec; j += kNormThreads) {
+    const u32x4 v = xr[j];
+    const u32x4 wv = wr[j];
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float nlo = round_bf16(lo_bf16(v[e]) * r);
+      const float nhi = round_bf16(hi_bf16(v[e]) * r);
+      o[e] = static_cast<uint32_t>(f32_to_bf16(lo_bf16(wv[e]) * nlo)) |
+             (static_cast<uint32_t>(f32_to_bf16(hi_bf16(wv[e]) * nhi)) << 16);
+    }
+    yr[j] = o;
+  }
+}
+
+}  // namespace cascade
+
+extern "C" int cascade_rmsnorm_bf16(const void *x, const void *weight, void *y,
+                                    int64_t rows, int64_t n, float eps,
+                                    void *stream) {
+  if (x == nullptr || weight == nullptr || y == nullptr || rows <= 0 ||
+      n <= 0 || rows > 0x7fffffff)
+    return CASCADE_EINVAL;
+  if ((n & 7) || !aligned16(x) || !aligned16(weight) || !aligned16(y))
+    return CASCADE_EALIGN;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)),
+                     dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t *>(x),
+                     static_cast<const uint16_t *>(weight),
+                     static_cast<uint16_t *>(y), n, eps);
+  return hipGetLastError();
+}

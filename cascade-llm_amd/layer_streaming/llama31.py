@@ -1,0 +1,451 @@
+"""Llama-3.1-8B decode executor running on the libcascade_hip kernels.
+
+Public surface as in the reference (layer_streaming/llama31.py):
+``Llama31DecodeExecutor(config, resident, kv_cache, vocab_runtime, top_k,
+return_full_logits)`` with ``begin`` / ``__call__`` / ``finish``,
+``SimpleKVCache`` and ``DecodeState``.  The executor is the ``compute_unit``
+callback of the runtimes: each call enqueues the kernels of one transfer
+unit on the current (compute) stream.
+
+Operation -> kernels (reference lines in parentheses):
+  qkv / q_proj / k_proj / v_proj   cascade_qkv_rope_bf16: input RMSNorm,
+      the projection(s), RoPE and the KV-cache write in one launch per
+      token (:169-180, :206-218, :241-245)
+  o_proj     cascade_decode_attention_bf16 then cascade_gemv_residual_bf16
+      (:182-234, :246-251)
+  gate_up    cascade_gate_up_swiglu_bf16 (post-attention RMSNorm, both
+      projections, SiLU and the product; :252-275)
+  gate_proj / up_proj   cascade_gate_silu_bf16 / cascade_up_mul_bf16
+  down_proj  cascade_gemv_residual_bf16 (:272-279)
+  finish     cascade_rmsnorm_bf16 + the LM head (cascade_lm_head_topk_bf16,
+      resident head or VocabStreamingRuntime) (:324-349)
+A prefill of S tokens runs the per-token kernels for t = 0..S-1 inside each
+unit; token t attends to positions <= past + t, which is the causal SDPA of
+the reference's prefill (:223-229).
+"""
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _hip
+from .plan import projection_key
+from .rope import RopeTable, rope_parameters
+
+__all__ = [
+    "LLAMA31_8B_MODEL_ID",
+    "MATRIX_ORDER",
+    "Llama31Config",
+    "SimpleKVCache",
+    "DecodeState",
+    "Llama31DecodeExecutor",
+]
+
+LLAMA31_8B_MODEL_ID = "meta-llama/Llama-3.1-8B"
+MATRIX_ORDER = (
+    "q_proj",
+    "k_proj",
+    "v_proj",
+    "o_proj",
+    "gate_proj",
+    "up_proj",
+    "down_proj",
+)
+
+
+@dataclass
+class Llama31Config:
+    """The Llama-3.1-8B config fields the executor reads (stand-in for a
+    transformers LlamaConfig when there is no checkpoint directory)."""
+
+    hidden_size: int = 4096
+    intermediate_size: int = 14336
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    vocab_size: int = 128256
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    rope_scaling: dict = field(
+        default_factory=lambda: {
+            "rope_type": "llama3",
+            "factor": 8.0,
+            "low_freq_factor": 1.0,
+            "high_freq_factor": 4.0,
+            "original_max_position_embeddings": 8192,
+        }
+    )
+    max_position_embeddings: int = 131072
+    tie_word_embeddings: bool = False
+
+
+class SimpleKVCache:
+    """Single-request KV cache, preallocated in HBM and grown by doubling.
+
+    Layout: one bf16 buffer [layers, 2 (K, V), kv_heads, capacity, head_dim];
+    the attention kernel reads KV head g of a layer at
+    ``g * head_stride`` elements.  ``entries[layer]`` gives the reference's
+    (key, value) pair of [1, kv_heads, length, head_dim] views
+    (reference llama31.py:34-54).
+    """
+
+    def __init__(self, layer_count=32, num_kv_heads=8, head_dim=128,
+                 capacity=0, device=None):
+        self.layer_count = int(layer_count)
+        self.num_kv_heads = int(num_kv_heads)
+        self.head_dim = int(head_dim)
+        self.device = None if device is None else torch.device(device)
+        self.capacity = 0
+        self.buffer = None
+        self.lengths = [0] * self.layer_count
+        if capacity:
+            self.reserve(capacity)
+
+    @property
+    def head_stride(self):
+        return self.capacity * self.head_dim
+
+    def reserve(self, length, device=None):
+        """Make room for ``length`` positions (copies existing entries)."""
+
+        if device is not None and self.device is None:
+            self.device = torch.device(device)
+        if length <= self.capacity:
+            return
+        if self.device is None:
+            raise RuntimeError("KV cache device is unknown")
+        capacity = max(int(length), 2 * self.capacity, 256)
+        capacity = -(-capacity // 256) * 256
+        buffer = torch.empty(
+            (self.layer_count, 2, self.num_kv_heads, capacity, self.head_dim),
+            dtype=torch.bfloat16,
+            device=self.device,
+        )
+        if self.buffer is not None:
+            used = max(self.lengths)
+            if used:
+                buffer[:, :, :, :used].copy_(self.buffer[:, :, :, :used])
+        self.buffer = buffer
+        self.capacity = capacity
+
+    def layer_base(self, layer_index, which):
+        """Flat view from position 0 of KV head 0 (which: 0 = K, 1 = V)."""
+
+        return self.buffer[layer_index, which].view(-1)
+
+    def sequence_length(self):
+        return self.lengths[0]
+
+    @property
+    def entries(self):
+        out = []
+        for layer in range(self.layer_count):
+            n = self.lengths[layer]
+            if n == 0:
+                out.append(None)
+            else:
+                out.append(
+                    (
+                        self.buffer[layer, 0, :, :n].unsqueeze(0),
+                        self.buffer[layer, 1, :, :n].unsqueeze(0),
+                    )
+                )
+        return out
+
+    def append(self, layer_index, key, value):
+        """Append [1, kv_heads, S, head_dim] key / value tensors."""
+
+        n = key.shape[-2]
+        start = self.lengths[layer_index]
+        self.reserve(start + n, device=key.device)
+        self.buffer[layer_index, 0, :, start : start + n].copy_(key[0])
+        self.buffer[layer_index, 1, :, start : start + n].copy_(value[0])
+        self.lengths[layer_index] = start + n
+        return self.entries[layer_index]
+
+    def set_length(self, layer_index, length):
+        self.lengths[layer_index] = int(length)
+
+    def clear(self):
+        self.lengths = [0] * self.layer_count
+
+
+@dataclass
+class DecodeState:
+    hidden_states: torch.Tensor
+    position_ids: torch.Tensor
+    layer_values: dict = field(default_factory=dict)
+    logits: object = None
+    topk_values: object = None
+    topk_indices: object = None
+    positions: tuple = ()
+
+
+_EXPECTED = {
+    "hidden_size": 4096,
+    "intermediate_size": 14336,
+    "num_attention_heads": 32,
+    "num_key_value_heads": 8,
+    "vocab_size": 128256,
+}
+
+
+class Llama31DecodeExecutor:
+    """Stateful callbacks consumed by the runtimes (one unpadded request: a
+    multi-token prefill, then one-token decode calls)."""
+
+    def __init__(self, config, resident, kv_cache=None, vocab_runtime=None,
+                 top_k=10, return_full_logits=False):
+        _hip.load()  # no kernels, no executor
+        layers = getattr(resident, "plan", None)
+        layers = layers.num_layers if layers is not None else 32
+        expected = dict(_EXPECTED, num_hidden_layers=layers)
+        for name, value in expected.items():
+            if getattr(config, name, None) != value:
+                raise ValueError(
+                    "config {}={} is not Llama-3.1-8B value {}".format(
+                        name, getattr(config, name, None), value
+                    )
+                )
+        self.config = config
+        self.resident = resident
+        self.vocab_runtime = vocab_runtime
+        self.top_k = int(top_k)
+        self.return_full_logits = bool(return_full_logits)
+        if self.top_k < 1:
+            raise ValueError("top_k must be positive")
+        if self.top_k > 64:
+            raise ValueError("top_k above 64 is not supported by the LM-head kernel")
+        self.device = resident.device
+        self.hidden = config.hidden_size
+        self.head_dim = config.hidden_size // config.num_attention_heads
+        self.n_heads = config.num_attention_heads
+        self.n_kv_heads = config.num_key_value_heads
+        self.kv_groups = self.n_heads // self.n_kv_heads
+        self.eps = float(config.rms_norm_eps)
+        self.scale = self.head_dim ** -0.5
+        self.kv_cache = kv_cache or SimpleKVCache(
+            config.num_hidden_layers, self.n_kv_heads, self.head_dim,
+            device=self.device,
+        )
+        if self.kv_cache.device is None:
+            self.kv_cache.device = self.device
+        self.rope = RopeTable(self.head_dim, rope_parameters(config), self.device)
+        self._norms = [
+            (
+                resident["model.layers.{}.input_layernorm.weight".format(i)],
+                resident["model.layers.{}.post_attention_layernorm.weight".format(i)],
+            )
+            for i in range(config.num_hidden_layers)
+        ]
+        self._tokens_cap = 0
+        self._attn_ws = None
+        self._attn_ws_len = 0
+        self._head_ws = None
+        self._ensure_buffers(1)
+
+    # ------------------------------------------------------------ buffers
+
+    def _ensure_buffers(self, tokens):
+        if tokens <= self._tokens_cap:
+            return
+        dev = self.device
+        bf16 = torch.bfloat16
+        self._q = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
+        self._attn = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
+        self._gate = torch.empty(
+            (tokens, self.config.intermediate_size), dtype=bf16, device=dev)
+        self._inter = torch.empty(
+            (tokens, self.config.intermediate_size), dtype=bf16, device=dev)
+        self._normed = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
+        self._tokens_cap = tokens
+
+    def _ensure_attention_workspace(self, length):
+        if length <= self._attn_ws_len:
+            return
+        target = max(length, 2 * self._attn_ws_len, 4096)
+        size = _hip.attention_workspace_bytes(
+            target, self.n_heads, self.n_kv_heads, self.head_dim)
+        # zero-filled once: the kernel's completion counters start at 0 and
+        # every call leaves them at 0
+        self._attn_ws = torch.zeros(size, dtype=torch.uint8, device=self.device)
+        self._attn_ws_len = target
+
+    def reserve(self, length):
+        """Pre-size the KV cache, RoPE table and workspaces for ``length``
+        positions (avoids growth inside a timed loop)."""
+
+        self.kv_cache.reserve(length, device=self.device)
+        self.rope.reserve(length)
+        self._ensure_attention_workspace(length)
+
+    # --------------------------------------------------------------- API
+
+    def begin(self, input_ids, position_ids=None):
+        if input_ids.ndim != 2 or input_ids.shape[0] != 1:
+            raise ValueError("first runtime supports one unpadded request")
+        past = self.kv_cache.sequence_length()
+        sequence = int(input_ids.shape[1])
+        if past and sequence != 1:
+            raise ValueError("after prefill, only one-token decode calls are supported")
+        if position_ids is None:
+            positions = tuple(range(past, past + sequence))
+            position_ids = torch.arange(past, past + sequence,
+                                        dtype=torch.long).unsqueeze(0)
+        else:
+            positions = tuple(int(p) for p in position_ids.reshape(-1).tolist())
+            if len(positions) != sequence:
+                raise ValueError("position_ids must match input_ids")
+        if positions and min(positions) < 0:
+            raise ValueError("negative position id")
+        # Token t attends to cache positions [0, past + t]; its K/V land at
+        # slot past + t (the reference appends in order, llama31.py:44-50).
+        self.reserve(past + sequence)
+        self.rope.reserve(max(positions) + 1)
+        self._ensure_buffers(sequence)
+        if self.vocab_runtime is None:
+            hidden = torch.empty((1, sequence, self.hidden),
+                                 dtype=torch.bfloat16, device=self.device)
+            ids = input_ids.reshape(-1)
+            if ids.device != self.device or ids.dtype != torch.long:
+                ids = ids.to(device=self.device, dtype=torch.long)
+            _hip.embedding_gather(self.resident["model.embed_tokens.weight"],
+                                  ids, hidden)
+        else:
+            hidden = self.vocab_runtime.embedding(input_ids)
+        return DecodeState(hidden_states=hidden, position_ids=position_ids,
+                           positions=positions)
+
+    def _token_rows(self, state):
+        return state.hidden_states.view(-1, self.hidden)
+
+    def _qkv(self, layer, wq, wk, wv, state):
+        x = self._token_rows(state)
+        k_base = self.kv_cache.layer_base(layer, 0)
+        v_base = self.kv_cache.layer_base(layer, 1)
+        stride = self.kv_cache.head_stride
+        norm = self._norms[layer][0]
+        for t, pos in enumerate(self._slots(state)):
+            cos, sin = self.rope.row(state.positions[t])
+            _hip.qkv_rope(
+                wq, wk, wv, x[t], norm, self.eps, cos, sin,
+                self._q[t] if wq is not None else None,
+                k_base[pos * self.head_dim :] if wk is not None else None,
+                v_base[pos * self.head_dim :] if wv is not None else None,
+                stride,
+            )
+
+    def _slots(self, state):
+        """Cache slots of the state's tokens (past .. past + S - 1)."""
+
+        first = self._first_slot
+        return range(first, first + len(state.positions))
+
+    def _attention_o(self, layer, wo, state):
+        x = self._token_rows(state)
+        k_base = self.kv_cache.layer_base(layer, 0)
+        v_base = self.kv_cache.layer_base(layer, 1)
+        stride = self.kv_cache.head_stride
+        for t, slot in enumerate(self._slots(state)):
+            _hip.decode_attention(
+                self._q[t], k_base, v_base, stride, slot + 1, self._attn[t],
+                self._attn_ws, self.scale, self.n_heads, self.n_kv_heads,
+                self.head_dim,
+            )
+            _hip.gemv_residual(wo, self._attn[t], x[t], x[t])
+        self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
+
+    def _gate_up(self, layer, wg, wu, state):
+        x = self._token_rows(state)
+        norm = self._norms[layer][1]
+        for t in range(len(state.positions)):
+            _hip.gate_up_swiglu(wg, wu, x[t], norm, self.eps, self._inter[t])
+
+    def _gate(self, layer, wg, state):
+        x = self._token_rows(state)
+        norm = self._norms[layer][1]
+        for t in range(len(state.positions)):
+            _hip.gate_silu(wg, x[t], norm, self.eps, self._gate[t])
+
+    def _up(self, layer, wu, state):
+        x = self._token_rows(state)
+        norm = self._norms[layer][1]
+        for t in range(len(state.positions)):
+            _hip.up_mul(wu, x[t], norm, self.eps, self._gate[t], self._inter[t])
+
+    def _down(self, layer, wd, state):
+        x = self._token_rows(state)
+        for t in range(len(state.positions)):
+            _hip.gemv_residual(wd, self._inter[t], x[t], x[t])
+
+    def __call__(self, unit, weights, state):
+        layer = unit.layer_index
+        op = unit.operation
+
+        def w(name):
+            return weights[projection_key(layer, name)]
+
+        if layer == 0 and op in ("qkv", "q_proj", "layer"):
+            # slot of the first token of this call, fixed for all layers
+            self._first_slot = self.kv_cache.sequence_length()
+        if op == "layer":
+            self._qkv(layer, w("q_proj"), w("k_proj"), w("v_proj"), state)
+            self._attention_o(layer, w("o_proj"), state)
+            self._gate_up(layer, w("gate_proj"), w("up_proj"), state)
+            self._down(layer, w("down_proj"), state)
+        elif op == "qkv":
+            self._qkv(layer, w("q_proj"), w("k_proj"), w("v_proj"), state)
+        elif op == "q_proj":
+            self._qkv(layer, w("q_proj"), None, None, state)
+        elif op == "k_proj":
+            self._qkv(layer, None, w("k_proj"), None, state)
+        elif op == "v_proj":
+            self._qkv(layer, None, None, w("v_proj"), state)
+        elif op == "o_proj":
+            self._attention_o(layer, w("o_proj"), state)
+        elif op == "gate_up":
+            self._gate_up(layer, w("gate_proj"), w("up_proj"), state)
+        elif op == "gate_proj":
+            self._gate(layer, w("gate_proj"), state)
+        elif op == "up_proj":
+            self._up(layer, w("up_proj"), state)
+        elif op == "down_proj":
+            self._down(layer, w("down_proj"), state)
+        else:
+            raise ValueError("unknown Llama operation {}".format(op))
+        return state
+
+    def finish(self, state):
+        rows = self._token_rows(state)
+        count = rows.shape[0]
+        final_norm = self.resident["model.norm.weight"]
+        if self.vocab_runtime is not None:
+            last = self._normed[:1]
+            _hip.rmsnorm(rows[count - 1 :], final_norm, last, self.eps)
+            result = self.vocab_runtime.lm_head_topk(
+                last.view(1, 1, self.hidden),
+                top_k=self.top_k,
+                return_full_logits=self.return_full_logits,
+            )
+            state.topk_values = result["values"]
+            state.topk_indices = result["indices"]
+            state.logits = result["logits"]
+            return state
+        normed = self._normed[:count]
+        _hip.rmsnorm(rows, final_norm, normed, self.eps)
+        head = self.resident["lm_head.weight"]
+        vocab = head.shape[0]
+        if self._head_ws is None:
+            size = _hip.lm_head_workspace_bytes(vocab, 64)
+            size = max(size, _hip.lm_head_workspace_bytes(vocab, self.top_k))
+            self._head_ws = torch.zeros(size, dtype=torch.uint8, device=self.device)
+        logits = torch.empty((1, count, vocab), dtype=torch.float32, device=self.device)
+        values = torch.empty((1, 1, self.top_k), dtype=torch.float32, device=self.device)
+        indices = torch.empty((1, 1, self.top_k), dtype=torch.int64, device=self.device)
+        for s in range(count):
+            _hip.lm_head_topk(head, normed[s], self.top_k, 0, True, self._head_ws,
+                              values, indices, logits_out=logits[0, s])
+        state.logits = logits
+        state.topk_values = values
+        state.topk_indices = indices
+        return state

@@ -1,0 +1,196 @@
+/*
+ * cascade_hip.h -- C ABI of libcascade_hip.so, the gfx950 (MI355X) kernels and
+ * copy primitives behind the layer_streaming batch=1 decode path.
+ *
+ * Every entry point:
+ *   - is extern "C", takes raw device / pinned-host pointers, int64 sizes and
+ *     a HIP stream handle passed as void* (torch: Stream.cuda_stream);
+ *   - returns 0 on success, a hipError_t value on a HIP failure, or one of the
+ *     CASCADE_E* codes below for a rejected argument (nothing is launched
+ *     then); cascade_error_string() names any of them;
+ *   - never allocates or frees memory and never synchronises the host, except
+ *     cascade_event_create / cascade_event_destroy / cascade_event_synchronize,
+ *     whose whole purpose is that;
+ *   - is called from one host thread per stream; kernels are enqueued on the
+ *     stream given.
+ *
+ * bf16 buffers are uint16_t arrays; all weight matrices are row-major
+ * [rows, K] with rows contiguous (the layout of the reference's packed
+ * host arena and device slots, layer_streaming/plan.py:219-243,
+ * layer_streaming/runtime.py:127-135).  Matrix, vector and cache pointers
+ * must be 16-byte aligned and K a multiple of 8.
+ *
+ * Reference citations are file:line in lianghan224-cloud/Cascade-LLM.
+ */
+#ifndef CASCADE_HIP_H
+#define CASCADE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CASCADE_ABI_VERSION 1
+
+/* Argument errors (no work enqueued). */
+#define CASCADE_EINVAL 1001     /* null pointer, bad size or count */
+#define CASCADE_EALIGN 1002     /* pointer or K not 16-byte / 8-element aligned */
+#define CASCADE_ESHAPE 1003     /* shape outside what the kernels support */
+#define CASCADE_EWORKSPACE 1004 /* workspace smaller than *_workspace_bytes() */
+
+int cascade_abi_version(void);
+const char *cascade_error_string(int code);
+
+/* ---------------------------------------------------------------- RMSNorm
+ * y = w * bf16(x * rsqrt(mean(x^2) + eps)), fp32 statistics, bf16 output,
+ * rows of length n (rows contiguous).
+ * Replaces _rms_norm, layer_streaming/llama31.py:21-25 (used at :173-179,
+ * :256-263, :325-329).                                                     */
+int cascade_rmsnorm_bf16(const void *x, const void *weight, void *y,
+                         int64_t rows, int64_t n, float eps, void *stream);
+
+/* ------------------------------------------------------------------ GEMV
+ * y[N] = bf16(W[N,K] . x[K]), fp32 accumulation.
+ * Replaces F.linear with one token, layer_streaming/llama31.py:241-245.    */
+int cascade_gemv_bf16(const void *w, const void *x, void *y, int64_t n,
+                      int64_t k, void *stream);
+
+/* y[N] = bf16(residual[N] + bf16(W . x)).  y may alias residual.
+ * Replaces `residual + F.linear(...)` for o_proj and down_proj,
+ * layer_streaming/llama31.py:246-251 and :272-279.                         */
+int cascade_gemv_residual_bf16(const void *w, const void *x,
+                               const void *residual, void *y, int64_t n,
+                               int64_t k, void *stream);
+
+/* Fused input RMSNorm + Q/K/V projections + RoPE + KV-cache write for one
+ * token at one position.
+ *   normalized = rmsnorm(x, norm_weight, eps)  (norm_weight NULL: x as is)
+ *   q = rope(bf16(Wq . normalized))  -> q_out[nq]
+ *   k = rope(bf16(Wk . normalized))  -> k_out[h * kv_head_stride + d]
+ *   v =      bf16(Wv . normalized)   -> v_out[h * kv_head_stride + d]
+ * Head dim is 128; nq, nk, nv are multiples of 128 and any of them may be 0
+ * (matrix granularity sends q_proj, k_proj and v_proj as separate units).
+ * rope_cos / rope_sin point at the 64 bf16 cos / sin values of this position
+ * (the two halves of a head share them).  k_out / v_out point at position
+ * `pos` of KV head 0 of this layer's cache.
+ * Replaces F.linear q/k/v (layer_streaming/llama31.py:241-245), the rotary
+ * embedding + apply_rotary_pos_emb (llama31.py:206-212; transformers
+ * models/llama/modeling_llama.py:113-160) and SimpleKVCache.append
+ * (llama31.py:44-50).                                                       */
+int cascade_qkv_rope_bf16(const void *wq, const void *wk, const void *wv,
+                          int64_t nq, int64_t nk, int64_t nv, int64_t k,
+                          const void *x, const void *norm_weight, float eps,
+                          const void *rope_cos, const void *rope_sin,
+                          void *q_out, void *k_out, void *v_out,
+                          int64_t kv_head_stride, void *stream);
+
+/* Fused post-attention RMSNorm + gate/up projections + SwiGLU:
+ *   y[i] = bf16(bf16(silu(bf16(Wg[i] . n))) * bf16(Wu[i] . n)), i < n_half
+ * norm_weight NULL: x is used as the normalized input.
+ * Replaces llama31.py:252-275 (F.silu(F.linear(gate)), F.linear(up),
+ * gate * up) for matrix_group / layer units, where gate and up are both
+ * present.                                                                  */
+int cascade_gate_up_swiglu_bf16(const void *w_gate, const void *w_up,
+                                int64_t n_half, int64_t k, const void *x,
+                                const void *norm_weight, float eps, void *y,
+                                void *stream);
+
+/* Matrix granularity halves of the same computation (gate_proj and up_proj
+ * arrive as separate units, llama31.py:252-271):
+ *   gate_silu: y[i] = bf16(silu(bf16(Wg[i] . n)))
+ *   up_mul:    y[i] = bf16(gate[i] * bf16(Wu[i] . n))                        */
+int cascade_gate_silu_bf16(const void *w_gate, int64_t n, int64_t k,
+                           const void *x, const void *norm_weight, float eps,
+                           void *y, void *stream);
+int cascade_up_mul_bf16(const void *w_up, int64_t n, int64_t k, const void *x,
+                        const void *norm_weight, float eps, const void *gate,
+                        void *y, void *stream);
+
+/* --------------------------------------------------------- decode attention
+ * GQA attention of one query token over positions [0, L) of one layer's
+ * cache: out[h*D + d] = bf16(softmax(q_h . K_g^T * scale) . V_g), g = h / G,
+ * G = n_q_heads / n_kv_heads, D = head_dim (must be 128, G must be 4).
+ * k_cache / v_cache point at position 0 of KV head 0; KV head g starts at
+ * g * kv_head_stride elements, position p of a head at p * D.
+ * Split over L; the workspace (zero-filled once by the caller, left zeroed
+ * by every call) holds per-split partial softmax state.
+ * Replaces _repeat_kv + F.scaled_dot_product_attention at decode,
+ * layer_streaming/llama31.py:213-234.                                      */
+size_t cascade_decode_attention_workspace_bytes(int64_t max_len,
+                                                int64_t n_q_heads,
+                                                int64_t n_kv_heads,
+                                                int64_t head_dim);
+int cascade_decode_attention_bf16(const void *q, const void *k_cache,
+                                  const void *v_cache, int64_t kv_head_stride,
+                                  int64_t len, int64_t n_q_heads,
+                                  int64_t n_kv_heads, int64_t head_dim,
+                                  float scale, void *out, void *workspace,
+                                  size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------ LM head + top-k
+ * One vocabulary chunk: logits[r] = W[r] . h (fp32, not rounded to bf16) for
+ * rows r < rows, then an exact running top-k over everything seen since the
+ * last call with first_chunk = 1.  Order: value descending, index ascending;
+ * -0.0 == +0.0; NaN ranks highest.  After every call out_values[0..top_k) /
+ * out_indices[0..top_k) hold the running result (global row index =
+ * row_offset + r; entries beyond the rows seen so far are -inf / -1).
+ * logits_out (nullable) receives the chunk's fp32 logits (logits_out[r]).
+ * 1 <= top_k <= 64.  The workspace (zero-filled once by the caller) carries
+ * the running list between calls on the same stream.
+ * Replaces the per-chunk F.linear(...).float() + torch.topk + merge_topk of
+ * VocabStreamingRuntime.lm_head_topk, layer_streaming/vocab.py:239-263 and
+ * merge_topk vocab.py:11-32; with one chunk covering the whole vocabulary it
+ * replaces the resident head, llama31.py:330-339.                          */
+size_t cascade_lm_head_workspace_bytes(int64_t rows, int64_t top_k);
+int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
+                              int64_t row_offset, const void *h, int64_t top_k,
+                              int first_chunk, float *logits_out,
+                              void *workspace, size_t workspace_bytes,
+                              float *out_values, int64_t *out_indices,
+                              void *stream);
+
+/* ----------------------------------------------------------- embedding
+ * out[i, :] = table[ids[i], :] for i < n_ids (ids are int64 on the device).
+ * An id outside [0, vocab) yields a zero row and sets *error_flag to 1
+ * (error_flag is a device int32, nullable).
+ * Replaces F.embedding on the resident table, llama31.py:144-148.           */
+int cascade_embedding_gather_bf16(const void *table, int64_t vocab,
+                                  int64_t hidden, const int64_t *ids,
+                                  int64_t n_ids, void *out, int32_t *error_flag,
+                                  void *stream);
+
+/* ------------------------------------------------------- copy pipeline
+ * Thin wrappers so the two-slot pipeline runs on hipMemcpyAsync + hipEvent:
+ * replaces slot.copy_(source, non_blocking=True) and the ready/free events
+ * of DoubleBufferRuntime.run, layer_streaming/runtime.py:155-160,194-230,
+ * and the LM-head chunk copies, layer_streaming/vocab.py:216-239.
+ * Events are opaque handles (hipEvent_t) stored in a uint64.               */
+int cascade_memcpy_h2d_async(void *dst, const void *src, size_t bytes,
+                             void *stream);
+int cascade_memcpy_d2d_async(void *dst, const void *src, size_t bytes,
+                             void *stream);
+int cascade_event_create(uint64_t *event, int enable_timing);
+int cascade_event_destroy(uint64_t event);
+int cascade_event_record(uint64_t event, void *stream);
+int cascade_stream_wait_event(void *stream, uint64_t event);
+int cascade_event_synchronize(uint64_t event);
+/* 0 = complete, 1 = not yet complete, else an error code. */
+int cascade_event_query(uint64_t event);
+int cascade_event_elapsed_ms(uint64_t start, uint64_t end, float *ms);
+
+/* ----------------------------------------------------------- measurement
+ * Streaming-read kernel: sums `bytes` of device memory (16-byte loads) into
+ * *sink; used to measure achievable HBM read bandwidth (no reference
+ * counterpart; the reference measures only H2D, h2d_driver_bench.c).
+ * Plain device copy of `bytes`: the calibration kernel for HBM traffic
+ * counters.                                                                */
+int cascade_hbm_read(const void *src, size_t bytes, float *sink, void *stream);
+int cascade_device_copy(void *dst, const void *src, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CASCADE_HIP_H */

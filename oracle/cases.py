@@ -1,0 +1,195 @@
+"""Seeded inputs and oracle expectations for the BASELINE configurations.
+
+TEST INFRASTRUCTURE (see oracle/llama_oracle.py).  Inputs are drawn in fp32
+from CPU torch.Generators and rounded to bf16, so the oracle and the GPU see
+identical bytes:
+  weights ~ N(0, 0.02), norm weights 1 + N(0, 0.1), hidden and KV ~ N(0, 1).
+"""
+
+import math
+
+import torch
+
+from . import llama_oracle as ref
+
+BF16 = torch.bfloat16
+
+# Tolerance of BASELINE.json north_star: |a - b| <= atol + rtol * |b|.
+ATOL = 2e-2
+RTOL = 1e-2
+
+
+def normal_bf16(shape, seed, std=1.0, mean=0.0):
+    gen = torch.Generator().manual_seed(int(seed))
+    return (torch.randn(shape, generator=gen) * std + mean).to(BF16)
+
+
+def compare(actual, expected, atol=ATOL, rtol=RTOL):
+    """Tolerance report of actual vs expected (both moved to CPU fp32)."""
+
+    a = actual.detach().float().cpu().reshape(-1)
+    b = expected.detach().float().cpu().reshape(-1)
+    diff = (a - b).abs()
+    bound = atol + rtol * b.abs()
+    return {
+        "ok": bool((diff <= bound).all()) and a.numel() == b.numel(),
+        "max_abs": float(diff.max()) if diff.numel() else 0.0,
+        "worst_ratio": float((diff / bound).max()) if diff.numel() else 0.0,
+        "exact_fraction": float((diff == 0).float().mean()) if diff.numel() else 1.0,
+    }
+
+
+def layer_case(seed, past, hidden=4096, intermediate=14336, n_heads=32,
+               n_kv_heads=8, head_dim=128):
+    """One decoder layer (BASELINE config 2 at past = 2048)."""
+
+    s = int(seed) * 100
+    kv = n_kv_heads * head_dim
+    return {
+        "past": int(past),
+        "x": normal_bf16((hidden,), s + 1),
+        "q": normal_bf16((hidden, hidden), s + 2, 0.02),
+        "k": normal_bf16((kv, hidden), s + 3, 0.02),
+        "v": normal_bf16((kv, hidden), s + 4, 0.02),
+        "o": normal_bf16((hidden, hidden), s + 5, 0.02),
+        "gate": normal_bf16((intermediate, hidden), s + 6, 0.02),
+        "up": normal_bf16((intermediate, hidden), s + 7, 0.02),
+        "down": normal_bf16((hidden, intermediate), s + 8, 0.02),
+        "ln1": normal_bf16((hidden,), s + 9, 0.1, 1.0),
+        "ln2": normal_bf16((hidden,), s + 10, 0.1, 1.0),
+        "k_cache": normal_bf16((n_kv_heads, past, head_dim), s + 11),
+        "v_cache": normal_bf16((n_kv_heads, past, head_dim), s + 12),
+        "n_heads": n_heads,
+        "n_kv_heads": n_kv_heads,
+        "head_dim": head_dim,
+        "eps": 1e-5,
+    }
+
+
+def layer_expected(case):
+    """Oracle intermediates of one decode step at position ``past``."""
+
+    n_heads, n_kv, dim = case["n_heads"], case["n_kv_heads"], case["head_dim"]
+    past = case["past"]
+    eps = case["eps"]
+    x = case["x"].reshape(1, -1)
+    inv_freq = ref.llama3_inv_freq(dim)
+    cos, sin = ref.rope_cos_sin(inv_freq, [past])
+    normalized = ref.rms_norm(x, case["ln1"], eps)
+    q = ref.linear(normalized, case["q"]).view(1, n_heads, dim).transpose(0, 1)
+    k = ref.linear(normalized, case["k"]).view(1, n_kv, dim).transpose(0, 1)
+    v = ref.linear(normalized, case["v"]).view(1, n_kv, dim).transpose(0, 1)
+    q = ref.apply_rope(q, cos, sin)
+    k = ref.apply_rope(k, cos, sin)
+    keys = torch.cat((case["k_cache"], k), dim=1)
+    values = torch.cat((case["v_cache"], v), dim=1)
+    attn = ref.attention(q, keys, values, past)
+    h1 = x + ref.linear(attn, case["o"])
+    n2 = ref.rms_norm(h1, case["ln2"], eps)
+    inter = torch.nn.functional.silu(ref.linear(n2, case["gate"])) * ref.linear(
+        n2, case["up"])
+    out = h1 + ref.linear(inter, case["down"])
+    return {
+        "q": q.transpose(0, 1).reshape(-1),
+        "k_new": k[:, 0],
+        "v_new": v[:, 0],
+        "attn": attn.reshape(-1),
+        "h_attn": h1.reshape(-1),
+        "inter": inter.reshape(-1),
+        "out": out.reshape(-1),
+        "cos": cos[0, : dim // 2],
+        "sin": sin[0, : dim // 2],
+    }
+
+
+def layer_expected_composed(case):
+    """Same step through oracle.decoder_layer (checks the composition)."""
+
+    dim = case["head_dim"]
+    cache = {"k": case["k_cache"], "v": case["v_cache"]}
+    if case["past"] == 0:
+        cache = {}
+    cos, sin = ref.rope_cos_sin(ref.llama3_inv_freq(dim), [case["past"]])
+    w = {name: case[name] for name in
+         ("q", "k", "v", "o", "gate", "up", "down", "ln1", "ln2")}
+    return ref.decoder_layer(case["x"].reshape(1, -1), w, cache, case["past"],
+                             cos, sin, case["eps"], case["n_heads"],
+                             case["n_kv_heads"]).reshape(-1)
+
+
+def lm_head_case(seed, rows, hidden=4096):
+    """LM head (BASELINE config 1 when rows = 128256)."""
+
+    s = int(seed) * 100
+    return {
+        "h": normal_bf16((hidden,), s + 1),
+        "w": normal_bf16((rows, hidden), s + 2, 0.02),
+    }
+
+
+def lm_head_expected(case, chunk_rows, top_k=10):
+    values, indices, logits = ref.streamed_lm_head(case["h"], case["w"],
+                                                   chunk_rows, top_k)
+    return {"values": values, "indices": indices, "logits": logits}
+
+
+def topk_contract(gpu_values, gpu_indices, gpu_logits, oracle_logits, top_k):
+    """Top-k checks of the north star on one step.
+
+    * ids / order bit-exact against a stable descending sort of the GPU's
+      own logits (== torch.topk when there is no tie);
+    * ids equal to the oracle's wherever the gaps between consecutive
+      oracle values exceed the logit tolerance.
+    """
+
+    logits = gpu_logits.float().cpu()
+    values = gpu_values.float().cpu().reshape(-1)
+    indices = gpu_indices.cpu().reshape(-1)
+    sv, si = ref.topk(logits, top_k)
+    own = bool(torch.equal(indices, si)) and bool(torch.equal(values, sv))
+    tv, ti = torch.topk(logits, top_k)
+    tied = bool((sv[1:] == sv[:-1]).any()) or (
+        top_k < logits.numel() and bool((logits == sv[-1]).sum() > 1)
+    )
+    torch_match = bool(torch.equal(ti, indices)) if not tied else None
+    ov, oi = ref.topk(oracle_logits.float().cpu(), top_k)
+    margin = ATOL + RTOL * ov.abs()
+    distinct = torch.ones(top_k, dtype=torch.bool)
+    gaps = ov[:-1] - ov[1:]
+    close = gaps <= (margin[:-1] + margin[1:])
+    distinct[:-1] &= ~close
+    distinct[1:] &= ~close
+    if top_k < logits.numel():
+        below = ref.topk(oracle_logits.float().cpu(), top_k + 1)[0][-1]
+        if ov[-1] - below <= margin[-1] * 2:
+            distinct[-1] = False
+    oracle_match = bool(torch.equal(indices[distinct], oi[distinct]))
+    return {
+        "self_exact": own,
+        "torch_topk_match": torch_match,
+        "tie_in_topk": tied,
+        "oracle_match_where_separated": oracle_match,
+        "separated_positions": int(distinct.sum()),
+        "ok": own and oracle_match and torch_match is not False,
+    }
+
+
+def greedy_comparable(oracle_logits, atol=ATOL, rtol=RTOL):
+    """True when the oracle's top-1 margin exceeds the tolerance, i.e. a
+    greedy token must then agree."""
+
+    top2 = torch.topk(oracle_logits.float(), 2).values
+    return bool(top2[0] - top2[1] > 2 * (atol + rtol * top2[0].abs()))
+
+
+def softmax_attention_reference(q, k, v):
+    """Attention by the library routine (F.scaled_dot_product_attention in
+    fp32, GQA by repeat_interleave) -- pins oracle.attention at decode."""
+
+    groups = q.shape[0] // k.shape[0]
+    kf = k.float().repeat_interleave(groups, 0)
+    vf = v.float().repeat_interleave(groups, 0)
+    out = torch.nn.functional.scaled_dot_product_attention(
+        q.float()[None], kf[None], vf[None], scale=1.0 / math.sqrt(q.shape[-1])
+    )[0]
+    return out.transpose(0, 1).reshape(q.shape[1], -1)
