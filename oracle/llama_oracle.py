@@ -264,6 +264,9 @@ class OracleLlama:
         self.n_heads = n_heads
         self.n_kv_heads = n_kv_heads
         self.inv_freq = llama3_inv_freq(head_dim, rope)
+        # cos / sin take the activations' dtype (bf16 for the 8B model; fp32
+        # when the oracle runs a fp32 model against a fp32 golden)
+        self.dtype = tensor("model.embed_tokens.weight").dtype
         self.caches = [dict() for _ in range(self.num_layers)]
         self.length = 0
 
@@ -274,7 +277,7 @@ class OracleLlama:
         ids = torch.as_tensor(ids, dtype=torch.long).reshape(-1)
         past = self.length
         positions = list(range(past, past + ids.numel()))
-        cos, sin = rope_cos_sin(self.inv_freq, positions)
+        cos, sin = rope_cos_sin(self.inv_freq, positions, self.dtype)
         hidden = self.tensor("model.embed_tokens.weight")[ids]
         for layer in range(self.num_layers):
             hidden = decoder_layer(

@@ -1,0 +1,81 @@
+"""The C ABI boundary, checked on a CPU-only host: the library loads, every
+function include/cascade_hip.h declares is exported and typed by the
+binding, and argument checks reject bad calls before anything is launched
+(no kernel runs here)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from layer_streaming import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "cascade_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cascade_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    assert "cascade_qkv_rope_bf16" in names
+    assert "cascade_lm_head_topk_bf16" in names
+    assert len(names) == len(set(names)) >= 20
+
+
+def test_library_exports_every_declared_function():
+    lib = ctypes.CDLL(_hip.library_path())
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert missing == []
+
+
+def test_binding_types_exactly_the_declared_functions():
+    assert sorted(_hip.exported_symbols()) == declared_functions()
+
+
+def test_abi_version_and_error_strings():
+    lib = _hip.load()
+    assert lib.cascade_abi_version() == _hip.ABI_VERSION
+    for code in (0, 1001, 1002, 1003, 1004):
+        assert lib.cascade_error_string(code)
+
+
+def test_argument_checks_reject_without_launching():
+    lib = _hip.load()
+    # null pointers / zero sizes / misalignment are refused host-side
+    assert lib.cascade_gemv_bf16(None, None, None, 16, 4096, None) == 1001
+    assert lib.cascade_gemv_bf16(16, 32, 48, 16, 4095, None) == 1002
+    assert lib.cascade_rmsnorm_bf16(None, None, None, 1, 4096, 1e-5, None) == 1001
+    assert lib.cascade_qkv_rope_bf16(16, 16, 16, 100, 0, 0, 4096, 16, None,
+                                     1e-5, 16, 16, 16, None, None, 0, None) == 1003
+    assert lib.cascade_decode_attention_bf16(16, 16, 16, 128, 4, 32, 8, 64,
+                                             0.1, 16, 16, 1 << 20, None) == 1003
+    assert lib.cascade_lm_head_topk_bf16(16, 100, 4096, 0, 16, 65, 1, None, 16,
+                                         1 << 20, 16, 16, None) == 1001
+    assert lib.cascade_memcpy_h2d_async(None, None, 0, None) == 1001
+
+
+def test_workspace_sizes():
+    # attention: counters + (m, l, acc[128]) per (kv head, split, q head)
+    small = _hip.attention_workspace_bytes(2048)
+    assert small == 256 + 8 * 32 * 4 * (2 + 128) * 4  # 32 splits of 64
+    big = _hip.attention_workspace_bytes(32769)
+    assert big == 256 + 8 * 129 * 4 * (2 + 128) * 4  # 129 splits of 256
+    assert _hip.lm_head_workspace_bytes(16384, 10) == 256 + 512 + 256 * 10 * 8
+    with pytest.raises(ValueError):
+        _hip.lm_head_workspace_bytes(16384, 65)
+    with pytest.raises(ValueError):
+        _hip.attention_workspace_bytes(100, 32, 8, 64)
+
+
+def test_host_tensors_never_reach_a_kernel():
+    import torch
+
+    w = torch.zeros(16, 4096, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        _hip.gemv(w, w[0], w[0])
