@@ -1,0 +1,328 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the MI355X layer_streaming path (one GPU).
+
+Headline (the JSON ``value``): BASELINE config 4 -- the 32-layer
+Llama-3.1-8B-shaped model with all 16 GB of bf16 weights resident in HBM,
+batch 1, greedy decode at context 32768 (KV cache 4 GiB ~ N(0, 1), synthetic
+N(0, 0.02) weights drawn on the device).  A step is one decode token; the
+timed region covers exactly --steps tokens between two synchronisations,
+inputs already resident in HBM.
+
+Also reported (extra keys, not ``value``):
+  * roofline of the dominant kernel (the fused gate/up SwiGLU GEMV, 224 MiB
+    per launch), timed live with HIP events on its stream;
+  * streamed: BASELINE config 3 -- full_pinned 16 GB host arena,
+    matrix_group units through two 224 MiB slots, streamed vocabulary;
+    decode ms/token and the PCIe-inclusive H2D GB/s (skip: --no-streamed);
+  * cpu_baseline: the CPU oracle on this host's cores on a bounded sample
+    (skip: --no-cpu-baseline).
+
+Run: python bench.py [--steps K] [--warmup W] [--context L]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "cascade-llm_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, vendor peak
+PCIE_PEAK_GBPS = 63.0   # PCIe Gen5 x16 per direction, vendor figure
+HIDDEN, INTER, VOCAB, LAYERS = 4096, 14336, 128256, 32
+KV_BYTES_PER_POS_LAYER = 2 * 8 * 128 * 2
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=32)
+    p.add_argument("--warmup", type=int, default=4)
+    p.add_argument("--context", type=int, default=32768)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-streamed", action="store_true")
+    p.add_argument("--streamed-steps", type=int, default=7)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-sample-seconds", type=float, default=15.0)
+    return p.parse_args()
+
+
+def token_bytes(context):
+    """Algorithmic HBM bytes of one decode token at a given context."""
+
+    weights = LAYERS * 436207616 + VOCAB * HIDDEN * 2
+    norms = (2 * LAYERS + 1) * HIDDEN * 2
+    kv_read = LAYERS * context * KV_BYTES_PER_POS_LAYER
+    kv_write = LAYERS * KV_BYTES_PER_POS_LAYER
+    embedding_row = HIDDEN * 2
+    return weights + norms + kv_read + kv_write + embedding_row
+
+
+def gate_up_bytes():
+    # W (gate | up) + input vector + norm weight + output (bf16)
+    return 2 * INTER * HIDDEN * 2 + HIDDEN * 2 + HIDDEN * 2 + INTER * 2
+
+
+def resident_decode(args):
+    import torch
+    from layer_streaming import (
+        Llama31Config,
+        Llama31DecodeExecutor,
+        ResidentDeviceArena,
+        ResidentTransformerRuntime,
+        build_llama31_8b_plan,
+    )
+
+    dev = torch.device("cuda:0")
+    plan = build_llama31_8b_plan("matrix_group", stream_vocab=False)
+    log("config 4: drawing 16 GB of synthetic weights in HBM")
+    resident = ResidentDeviceArena(plan, None, dev, fill=False).fill_random(args.seed)
+    runtime = ResidentTransformerRuntime(plan, None, resident, dev,
+                                         synchronize=False).fill_random(args.seed)
+    executor = Llama31DecodeExecutor(Llama31Config(), resident, top_k=10)
+    total = args.context + args.warmup + args.steps + 1
+    executor.reserve(total)
+    cache = executor.kv_cache
+    log("config 4: KV cache {} positions x 32 layers ~ N(0,1)".format(args.context))
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+    for layer in range(LAYERS):
+        cache.buffer[layer, :, :, : args.context].normal_(generator=gen)
+        cache.set_length(layer, args.context)
+    torch.cuda.synchronize(dev)
+
+    token = torch.tensor([[int(args.seed * 7919 % VOCAB)]], device=dev)
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            state = executor.finish(runtime.run(executor, executor.begin(token)))
+            token = state.topk_indices.reshape(1, -1)[:, :1]
+        torch.cuda.synchronize(dev)
+        executor.instrument("gate_up", args.steps * LAYERS)
+        log("config 4: timing {} decode steps".format(args.steps))
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            state = executor.finish(runtime.run(executor, executor.begin(token)))
+            token = state.topk_indices.reshape(1, -1)[:, :1]
+        torch.cuda.synchronize(dev)
+        elapsed = time.perf_counter() - start
+    gate_up_ms = executor.kernel_times_ms("gate_up")
+    ms_per_step = elapsed * 1000.0 / args.steps
+    mean_context = args.context + args.warmup + (args.steps - 1) / 2.0
+    result = {
+        "ms_per_step": ms_per_step,
+        "tokens": args.steps,
+        "gate_up_launches": len(gate_up_ms),
+        "gate_up_avg_us": 1000.0 * statistics.mean(gate_up_ms),
+        "gate_up_median_us": 1000.0 * statistics.median(gate_up_ms),
+        "token_hbm_bytes": token_bytes(int(mean_context)),
+        "last_token": int(token.reshape(-1)[0]),
+    }
+    del executor, runtime, resident, cache
+    torch.cuda.empty_cache()
+    return result
+
+
+def streamed_decode(args):
+    import torch
+    from layer_streaming import (
+        DoubleBufferRuntime,
+        Llama31Config,
+        Llama31DecodeExecutor,
+        ResidentDeviceArena,
+        VocabStreamingRuntime,
+        build_llama31_8b_plan,
+        create_weight_store,
+    )
+
+    dev = torch.device("cuda:0")
+    plan = build_llama31_8b_plan("matrix_group", stream_vocab=True)
+    log("config 3: pinning a {:.1f} GB host arena".format(plan.host_arena_bytes / 1e9))
+    t0 = time.perf_counter()
+    store = create_weight_store(plan, "full_pinned")
+    store.fill_random(seed=args.seed, device=dev)
+    setup_s = time.perf_counter() - t0
+    resident = ResidentDeviceArena(plan, store, dev)
+    runtime = DoubleBufferRuntime(plan, store, resident, dev, profile=True)
+    vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
+    executor = Llama31DecodeExecutor(Llama31Config(), resident, vocab_runtime=vocab,
+                                     top_k=10)
+    prompt = torch.tensor([[128000, 791, 7438, 315, 2324, 374]], device=dev)
+    walls, h2d, lm = [], [], []
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        state = executor.finish(runtime.run(executor, executor.begin(prompt)))
+        prefill_ms = (time.perf_counter() - t0) * 1000.0
+        token = state.topk_indices[..., 0]
+        for step in range(1 + args.streamed_steps):
+            t0 = time.perf_counter()
+            state = executor.begin(token)
+            state = runtime.run(executor, state)
+            state = executor.finish(state)
+            token = state.topk_indices[..., 0]
+            torch.cuda.synchronize(dev)
+            wall = (time.perf_counter() - t0) * 1000.0
+            if step == 0:
+                continue  # warm-up decode, as the reference's protocol
+            walls.append(wall)
+            h2d.append(runtime.last_profile)
+            lm.append(vocab.last_profile)
+            log("config 3: decode {} {:.1f} ms".format(step, wall))
+    bytes_token = plan.stream_bytes_per_token + VOCAB * HIDDEN * 2 + HIDDEN * 2
+    result = {
+        "ms_per_token_median": statistics.median(walls),
+        "ms_per_token_p10": sorted(walls)[max(0, int(0.1 * (len(walls) - 1)))],
+        "ms_per_token_p90": sorted(walls)[int(0.9 * (len(walls) - 1))],
+        "prefill_6_tokens_ms": prefill_ms,
+        "h2d_bytes_per_token": bytes_token,
+        "pcie_inclusive_gbps": bytes_token / 1e9 / (statistics.median(walls) / 1e3),
+        "transformer_h2d_gbps_median": statistics.median(
+            p["h2d_effective_gbps"] for p in h2d),
+        "transformer_compute_event_sum_ms": statistics.median(
+            p["compute_event_sum_ms"] for p in h2d),
+        "lm_head_h2d_gbps_median": statistics.median(
+            p["h2d_effective_gbps"] for p in lm),
+        "lm_head_compute_event_sum_ms": statistics.median(
+            p["compute_event_sum_ms"] for p in lm),
+        "host_setup_s": setup_s,
+    }
+    store.close()
+    del executor, vocab, runtime, resident, store
+    torch.cuda.empty_cache()
+    return result
+
+
+def cpu_baseline(args):
+    """The CPU oracle on this host: one decode token at context 32768 is
+    timed as (32 x one decoder layer) + the full LM head, on a bounded
+    sample of repeated layer steps."""
+
+    import torch
+    from oracle import llama_oracle as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(5)
+
+    def draw(shape, std=0.02):
+        return (torch.randn(shape, generator=gen) * std).to(torch.bfloat16)
+
+    w = {"q": draw((4096, 4096)), "k": draw((1024, 4096)), "v": draw((1024, 4096)),
+         "o": draw((4096, 4096)), "gate": draw((INTER, 4096)),
+         "up": draw((INTER, 4096)), "down": draw((4096, INTER)),
+         "ln1": torch.ones(4096, dtype=torch.bfloat16),
+         "ln2": torch.ones(4096, dtype=torch.bfloat16)}
+    ctx = args.context
+    kv = {"k": draw((8, ctx, 128), 1.0), "v": draw((8, ctx, 128), 1.0)}
+    head = draw((VOCAB, 4096))
+    inv = ref.llama3_inv_freq(128)
+    cos, sin = ref.rope_cos_sin(inv, [ctx])
+    h = draw((1, 4096), 1.0)
+    layer_times = []
+    deadline = time.perf_counter() + args.cpu_sample_seconds * 0.8
+    while time.perf_counter() < deadline or len(layer_times) < 2:
+        cache = dict(kv)
+        t0 = time.perf_counter()
+        ref.decoder_layer(h, w, cache, ctx, cos, sin, 1e-5)
+        layer_times.append(time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    logits = ref.lm_head_logits(h[0], head)
+    ref.topk(logits, 10)
+    head_s = time.perf_counter() - t0
+    token_ms = (LAYERS * statistics.median(layer_times) + head_s) * 1000.0
+    return {
+        "value": token_ms,
+        "unit": "ms/token",
+        "cores": cores,
+        "kind": "port",
+        "sample": "CPU oracle (torch bf16 ops, fp32 softmax) on {} cores: {} "
+                  "repeats of one full-width decoder layer at context {} "
+                  "(median {:.1f} ms) x 32 layers + one 128256-row LM head "
+                  "with top-10 ({:.1f} ms)".format(
+                      cores, len(layer_times), ctx,
+                      1000 * statistics.median(layer_times), 1000 * head_s),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(--gpus {} requested); run with --gpus 1".format(args.gpus),
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from layer_streaming import _hip
+
+    _hip.load()
+    resident = resident_decode(args)
+    ms = resident["ms_per_step"]
+    gu_us = resident["gate_up_avg_us"]
+    achieved = gate_up_bytes() / (gu_us * 1e-6) / 1e9
+    line = {
+        "metric": "decode ms/token, 8B-shape bf16 b=1; achieved HBM & H2D GB/s vs peak",
+        "value": round(ms, 4),
+        "unit": "ms/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights drawn in HBM; KV ~ N(0,1))",
+        "config": {
+            "workload": "BASELINE config 4: 32-layer Llama-3.1-8B-shaped model, "
+                        "all weights HBM-resident, batch 1 greedy decode at "
+                        "context {}".format(args.context),
+            "context": args.context,
+            "batch": 1,
+            "layers": LAYERS,
+            "vocab": VOCAB,
+            "parallelism": "single GPU",
+        },
+        "tokens_per_s": round(1000.0 / ms, 3),
+        "token_hbm_gbps": round(resident["token_hbm_bytes"] / 1e9 / (ms / 1e3), 2),
+        "token_hbm_frac_of_peak": round(
+            resident["token_hbm_bytes"] / 1e9 / (ms / 1e3) / HBM_PEAK_GBPS, 4),
+        "roofline": {
+            "kernel": "gate_up_swiglu GEMV (gemv_kernel<8,2,4,3>), 2x[14336,4096] bf16",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "bytes_per_launch": gate_up_bytes(),
+            "avg_launch_us": round(gu_us, 3),
+            "launches_timed": resident["gate_up_launches"],
+        },
+    }
+    if not args.no_streamed:
+        s = streamed_decode(args)
+        line["streamed"] = {
+            "workload": "BASELINE config 3: full_pinned, matrix_group, 2 x 224 MiB "
+                        "slots, streamed vocab, 6-token prompt, 1 warm-up + {} "
+                        "decodes".format(args.streamed_steps),
+            **{k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()},
+            "pcie_peak_gbps": PCIE_PEAK_GBPS,
+        }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

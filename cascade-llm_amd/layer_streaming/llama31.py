@@ -238,6 +238,11 @@ class Llama31DecodeExecutor:
             )
             for i in range(config.num_hidden_layers)
         ]
+        self._instrumented = {}
+        self._instrument_next = {}
+        # Debug hook: a list receives (layer, hidden copy) after the
+        # embedding (layer -1) and after every decoder layer.
+        self.capture = None
         self._tokens_cap = 0
         self._attn_ws = None
         self._attn_ws_len = 0
@@ -313,6 +318,8 @@ class Llama31DecodeExecutor:
                                   ids, hidden)
         else:
             hidden = self.vocab_runtime.embedding(input_ids)
+        if self.capture is not None:
+            self.capture.append((-1, hidden.detach().clone()))
         return DecodeState(hidden_states=hidden, position_ids=position_ids,
                            positions=positions)
 
@@ -355,11 +362,43 @@ class Llama31DecodeExecutor:
             _hip.gemv_residual(wo, self._attn[t], x[t], x[t])
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
 
+    def instrument(self, name, launches):
+        """Bracket the next ``launches`` launches of kernel group ``name``
+        ("gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head")
+        with timing events on the launching stream; read them back with
+        :meth:`kernel_times_ms` after a synchronize."""
+
+        self._instrumented[name] = [
+            (_hip.HipEvent(enable_timing=True), _hip.HipEvent(enable_timing=True))
+            for _ in range(int(launches))
+        ]
+        self._instrument_next[name] = 0
+
+    def kernel_times_ms(self, name):
+        pairs = self._instrumented.get(name, [])
+        used = self._instrument_next.get(name, 0)
+        return [a.elapsed_time(b) for a, b in pairs[:used]]
+
+    def _events(self, name):
+        pairs = self._instrumented.get(name)
+        if not pairs:
+            return None
+        index = self._instrument_next[name]
+        if index >= len(pairs):
+            return None
+        self._instrument_next[name] = index + 1
+        return pairs[index]
+
     def _gate_up(self, layer, wg, wu, state):
         x = self._token_rows(state)
         norm = self._norms[layer][1]
         for t in range(len(state.positions)):
+            ev = self._events("gate_up")
+            if ev:
+                ev[0].record()
             _hip.gate_up_swiglu(wg, wu, x[t], norm, self.eps, self._inter[t])
+            if ev:
+                ev[1].record()
 
     def _gate(self, layer, wg, state):
         x = self._token_rows(state)
@@ -377,6 +416,8 @@ class Llama31DecodeExecutor:
         x = self._token_rows(state)
         for t in range(len(state.positions)):
             _hip.gemv_residual(wd, self._inter[t], x[t], x[t])
+        if self.capture is not None:
+            self.capture.append((layer, state.hidden_states.detach().clone()))
 
     def __call__(self, unit, weights, state):
         layer = unit.layer_index

@@ -103,6 +103,30 @@ class ResidentDeviceArena:
     def nbytes(self):
         return self.plan.resident_bytes
 
+    def fill_random(self, seed=0, std=0.02, norm="ones"):
+        """Synthetic resident tensors drawn on the device: matrices
+        N(0, std) seeded base*1000 + plan index, norm weights 1 (or
+        1 + N(0, 0.1) with norm="random")."""
+
+        with torch.inference_mode():
+            for placement in self.plan.resident:
+                key = placement.tensor.key
+                view = self.views[key]
+                if view.dim() == 1 and norm == "ones":
+                    view.fill_(1.0)
+                    continue
+                gen = torch.Generator(device=self.device)
+                gen.manual_seed(int(seed) * 1000 + self.plan.tensor_index(key))
+                flat = view.reshape(-1)
+                scale, shift = (0.1, 1.0) if view.dim() == 1 else (std, 0.0)
+                step = 1 << 28
+                for start in range(0, flat.numel(), step):
+                    piece = flat[start : start + step]
+                    piece.copy_(torch.randn(piece.numel(), generator=gen,
+                                            device=self.device) * scale + shift)
+        torch.cuda.synchronize(self.device)
+        return self
+
     def __getitem__(self, key):
         return self.views[key]
 
