@@ -168,6 +168,29 @@ def call(name, *args):
     _check(name, getattr(load(), name)(*args))
 
 
+def check(name, code):
+    """Raise HipCallError when a raw entry-point call returned non-zero."""
+
+    if code != 0:
+        _check(name, code)
+
+
+def bf16_weight(tensor, name, rows=None, k=None):
+    """Validate a weight view once (device, dtype, layout, shape) and return
+    its (rows, K); the executor then launches on raw pointers."""
+
+    _bf16(tensor, name)
+    if tensor.dim() != 2:
+        raise ValueError("{} must be 2-D [rows, K]".format(name))
+    n, kk = tensor.shape
+    if (rows is not None and n != rows) or (k is not None and kk != k):
+        raise ValueError("{} has shape {}, expected [{}, {}]".format(
+            name, tuple(tensor.shape), rows, k))
+    if tensor.data_ptr() % 16 or kk % 8:
+        raise ValueError("{} is not 16-byte aligned".format(name))
+    return n, kk
+
+
 def stream_handle(stream=None, device=None):
     """Raw hipStream_t (as int) of a torch stream; default: current stream."""
 

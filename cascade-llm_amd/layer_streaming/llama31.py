@@ -29,7 +29,6 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _hip
-from .plan import projection_key
 from .rope import RopeTable, rope_parameters
 
 __all__ = [
@@ -231,6 +230,7 @@ class Llama31DecodeExecutor:
         if self.kv_cache.device is None:
             self.kv_cache.device = self.device
         self.rope = RopeTable(self.head_dim, rope_parameters(config), self.device)
+        self.intermediate = config.intermediate_size
         self._norms = [
             (
                 resident["model.layers.{}.input_layernorm.weight".format(i)],
@@ -238,6 +238,20 @@ class Llama31DecodeExecutor:
             )
             for i in range(config.num_hidden_layers)
         ]
+        for pair in self._norms:
+            for norm in pair:
+                _hip.require_device(norm, "norm weight", torch.bfloat16, self.hidden)
+        self._norm_ptrs = [(a.data_ptr(), b.data_ptr()) for a, b in self._norms]
+        lib = _hip.load()
+        self._k_qkv = lib.cascade_qkv_rope_bf16
+        self._k_attn = lib.cascade_decode_attention_bf16
+        self._k_residual = lib.cascade_gemv_residual_bf16
+        self._k_swiglu = lib.cascade_gate_up_swiglu_bf16
+        self._k_silu = lib.cascade_gate_silu_bf16
+        self._k_mul = lib.cascade_up_mul_bf16
+        self._k_rmsnorm = lib.cascade_rmsnorm_bf16
+        self._k_head = lib.cascade_lm_head_topk_bf16
+        self._unit_cache = {}
         self._instrumented = {}
         self._instrument_next = {}
         # Debug hook: a list receives (layer, hidden copy) after the
@@ -258,11 +272,15 @@ class Llama31DecodeExecutor:
         bf16 = torch.bfloat16
         self._q = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
         self._attn = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
-        self._gate = torch.empty(
+        self._gate_buf = torch.empty(
             (tokens, self.config.intermediate_size), dtype=bf16, device=dev)
         self._inter = torch.empty(
             (tokens, self.config.intermediate_size), dtype=bf16, device=dev)
         self._normed = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
+        self._q_ptr = self._q.data_ptr()
+        self._attn_ptr = self._attn.data_ptr()
+        self._gate_ptr = self._gate_buf.data_ptr()
+        self._inter_ptr = self._inter.data_ptr()
         self._tokens_cap = tokens
 
     def _ensure_attention_workspace(self, length):
@@ -318,6 +336,8 @@ class Llama31DecodeExecutor:
                                   ids, hidden)
         else:
             hidden = self.vocab_runtime.embedding(input_ids)
+        _hip.require_device(hidden, "hidden_states", torch.bfloat16,
+                            sequence * self.hidden)
         if self.capture is not None:
             self.capture.append((-1, hidden.detach().clone()))
         return DecodeState(hidden_states=hidden, position_ids=position_ids,
@@ -326,21 +346,33 @@ class Llama31DecodeExecutor:
     def _token_rows(self, state):
         return state.hidden_states.view(-1, self.hidden)
 
-    def _qkv(self, layer, wq, wk, wv, state):
-        x = self._token_rows(state)
-        k_base = self.kv_cache.layer_base(layer, 0)
-        v_base = self.kv_cache.layer_base(layer, 1)
-        stride = self.kv_cache.head_stride
-        norm = self._norms[layer][0]
-        for t, pos in enumerate(self._slots(state)):
-            cos, sin = self.rope.row(state.positions[t])
-            _hip.qkv_rope(
-                wq, wk, wv, x[t], norm, self.eps, cos, sin,
-                self._q[t] if wq is not None else None,
-                k_base[pos * self.head_dim :] if wk is not None else None,
-                v_base[pos * self.head_dim :] if wv is not None else None,
-                stride,
-            )
+    # ------------------------------------------------------ unit launches
+    # Units launch on raw pointers.  A unit's weight views are validated
+    # (device, dtype, shape, alignment) the first time a (unit, slot) pair is
+    # seen; per-token pointers are byte offsets into buffers that begin()
+    # sized: the hidden rows, the q / attention / intermediate scratch rows,
+    # the KV cache slots and the RoPE rows.
+
+    def _stream(self):
+        """Raw handle of the current stream (kernels launch there)."""
+
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _unit_pointers(self, unit, weights):
+        first = weights[unit.pieces[0].tensor.key]
+        key = (unit.unit_id, first.data_ptr())
+        entry = self._unit_cache.get(key)
+        if entry is None:
+            if len(self._unit_cache) > 4096:
+                self._unit_cache.clear()
+            entry = {}
+            for piece in unit.pieces:
+                spec = piece.tensor
+                view = weights[spec.key]
+                _hip.bf16_weight(view, spec.key, *spec.shape)
+                entry[spec.key.rsplit(".", 2)[-2]] = view.data_ptr()
+            self._unit_cache[key] = entry
+        return entry
 
     def _slots(self, state):
         """Cache slots of the state's tokens (past .. past + S - 1)."""
@@ -348,18 +380,71 @@ class Llama31DecodeExecutor:
         first = self._first_slot
         return range(first, first + len(state.positions))
 
-    def _attention_o(self, layer, wo, state):
-        x = self._token_rows(state)
-        k_base = self.kv_cache.layer_base(layer, 0)
-        v_base = self.kv_cache.layer_base(layer, 1)
+    def _kv_pointer(self, layer, which, slot):
+        cache = self.kv_cache
+        element = ((layer * 2 + which) * cache.num_kv_heads * cache.capacity
+                   + slot) * cache.head_dim
+        return cache.buffer.data_ptr() + 2 * element
+
+    def _qkv(self, layer, ptrs, state, stream):
+        wq = ptrs.get("q_proj", 0)
+        wk = ptrs.get("k_proj", 0)
+        wv = ptrs.get("v_proj", 0)
+        nq = self.hidden if wq else 0
+        nkv = self.n_kv_heads * self.head_dim
+        nk = nkv if wk else 0
+        nv = nkv if wv else 0
+        x = state.hidden_states.data_ptr()
+        row = 2 * self.hidden
+        norm = self._norm_ptrs[layer][0]
         stride = self.kv_cache.head_stride
+        cos = self.rope.cos.data_ptr()
+        sin = self.rope.sin.data_ptr()
+        half = self.head_dim // 2
         for t, slot in enumerate(self._slots(state)):
-            _hip.decode_attention(
-                self._q[t], k_base, v_base, stride, slot + 1, self._attn[t],
-                self._attn_ws, self.scale, self.n_heads, self.n_kv_heads,
-                self.head_dim,
-            )
-            _hip.gemv_residual(wo, self._attn[t], x[t], x[t])
+            pos = state.positions[t]
+            ev = self._events("qkv")
+            if ev:
+                ev[0].record()
+            rc = self._k_qkv(
+                wq, wk, wv, nq, nk, nv, self.hidden, x + t * row, norm, self.eps,
+                cos + 2 * half * pos, sin + 2 * half * pos,
+                self._q_ptr + t * row if wq else 0,
+                self._kv_pointer(layer, 0, slot) if wk else 0,
+                self._kv_pointer(layer, 1, slot) if wv else 0,
+                stride, stream)
+            if ev:
+                ev[1].record()
+            _hip.check("cascade_qkv_rope_bf16", rc)
+
+    def _attention_o(self, layer, ptrs, state, stream):
+        wo = ptrs["o_proj"]
+        x = state.hidden_states.data_ptr()
+        row = 2 * self.hidden
+        k0 = self._kv_pointer(layer, 0, 0)
+        v0 = self._kv_pointer(layer, 1, 0)
+        stride = self.kv_cache.head_stride
+        ws, ws_bytes = self._attn_ws.data_ptr(), self._attn_ws.numel()
+        for t, slot in enumerate(self._slots(state)):
+            ev = self._events("attention")
+            if ev:
+                ev[0].record()
+            rc = self._k_attn(self._q_ptr + t * row, k0, v0, stride, slot + 1,
+                              self.n_heads, self.n_kv_heads, self.head_dim,
+                              self.scale, self._attn_ptr + t * row, ws, ws_bytes,
+                              stream)
+            if ev:
+                ev[1].record()
+            _hip.check("cascade_decode_attention_bf16", rc)
+            ev = self._events("o_proj")
+            if ev:
+                ev[0].record()
+            xt = x + t * row
+            rc = self._k_residual(wo, self._attn_ptr + t * row, xt, xt,
+                                  self.hidden, self.hidden, stream)
+            if ev:
+                ev[1].record()
+            _hip.check("cascade_gemv_residual_bf16", rc)
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
 
     def instrument(self, name, launches):
@@ -389,69 +474,86 @@ class Llama31DecodeExecutor:
         self._instrument_next[name] = index + 1
         return pairs[index]
 
-    def _gate_up(self, layer, wg, wu, state):
-        x = self._token_rows(state)
-        norm = self._norms[layer][1]
+    def _gate_up(self, layer, ptrs, state, stream):
+        x = state.hidden_states.data_ptr()
+        row = 2 * self.hidden
+        inter_row = 2 * self.intermediate
+        norm = self._norm_ptrs[layer][1]
+        wg, wu = ptrs["gate_proj"], ptrs["up_proj"]
         for t in range(len(state.positions)):
             ev = self._events("gate_up")
             if ev:
                 ev[0].record()
-            _hip.gate_up_swiglu(wg, wu, x[t], norm, self.eps, self._inter[t])
+            rc = self._k_swiglu(wg, wu, self.intermediate, self.hidden, x + t * row,
+                                norm, self.eps, self._inter_ptr + t * inter_row,
+                                stream)
             if ev:
                 ev[1].record()
+            _hip.check("cascade_gate_up_swiglu_bf16", rc)
 
-    def _gate(self, layer, wg, state):
-        x = self._token_rows(state)
-        norm = self._norms[layer][1]
+    def _gate(self, layer, ptrs, state, stream):
+        x = state.hidden_states.data_ptr()
+        row, inter_row = 2 * self.hidden, 2 * self.intermediate
+        norm = self._norm_ptrs[layer][1]
         for t in range(len(state.positions)):
-            _hip.gate_silu(wg, x[t], norm, self.eps, self._gate[t])
+            rc = self._k_silu(ptrs["gate_proj"], self.intermediate, self.hidden,
+                              x + t * row, norm, self.eps,
+                              self._gate_ptr + t * inter_row, stream)
+            _hip.check("cascade_gate_silu_bf16", rc)
 
-    def _up(self, layer, wu, state):
-        x = self._token_rows(state)
-        norm = self._norms[layer][1]
+    def _up(self, layer, ptrs, state, stream):
+        x = state.hidden_states.data_ptr()
+        row, inter_row = 2 * self.hidden, 2 * self.intermediate
+        norm = self._norm_ptrs[layer][1]
         for t in range(len(state.positions)):
-            _hip.up_mul(wu, x[t], norm, self.eps, self._gate[t], self._inter[t])
+            rc = self._k_mul(ptrs["up_proj"], self.intermediate, self.hidden,
+                             x + t * row, norm, self.eps,
+                             self._gate_ptr + t * inter_row,
+                             self._inter_ptr + t * inter_row, stream)
+            _hip.check("cascade_up_mul_bf16", rc)
 
-    def _down(self, layer, wd, state):
-        x = self._token_rows(state)
+    def _down(self, layer, ptrs, state, stream):
+        x = state.hidden_states.data_ptr()
+        row, inter_row = 2 * self.hidden, 2 * self.intermediate
+        wd = ptrs["down_proj"]
         for t in range(len(state.positions)):
-            _hip.gemv_residual(wd, self._inter[t], x[t], x[t])
+            ev = self._events("down_proj")
+            if ev:
+                ev[0].record()
+            xt = x + t * row
+            rc = self._k_residual(wd, self._inter_ptr + t * inter_row, xt, xt,
+                                  self.hidden, self.intermediate, stream)
+            if ev:
+                ev[1].record()
+            _hip.check("cascade_gemv_residual_bf16", rc)
         if self.capture is not None:
             self.capture.append((layer, state.hidden_states.detach().clone()))
 
     def __call__(self, unit, weights, state):
         layer = unit.layer_index
         op = unit.operation
-
-        def w(name):
-            return weights[projection_key(layer, name)]
-
+        ptrs = self._unit_pointers(unit, weights)
+        stream = self._stream()
         if layer == 0 and op in ("qkv", "q_proj", "layer"):
             # slot of the first token of this call, fixed for all layers
             self._first_slot = self.kv_cache.sequence_length()
         if op == "layer":
-            self._qkv(layer, w("q_proj"), w("k_proj"), w("v_proj"), state)
-            self._attention_o(layer, w("o_proj"), state)
-            self._gate_up(layer, w("gate_proj"), w("up_proj"), state)
-            self._down(layer, w("down_proj"), state)
-        elif op == "qkv":
-            self._qkv(layer, w("q_proj"), w("k_proj"), w("v_proj"), state)
-        elif op == "q_proj":
-            self._qkv(layer, w("q_proj"), None, None, state)
-        elif op == "k_proj":
-            self._qkv(layer, None, w("k_proj"), None, state)
-        elif op == "v_proj":
-            self._qkv(layer, None, None, w("v_proj"), state)
+            self._qkv(layer, ptrs, state, stream)
+            self._attention_o(layer, ptrs, state, stream)
+            self._gate_up(layer, ptrs, state, stream)
+            self._down(layer, ptrs, state, stream)
+        elif op in ("qkv", "q_proj", "k_proj", "v_proj"):
+            self._qkv(layer, ptrs, state, stream)
         elif op == "o_proj":
-            self._attention_o(layer, w("o_proj"), state)
+            self._attention_o(layer, ptrs, state, stream)
         elif op == "gate_up":
-            self._gate_up(layer, w("gate_proj"), w("up_proj"), state)
+            self._gate_up(layer, ptrs, state, stream)
         elif op == "gate_proj":
-            self._gate(layer, w("gate_proj"), state)
+            self._gate(layer, ptrs, state, stream)
         elif op == "up_proj":
-            self._up(layer, w("up_proj"), state)
+            self._up(layer, ptrs, state, stream)
         elif op == "down_proj":
-            self._down(layer, w("down_proj"), state)
+            self._down(layer, ptrs, state, stream)
         else:
             raise ValueError("unknown Llama operation {}".format(op))
         return state
@@ -459,6 +561,7 @@ class Llama31DecodeExecutor:
     def finish(self, state):
         rows = self._token_rows(state)
         count = rows.shape[0]
+        stream = self._stream()
         final_norm = self.resident["model.norm.weight"]
         if self.vocab_runtime is not None:
             last = self._normed[:1]
@@ -473,19 +576,32 @@ class Llama31DecodeExecutor:
             state.logits = result["logits"]
             return state
         normed = self._normed[:count]
-        _hip.rmsnorm(rows, final_norm, normed, self.eps)
-        head = self.resident["lm_head.weight"]
-        vocab = head.shape[0]
+        _hip.check("cascade_rmsnorm_bf16", self._k_rmsnorm(
+            rows.data_ptr(), final_norm.data_ptr(), normed.data_ptr(), count,
+            self.hidden, self.eps, stream))
         if self._head_ws is None:
-            size = _hip.lm_head_workspace_bytes(vocab, 64)
-            size = max(size, _hip.lm_head_workspace_bytes(vocab, self.top_k))
+            head = self.resident["lm_head.weight"]
+            vocab, _ = _hip.bf16_weight(head, "lm_head.weight", k=self.hidden)
+            size = _hip.lm_head_workspace_bytes(vocab, self.top_k)
+            # zero-filled once; the kernel returns its ticket counter to 0
             self._head_ws = torch.zeros(size, dtype=torch.uint8, device=self.device)
+            self._head = (head.data_ptr(), vocab)
+        head_ptr, vocab = self._head
         logits = torch.empty((1, count, vocab), dtype=torch.float32, device=self.device)
         values = torch.empty((1, 1, self.top_k), dtype=torch.float32, device=self.device)
         indices = torch.empty((1, 1, self.top_k), dtype=torch.int64, device=self.device)
+        ws, ws_bytes = self._head_ws.data_ptr(), self._head_ws.numel()
         for s in range(count):
-            _hip.lm_head_topk(head, normed[s], self.top_k, 0, True, self._head_ws,
-                              values, indices, logits_out=logits[0, s])
+            ev = self._events("lm_head")
+            if ev:
+                ev[0].record()
+            rc = self._k_head(head_ptr, vocab, self.hidden, 0,
+                              normed.data_ptr() + 2 * self.hidden * s, self.top_k,
+                              1, logits.data_ptr() + 4 * vocab * s, ws, ws_bytes,
+                              values.data_ptr(), indices.data_ptr(), stream)
+            if ev:
+                ev[1].record()
+            _hip.check("cascade_lm_head_topk_bf16", rc)
         state.logits = logits
         state.topk_values = values
         state.topk_indices = indices

@@ -147,14 +147,16 @@ def attention(q, k, v, past):
 
 
 def decoder_layer(hidden, w, cache, past, cos, sin, eps, n_heads=32,
-                  n_kv_heads=8):
+                  n_kv_heads=8, linear_fn=None):
     """One decoder layer for S tokens, llama31.py:169-283.
 
     hidden [S, H] bf16; w: dict with q, k, v, o, gate, up, down, ln1, ln2;
     cache: dict with "k" / "v" tensors [Hkv, past, D] (or None), updated in
-    place.  Returns the new hidden [S, H].
+    place.  Returns the new hidden [S, H].  ``linear_fn`` replaces the GEMV
+    restatement (default: ``linear``).
     """
 
+    linear = globals()["linear"] if linear_fn is None else linear_fn
     seq, width = hidden.shape
     dim = width // n_heads
     residual = hidden

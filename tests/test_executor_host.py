@@ -1,0 +1,293 @@
+"""Host logic of the decode executor, on the CPU.
+
+The executor launches kernels with raw pointers and byte offsets (hidden
+rows, q / attention / intermediate scratch rows, KV-cache slots per layer
+and head, RoPE rows).  Here every buffer lives in host memory and the
+kernel entry points are replaced by test doubles that read and write
+through exactly those pointers with the oracle's math.  Both the doubles
+and the oracle model use float64-exact products (rounded to bf16) and a
+float64 softmax, so executor-with-doubles and OracleLlama must agree bit
+for bit: any addressing or orchestration slip (wrong slot, position,
+layer, norm or buffer row; wrong unit dispatch for a granularity) shows up
+as a mismatch.  The GPU kernels themselves are covered by the gpu tests.
+"""
+
+import ctypes
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from layer_streaming import _hip, build_llama31_8b_plan, create_weight_store
+from layer_streaming.llama31 import Llama31Config, Llama31DecodeExecutor, SimpleKVCache
+from layer_streaming.rope import inverse_frequencies, rope_parameters
+from layer_streaming.runtime import _unit_views
+from oracle import llama_oracle as ref
+
+BF16 = torch.bfloat16
+LAYERS = 2
+
+
+def at(ptr, n, dtype=BF16):
+    size = torch.empty((), dtype=dtype).element_size()
+    return torch.frombuffer((ctypes.c_char * (n * size)).from_address(ptr),
+                            dtype=dtype, count=n)
+
+
+_DOUBLE_WEIGHTS = {}
+
+
+def exact_linear(x, w):
+    key = (w.data_ptr(), tuple(w.shape))
+    wd = _DOUBLE_WEIGHTS.get(key)
+    if wd is None:
+        wd = _DOUBLE_WEIGHTS[key] = w.double().t().contiguous()
+    y = x.double().reshape(-1, x.shape[-1]) @ wd
+    return y.reshape(*x.shape[:-1], w.shape[0]).to(BF16)
+
+
+def exact_attention(q, k, v, past):
+    heads, seq, dim = q.shape
+    groups = heads // k.shape[0]
+    kf = k.double().repeat_interleave(groups, 0)
+    vf = v.double().repeat_interleave(groups, 0)
+    scores = (q.double() @ kf.transpose(1, 2)) / math.sqrt(dim)
+    allowed = torch.arange(k.shape[1])[None, :] <= (past + torch.arange(seq))[:, None]
+    scores = scores.masked_fill(~allowed[None], float("-inf"))
+    out = torch.softmax(scores, -1) @ vf
+    return out.transpose(0, 1).reshape(seq, heads * dim).to(q.dtype)
+
+
+class FakeKernels:
+    """Pointer-level doubles of the libcascade_hip entry points."""
+
+    def __init__(self):
+        self.calls = []
+
+    def qkv(self, wq, wk, wv, nq, nk, nv, k, x, norm, eps, cos, sin, q_out,
+            k_out, v_out, stride, stream):
+        self.calls.append("qkv")
+        n = ref.rms_norm(at(x, k).reshape(1, k), at(norm, k), eps)
+        c, s = at(cos, 64), at(sin, 64)
+        c, s = torch.cat((c, c))[None], torch.cat((s, s))[None]
+        for w, rows, rope, write in ((wq, nq, True, "q"), (wk, nk, True, "k"),
+                                     (wv, nv, False, "v")):
+            if not rows:
+                continue
+            y = ref.linear(n, at(w, rows * k).view(rows, k)).view(rows // 128, 1, 128)
+            if rope:
+                y = ref.apply_rope(y, c, s)
+            if write == "q":
+                at(q_out, rows).copy_(y.reshape(-1))
+            else:
+                base = k_out if write == "k" else v_out
+                for h in range(rows // 128):
+                    at(base + 2 * h * stride, 128).copy_(y[h, 0])
+        return 0
+
+    def attention(self, q, k0, v0, stride, length, hq, hkv, dim, scale, out,
+                  ws, ws_bytes, stream):
+        self.calls.append("attention")
+        keys = torch.stack([at(k0 + 2 * h * stride, length * dim).view(length, dim)
+                            for h in range(hkv)])
+        vals = torch.stack([at(v0 + 2 * h * stride, length * dim).view(length, dim)
+                            for h in range(hkv)])
+        qq = at(q, hq * dim).view(hq, 1, dim)
+        at(out, hq * dim).copy_(ref.attention(qq, keys, vals, length - 1).reshape(-1))
+        return 0
+
+    def residual(self, w, x, res, y, n, k, stream):
+        self.calls.append("residual")
+        out = at(res, n).reshape(1, n) + ref.linear(at(x, k).reshape(1, k),
+                                                    at(w, n * k).view(n, k))
+        at(y, n).copy_(out.reshape(-1))
+        return 0
+
+    def _normed(self, x, norm, k, eps):
+        xx = at(x, k).reshape(1, k)
+        return ref.rms_norm(xx, at(norm, k), eps) if norm else xx
+
+    def swiglu(self, wg, wu, n, k, x, norm, eps, y, stream):
+        self.calls.append("swiglu")
+        nn = self._normed(x, norm, k, eps)
+        out = F.silu(ref.linear(nn, at(wg, n * k).view(n, k))) * ref.linear(
+            nn, at(wu, n * k).view(n, k))
+        at(y, n).copy_(out.reshape(-1))
+        return 0
+
+    def silu(self, wg, n, k, x, norm, eps, y, stream):
+        self.calls.append("silu")
+        out = F.silu(ref.linear(self._normed(x, norm, k, eps), at(wg, n * k).view(n, k)))
+        at(y, n).copy_(out.reshape(-1))
+        return 0
+
+    def mul(self, wu, n, k, x, norm, eps, gate, y, stream):
+        self.calls.append("mul")
+        out = at(gate, n).reshape(1, n) * ref.linear(self._normed(x, norm, k, eps),
+                                                     at(wu, n * k).view(n, k))
+        at(y, n).copy_(out.reshape(-1))
+        return 0
+
+    def rmsnorm(self, x, w, y, rows, n, eps, stream):
+        self.calls.append("rmsnorm")
+        at(y, rows * n).copy_(ref.rms_norm(at(x, rows * n).view(rows, n),
+                                           at(w, n), eps).reshape(-1))
+        return 0
+
+    def head(self, w, rows, k, offset, h, top_k, first, logits, ws, ws_bytes,
+             values, indices, stream):
+        self.calls.append("lm_head")
+        lg = ref.lm_head_logits(at(h, k), at(w, rows * k).view(rows, k))
+        at(logits, rows, torch.float32).copy_(lg)
+        v, i = ref.topk(lg, top_k)
+        at(values, top_k, torch.float32).copy_(v)
+        at(indices, top_k, torch.int64).copy_(i + offset)
+        return 0
+
+
+class HostResident:
+    """CPU stand-in for ResidentDeviceArena (views into the host store)."""
+
+    def __init__(self, plan, store):
+        self.plan = plan
+        self.store = store
+        self.device = torch.device("cpu")
+
+    def __getitem__(self, key):
+        return self.store.tensor(key)
+
+
+def lenient_require(tensor, name, dtype=None, min_numel=None, contiguous=True):
+    assert isinstance(tensor, torch.Tensor), name
+    if dtype is not None:
+        assert tensor.dtype == dtype, name
+    if contiguous:
+        assert tensor.is_contiguous(), name
+    if min_numel is not None:
+        assert tensor.numel() >= min_numel, name
+    return tensor
+
+
+@pytest.fixture(scope="module")
+def weights():
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    store = create_weight_store(plan, "pinned_staging",
+                                tensor_factory=lambda n, **kw: torch.empty(
+                                    n, dtype=kw["dtype"]))
+    store.fill_random(seed=11, norm="random")
+    yield store
+    _DOUBLE_WEIGHTS.clear()
+
+
+@pytest.fixture
+def exact_oracle(monkeypatch):
+    monkeypatch.setattr(ref, "linear", exact_linear)
+    monkeypatch.setattr(ref, "attention", exact_attention)
+    monkeypatch.setattr(_hip, "require_device", lenient_require)
+
+
+def make_executor(monkeypatch, plan, store):
+    fakes = FakeKernels()
+
+    def gather(table, ids, out, error_flag=None, stream=None):
+        out.view(-1, table.shape[1]).copy_(table[ids.cpu()])
+        return out
+
+    monkeypatch.setattr(_hip, "embedding_gather", gather)
+    cache = SimpleKVCache(LAYERS, device="cpu")
+    ex = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
+                               HostResident(plan, store), kv_cache=cache, top_k=5)
+    ex._stream = lambda: 0
+    ex._k_qkv, ex._k_attn, ex._k_residual = fakes.qkv, fakes.attention, fakes.residual
+    ex._k_swiglu, ex._k_silu, ex._k_mul = fakes.swiglu, fakes.silu, fakes.mul
+    ex._k_rmsnorm, ex._k_head = fakes.rmsnorm, fakes.head
+    return ex, fakes
+
+
+def run_units(plan, store, executor, state):
+    for unit in plan.units:
+        views = _unit_views(unit, store.unit_source(unit))
+        state = executor(unit, views, state)
+    return state
+
+
+@pytest.mark.parametrize("granularity", ["matrix_group", "matrix", "layer"])
+def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
+                                                        exact_oracle, granularity):
+    plan = build_llama31_8b_plan(granularity, num_layers=LAYERS)
+    # every granularity packs the arena identically, so one store serves all
+    for key in plan.tensors:
+        assert plan.tensor_host_offset(key) == weights.plan.tensor_host_offset(key)
+    store = weights
+    executor, fakes = make_executor(monkeypatch, plan, store)
+    oracle = ref.OracleLlama(store.tensor, LAYERS)
+    prompt = [7, 99, 1234, 5, 128255, 0]
+    expected_logits, ev, ei = oracle.step(prompt, 5)
+    state = run_units(plan, store, executor,
+                      executor.begin(torch.tensor([prompt])))
+    state = executor.finish(state)
+    assert torch.equal(state.logits[0, -1], expected_logits)
+    assert state.topk_indices.reshape(-1).tolist() == ei.tolist()
+    token = int(ei[0])
+    for _ in range(3):
+        expected_logits, ev, ei = oracle.step([token], 5)
+        state = run_units(plan, store, executor,
+                          executor.begin(torch.tensor([[token]])))
+        state = executor.finish(state)
+        assert torch.equal(state.logits[0, -1], expected_logits)
+        assert state.topk_indices.reshape(-1).tolist() == ei.tolist()
+        token = int(ei[0])
+    assert executor.kv_cache.sequence_length() == len(prompt) + 3
+    # the oracle's cache and the executor's cache hold the same K / V
+    for layer in range(LAYERS):
+        k, v = executor.kv_cache.entries[layer]
+        assert torch.equal(k[0], oracle.caches[layer]["k"])
+        assert torch.equal(v[0], oracle.caches[layer]["v"])
+    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5}[granularity]
+    # per layer and token: qkv launch(es), attention, o residual, MLP, down;
+    # finish: one rmsnorm plus one LM-head launch per position
+    layers = LAYERS * per_token * (len(prompt) + 3)
+    assert len(fakes.calls) == layers + (1 + len(prompt)) + 3 * 2
+
+
+def test_rope_table_equals_oracle_cos_sin():
+    params = rope_parameters(Llama31Config())
+    assert torch.equal(inverse_frequencies(128, params), ref.llama3_inv_freq(128))
+    from layer_streaming.rope import cos_sin_rows
+
+    cos, sin = cos_sin_rows(inverse_frequencies(128, params), 0, 40000)
+    positions = [0, 1, 2047, 8192, 32768, 39999]
+    oc, os_ = ref.rope_cos_sin(ref.llama3_inv_freq(128), positions)
+    assert torch.equal(cos[positions], oc[:, :64])
+    assert torch.equal(sin[positions], os_[:, :64])
+    assert torch.equal(oc[:, :64], oc[:, 64:])
+
+
+def test_kv_cache_growth_keeps_entries():
+    cache = SimpleKVCache(2, num_kv_heads=2, head_dim=4, device="cpu")
+    k = torch.randn(1, 2, 300, 4).to(BF16)
+    v = torch.randn(1, 2, 300, 4).to(BF16)
+    cache.append(0, k, v)
+    cache.append(1, k, v)
+    assert cache.capacity == 512 and cache.sequence_length() == 300
+    cache.append(0, k, v)  # grows to 768 slots, copying the first 300
+    assert cache.capacity >= 600
+    assert torch.equal(cache.entries[0][0][0, :, :300], k[0])
+    assert torch.equal(cache.entries[0][0][0, :, 300:], k[0])
+    cache.clear()
+    assert cache.sequence_length() == 0 and cache.entries[0] is None
+
+
+def test_begin_rejects_multi_token_after_prefill(monkeypatch, weights, exact_oracle):
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    executor, _ = make_executor(monkeypatch, plan, weights)
+    with pytest.raises(ValueError):
+        executor.begin(torch.tensor([1, 2]))
+    executor.kv_cache.reserve(8)
+    executor.kv_cache.set_length(0, 3)
+    with pytest.raises(ValueError):
+        executor.begin(torch.tensor([[1, 2]]))
+    with pytest.raises(ValueError):
+        Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS, hidden_size=8),
+                              HostResident(plan, weights))

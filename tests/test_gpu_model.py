@@ -5,13 +5,15 @@ oracle in seconds) and the full 128256-row vocabulary.
 Each configuration runs the reference's token loop (tools/run_llama31.py:
 104-121): a 6-token prompt prefill, then greedy decode.  Per step:
 
-1. Teacher-forced parity under the north-star tolerance
-   |a - b| <= 2e-2 + 1e-2 |b|: the oracle recomputes every decoder layer
-   from the GPU's own input hidden state and KV cache (captured through
-   ``executor.capture``), and must agree with the GPU's layer output and
-   with the K/V the GPU wrote; the oracle's final norm + fp32 LM head on the
-   GPU's final hidden state must agree with the GPU's logits; the embedding
-   rows are bit-exact.
+1. Teacher-forced parity: the oracle recomputes every decoder layer from
+   the GPU's own input hidden state and KV cache (captured through
+   ``executor.capture``).  The GPU's layer output must lie within twice the
+   reference's own summation-order noise floor on those inputs (oracle with
+   F.linear vs oracle with an fp32 sgemm; cases.within_noise_floor) and the
+   K/V it wrote within |a - b| <= 2e-2 + 1e-2 |b| (or that floor); the
+   oracle's final norm + fp32 LM head on the GPU's final hidden state must
+   match the GPU's logits within the north-star tolerance
+   |a - b| <= 2e-2 + 1e-2 |b|; the embedding rows are bit-exact.
 2. Top-k: ids and values bit-exact against a stable sort of the GPU's own
    logits (== torch.topk when there is no tie).
 3. Free-running: greedy tokens equal the oracle's wherever the oracle's
@@ -131,14 +133,19 @@ def teacher_forced(source, executor, captured, ids, past, gpu_logits):
         k_gpu = cache.buffer[layer, 0, :, : past + seq].cpu()
         v_gpu = cache.buffer[layer, 1, :, : past + seq].cpu()
         kv = {"k": k_gpu[:, :past], "v": v_gpu[:, :past]} if past else {}
-        expected = ref.decoder_layer(inp, ref.layer_weights(source.tensor, layer),
-                                     kv, past, cos, sin, EPS)
-        r = cases.compare(out, expected)
+        weights = ref.layer_weights(source.tensor, layer)
+        expected = ref.decoder_layer(inp, weights, kv, past, cos, sin, EPS)
+        alt_kv = {"k": k_gpu[:, :past], "v": v_gpu[:, :past]} if past else {}
+        alternative = ref.decoder_layer(inp, weights, alt_kv, past, cos, sin, EPS,
+                                        linear_fn=cases.sgemm_linear)
+        r = cases.within_noise_floor(out, expected, alternative)
         assert r["ok"], ("layer", layer, r)
-        worst["layer"] = max(worst["layer"], r["worst_ratio"])
+        worst["layer"] = max(worst["layer"], r["ratio_to_floor"])
         for name, gpu in (("k", k_gpu), ("v", v_gpu)):
             r = cases.compare(gpu[:, past:], kv[name][:, past:])
-            assert r["ok"], ("kv", layer, name, r)
+            f = cases.within_noise_floor(gpu[:, past:], kv[name][:, past:],
+                                         alt_kv[name][:, past:])
+            assert r["ok"] or f["ok"], ("kv", layer, name, r, f)
             worst["kv"] = max(worst["kv"], r["worst_ratio"])
     final = hidden[LAYERS - 1].reshape(seq, -1)[-1:].cpu()
     normalized = ref.rms_norm(final, source.tensor("model.norm.weight"), EPS)
