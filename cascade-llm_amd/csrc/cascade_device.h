@@ -71,10 +71,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15).
+template <int CTRL>
+__device__ __forceinline__ float dpp_float(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane of
+// the row receives the sum.  quad_perm [1,0,3,2] and [2,3,0,1] sum each
+// quad, row_half_mirror pairs the two quads of each half row, row_mirror
+// pairs the two halves.
 __device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  v += dpp_float<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_float<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_float<0x141>(v);  // row_half_mirror
+  v += dpp_float<0x140>(v);  // row_mirror
   return v;
 }
 

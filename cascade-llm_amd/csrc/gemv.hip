@@ -28,6 +28,7 @@ enum GemvEpilogue : int {
   kSwiglu = 3,
   kSilu = 4,
   kMul = 5,
+  kLogits = 6,  // fp32 output, no rounding (LM head)
 };
 
 struct GemvArgs {
@@ -41,6 +42,7 @@ struct GemvArgs {
   float eps;
   uint16_t *y;
   const uint16_t *aux;  // residual (kResidual) or gate (kMul)
+  float *yf;            // kLogits output
   const uint16_t *rope_cos;
   const uint16_t *rope_sin;
   uint16_t *k_out;
@@ -52,8 +54,13 @@ struct GemvArgs {
 constexpr int kHeadDim = 128;
 constexpr int kHalfHead = 64;
 
+template <bool NT>
 __device__ __forceinline__ u32x4 load16(const uint16_t *p) {
-  return *reinterpret_cast<const u32x4 *>(p);
+  // NT: streaming weights that are read once (nontemporal hint)
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  else
+    return *reinterpret_cast<const u32x4 *>(p);
 }
 
 // Builds the GEMV input vector in LDS.  With a norm weight it applies
@@ -214,6 +221,10 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
     for (int r = 0; r < R; ++r) {
       if (!ok[r]) continue;
       const int64_t row = tile * R + r;
+      if constexpr (EPI == kLogits) {
+        a.yf[row] = acc[r];
+        continue;
+      }
       const float v = round_bf16(acc[r]);
       float out;
       if constexpr (EPI == kPlain) {
@@ -232,7 +243,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
 
 // KC > 0: K == KC * 512, loads fully unrolled and issued up front.
 // KC == 0: any K that is a multiple of 8 (loop over 16-byte pieces).
-template <int KC, int R, int WAVES, int EPI>
+template <int KC, int R, int WAVES, int EPI, bool NT>
 __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
   extern __shared__ u32x4 xs[];
   const int lane = threadIdx.x & (kWave - 1);
@@ -251,7 +262,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
     for (int r = 0; r < R; ++r) {
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        wv[r][c] = ok[r] ? load16(wrow[r] + (c * kWave + lane) * 8)
+        wv[r][c] = ok[r] ? load16<NT>(wrow[r] + (c * kWave + lane) * 8)
                          : u32x4{0u, 0u, 0u, 0u};
       }
     }
@@ -286,7 +297,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
       const u32x4 xv = xs[j];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        if (ok[r]) acc[r] = dot8_bf16(load16(wrow[r] + j * 8), xv, acc[r]);
+        if (ok[r]) acc[r] = dot8_bf16(load16<NT>(wrow[r] + j * 8), xv, acc[r]);
       }
     }
   }
@@ -295,24 +306,35 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
   if (lane == 0 && tile_ok) epilogue<EPI, R>(a, tile, acc, ok);
 }
 
-template <int KC, int R, int WAVES, int EPI>
+template <int KC, int R, int WAVES, int EPI, bool NT>
 static hipError_t launch_gemv(const GemvArgs &a, hipStream_t stream) {
   const int64_t blocks = (a.n_tiles + WAVES - 1) / WAVES;
   const size_t lds = static_cast<size_t>(a.k) * 2;
-  hipLaunchKernelGGL((gemv_kernel<KC, R, WAVES, EPI>), dim3(blocks),
+  hipLaunchKernelGGL((gemv_kernel<KC, R, WAVES, EPI, NT>), dim3(blocks),
                      dim3(WAVES * kWave), lds, stream, a);
   return hipGetLastError();
 }
 
-// Shape policy: K = 4096 rows are 8 KiB (8 loads per lane), K = 14336 rows
-// are 28 KiB (28 loads per lane); other K use the looped kernel.
+// Launch shapes, from the MI355X sweep of one-shot grids: K = 4096 rows are
+// 8 KiB (8 loads per lane), K = 14336 rows 28 KiB (28 loads per lane, one
+// row per wave); 8 waves per workgroup except for the fused gate/up tile
+// and the LM head; nontemporal loads for the 1 GB LM head.  Other K use
+// the looped kernel.
+template <int EPI>
+struct GemvShape {
+  static constexpr int WAVES = (EPI == kSwiglu || EPI == kLogits) ? 4 : 8;
+  static constexpr bool NT = EPI == kLogits;
+};
+
 template <int R, int EPI>
 static hipError_t dispatch_gemv(const GemvArgs &a, hipStream_t stream) {
-  if (a.k == 4096) return launch_gemv<8, R, 4, EPI>(a, stream);
+  constexpr int W = GemvShape<EPI>::WAVES;
+  constexpr bool NT = GemvShape<EPI>::NT;
+  if (a.k == 4096) return launch_gemv<8, R, W, EPI, NT>(a, stream);
   if constexpr (R == 1) {
-    if (a.k == 14336) return launch_gemv<28, 1, 4, EPI>(a, stream);
+    if (a.k == 14336) return launch_gemv<28, 1, 8, EPI, NT>(a, stream);
   }
-  return launch_gemv<0, R, 4, EPI>(a, stream);
+  return launch_gemv<0, R, 4, EPI, NT>(a, stream);
 }
 
 static int check_common(const void *w, const void *x, int64_t n, int64_t k) {
@@ -320,6 +342,19 @@ static int check_common(const void *w, const void *x, int64_t n, int64_t k) {
   if ((k & 7) != 0 || !aligned16(w) || !aligned16(x)) return CASCADE_EALIGN;
   if (k * 2 > kMaxGemvLdsBytes) return CASCADE_ESHAPE;
   return 0;
+}
+
+hipError_t launch_logits_gemv(const uint16_t *w, int64_t rows, int64_t k,
+                              const uint16_t *h, float *logits,
+                              hipStream_t stream) {
+  GemvArgs a{};
+  a.w0 = w;
+  a.n0 = rows;
+  a.k = k;
+  a.x = h;
+  a.yf = logits;
+  a.n_tiles = (rows + 1) / 2;
+  return dispatch_gemv<2, kLogits>(a, stream);
 }
 
 }  // namespace cascade

@@ -1,15 +1,14 @@
 // Vocabulary-chunk LM head with an exact on-device top-k (gfx950).
 //
-// One launch handles one chunk of `rows` LM-head rows (a streamed 128 MiB
-// slot, or the whole resident head):
-//   1. each workgroup (8 waves) computes the fp32 logits of its block of
-//      rows with the same wave-per-row-pair GEMV as gemv.hip, keeping them in
-//      LDS (and optionally writing them out);
-//   2. wave 0 selects the block's top-k with k passes of a wave-wide
-//      maximum over (value, index) keys;
-//   3. the last workgroup to finish (atomic ticket) merges every block's
-//      candidates with the running list of earlier chunks and publishes the
-//      running top-k.
+// One call handles one chunk of `rows` LM-head rows (a streamed 128 MiB
+// slot, or the whole resident head) in three launches:
+//   1. the logits GEMV (gemv.hip, fp32 output, nontemporal weight loads)
+//      writes logits[r] = W[r] . h, unrounded;
+//   2. topk_candidates_kernel: each workgroup takes a span of logits and
+//      selects its top-k with k passes of a block-wide maximum over
+//      (value, index) keys;
+//   3. topk_merge_kernel (one workgroup) merges all spans' candidates with
+//      the running list of earlier chunks and publishes the running top-k.
 // Keys order by value descending then index ascending (see topk_key), so the
 // result is the exact top-k of the fp32 logits with lower-index-first ties:
 // the reference's per-chunk torch.topk + merge_topk (layer_streaming/
@@ -19,187 +18,123 @@
 
 namespace cascade {
 
-constexpr int kLmWaves = 8;
-constexpr int kLmThreads = kLmWaves * kWave;
-constexpr int kLmRowsPerWaveIter = 2;
-constexpr int kLmMaxRowsPerBlock = 1024;   // 16 keys per lane in step 2
-constexpr int kLmMergeSlots = 16;          // keys per thread in step 3
-constexpr int kLmMaxMerge = kLmMergeSlots * kLmThreads;  // 8192
+constexpr int kTopkThreads = 256;
+constexpr int kTopkWaves = kTopkThreads / kWave;
+constexpr int kTopkSlots = 16;  // keys per thread
+constexpr int kTopkMaxSpan = kTopkSlots * kTopkThreads;   // 4096 logits
+constexpr int kTopkMaxMerge = kTopkSlots * kTopkThreads;  // 4096 keys
+constexpr int kTopkMinSpan = 1024;
 constexpr int kLmMaxTopK = 64;
-constexpr size_t kLmHeaderBytes = 256;     // ticket counter
+constexpr size_t kLmHeaderBytes = 256;  // reserved
 constexpr size_t kLmRunningBytes = kLmMaxTopK * sizeof(uint64_t);
+constexpr size_t kLmCandBytes = kTopkMaxMerge * sizeof(uint64_t);
 
-struct LmArgs {
-  const uint16_t *w;
+struct TopkArgs {
+  const float *logits;
   int64_t rows;
-  int64_t k;
   int64_t row_offset;
-  const uint16_t *h;
   int top_k;
   int first;
-  int rows_per_block;
+  int span;
   int nblocks;
-  float *logits_out;
-  uint32_t *counter;
   uint64_t *running;
   uint64_t *cand;
   float *out_values;
   int64_t *out_indices;
 };
 
-template <int KC>
-__global__ __launch_bounds__(kLmThreads) void lm_head_topk_kernel(LmArgs a) {
-  constexpr int R = kLmRowsPerWaveIter;
-  extern __shared__ u32x4 xs[];
-  __shared__ float s_logit[kLmMaxRowsPerBlock];
-  __shared__ uint64_t s_red[2][kLmWaves];
-  __shared__ int s_last;
+// Largest key strictly below `thr` among a thread's keys, maximised over the
+// workgroup.  `parity` alternates the LDS slot between passes so one barrier
+// per pass suffices.
+__device__ __forceinline__ uint64_t block_next_key(
+    const uint64_t (&keys)[kTopkSlots], uint64_t thr,
+    uint64_t (&red)[2][kTopkWaves], int parity) {
+  uint64_t best = 0ull;
+#pragma unroll
+  for (int t = 0; t < kTopkSlots; ++t)
+    if (keys[t] < thr && keys[t] > best) best = keys[t];
+  best = wave_max_u64(best);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[parity][threadIdx.x / kWave] = best;
+  __syncthreads();
+  best = 0ull;
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w)
+    best = red[parity][w] > best ? red[parity][w] : best;
+  return best;
+}
+
+// Candidates: workgroup b selects the top-k of logits [b*span, (b+1)*span).
+__global__ __launch_bounds__(kTopkThreads) void topk_candidates_kernel(
+    TopkArgs a) {
+  __shared__ uint64_t s_red[2][kTopkWaves];
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const int64_t rb = static_cast<int64_t>(blockIdx.x) * a.rows_per_block;
-  const int nrows =
-      static_cast<int>(min(static_cast<int64_t>(a.rows_per_block), a.rows - rb));
-
-  {
-    const int64_t nvec = a.k >> 3;
-    const u32x4 *hg = reinterpret_cast<const u32x4 *>(a.h);
-    for (int64_t j = tid; j < nvec; j += kLmThreads) xs[j] = hg[j];
-  }
-  __syncthreads();
-
-  // 1. logits of this block's rows.
-  for (int base = wave * R; base < nrows; base += kLmWaves * R) {
-    float acc[R];
-    bool ok[R];
-    const uint16_t *wrow[R];
+  const int64_t begin = static_cast<int64_t>(blockIdx.x) * a.span;
+  const int n = static_cast<int>(min(static_cast<int64_t>(a.span), a.rows - begin));
+  uint64_t keys[kTopkSlots];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      ok[r] = base + r < nrows;
-      wrow[r] = a.w + (rb + base + (ok[r] ? r : 0)) * a.k;
-      acc[r] = 0.0f;
-    }
-    if constexpr (KC > 0) {
-      u32x4 wv[R][KC];
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int c = 0; c < KC; ++c)
-          wv[r][c] = ok[r] ? *reinterpret_cast<const u32x4 *>(
-                                 wrow[r] + (c * kWave + lane) * 8)
-                           : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const u32x4 xv = xs[c * kWave + lane];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = dot8_bf16(wv[r][c], xv, acc[r]);
-      }
-    } else {
-      const int64_t nvec = a.k >> 3;
-      for (int64_t j = lane; j < nvec; j += kWave) {
-        const u32x4 xv = xs[j];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (ok[r])
-            acc[r] = dot8_bf16(
-                *reinterpret_cast<const u32x4 *>(wrow[r] + j * 8), xv, acc[r]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (!ok[r]) continue;
-        s_logit[base + r] = acc[r];
-        if (a.logits_out != nullptr) a.logits_out[rb + base + r] = acc[r];
-      }
-    }
-  }
-  __syncthreads();
-
-  // 2. block top-k (wave 0): k passes of "largest key below the previous".
-  if (wave == 0) {
-    uint64_t keys[kLmMaxRowsPerBlock / kWave];
-#pragma unroll
-    for (int t = 0; t < kLmMaxRowsPerBlock / kWave; ++t) {
-      const int li = t * kWave + lane;
-      keys[t] = li < nrows
-                    ? topk_key(s_logit[li],
-                               static_cast<uint32_t>(a.row_offset + rb + li))
+  for (int t = 0; t < kTopkSlots; ++t) {
+    const int i = t * kTopkThreads + tid;
+    keys[t] = i < n ? topk_key(a.logits[begin + i],
+                               static_cast<uint32_t>(a.row_offset + begin + i))
                     : 0ull;
-    }
-    uint64_t thr = ~0ull;
-    for (int j = 0; j < a.top_k; ++j) {
-      uint64_t best = 0ull;
-#pragma unroll
-      for (int t = 0; t < kLmMaxRowsPerBlock / kWave; ++t)
-        if (keys[t] < thr && keys[t] > best) best = keys[t];
-      best = wave_max_u64(best);
-      if (lane == 0)
-        a.cand[static_cast<int64_t>(blockIdx.x) * a.top_k + j] = best;
-      thr = best;
-    }
-  }
-
-  // 3. the last block merges all candidates with the running list.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(a.counter, 1u);
-    s_last = (prev == static_cast<uint32_t>(a.nblocks - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  const int ncand = a.nblocks * a.top_k;
-  const int ntot = ncand + (a.first ? 0 : a.top_k);
-  uint64_t keys[kLmMergeSlots];
-#pragma unroll
-  for (int t = 0; t < kLmMergeSlots; ++t) {
-    const int i = t * kLmThreads + tid;
-    keys[t] = i < ncand ? a.cand[i] : (i < ntot ? a.running[i - ncand] : 0ull);
   }
   uint64_t thr = ~0ull;
   for (int j = 0; j < a.top_k; ++j) {
-    uint64_t best = 0ull;
+    thr = block_next_key(keys, thr, s_red, j & 1);
+    if (tid == 0) a.cand[static_cast<int64_t>(blockIdx.x) * a.top_k + j] = thr;
+  }
+}
+
+// Merge (one workgroup): all spans' candidates plus the running list of
+// earlier chunks.  A separate launch, so the kernel boundary publishes the
+// candidates (no per-workgroup L2 writeback for a ticket).
+__global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(TopkArgs a) {
+  __shared__ uint64_t s_red[2][kTopkWaves];
+  const int tid = threadIdx.x;
+  const int ncand = a.nblocks * a.top_k;
+  const int ntot = ncand + (a.first ? 0 : a.top_k);
+  uint64_t keys[kTopkSlots];
 #pragma unroll
-    for (int t = 0; t < kLmMergeSlots; ++t)
-      if (keys[t] < thr && keys[t] > best) best = keys[t];
-    best = wave_max_u64(best);
-    if (lane == 0) s_red[j & 1][wave] = best;
-    __syncthreads();
-    best = 0ull;
-#pragma unroll
-    for (int w = 0; w < kLmWaves; ++w)
-      best = s_red[j & 1][w] > best ? s_red[j & 1][w] : best;
-    thr = best;
+  for (int t = 0; t < kTopkSlots; ++t) {
+    const int i = t * kTopkThreads + tid;
+    keys[t] = i < ncand ? a.cand[i] : (i < ntot ? a.running[i - ncand] : 0ull);
+  }
+  __syncthreads();  // every read of the old running list precedes its rewrite
+  uint64_t thr = ~0ull;
+  for (int j = 0; j < a.top_k; ++j) {
+    thr = block_next_key(keys, thr, s_red, j & 1);
     if (tid == 0) {
-      a.running[j] = best;
-      a.out_values[j] = best ? key_value(best) : -INFINITY;
-      a.out_indices[j] = best ? key_index(best) : int64_t{-1};
+      a.running[j] = thr;
+      a.out_values[j] = thr ? key_value(thr) : -INFINITY;
+      a.out_indices[j] = thr ? key_index(thr) : int64_t{-1};
     }
   }
-  if (tid == 0) *a.counter = 0u;  // ready for the next chunk
 }
 
-static int lm_rows_per_block(int64_t rows, int64_t top_k) {
-  // Smallest multiple of 16 rows (>= 64) such that every block's candidates
-  // plus the running list fit the single-block merge.
-  const int64_t budget = kLmMaxMerge - top_k;
-  int64_t rpb = (rows * top_k + budget - 1) / budget;
-  rpb = ((rpb + 15) / 16) * 16;
-  if (rpb < 64) rpb = 64;
-  while (rpb <= kLmMaxRowsPerBlock &&
-         ((rows + rpb - 1) / rpb) * top_k + top_k > kLmMaxMerge)
-    rpb += 16;
-  return static_cast<int>(rpb);
+struct TopkShape {
+  int span;
+  int nblocks;
+};
+
+// Spans of 1024..4096 logits (whole multiples of the block size) such that
+// every span's candidates plus the running list fit the single-block merge.
+static bool topk_shape(int64_t rows, int64_t top_k, TopkShape *out) {
+  const int64_t budget = kTopkMaxMerge - top_k;
+  int64_t span = (rows * top_k + budget - 1) / budget;
+  span = ((span + kTopkThreads - 1) / kTopkThreads) * kTopkThreads;
+  if (span < kTopkMinSpan) span = kTopkMinSpan;
+  while (span <= kTopkMaxSpan &&
+         ((rows + span - 1) / span) * top_k + top_k > kTopkMaxMerge)
+    span += kTopkThreads;
+  if (span > kTopkMaxSpan) return false;
+  out->span = static_cast<int>(span);
+  out->nblocks = static_cast<int>((rows + span - 1) / span);
+  return true;
 }
 
-static size_t lm_workspace(int64_t nblocks, int64_t top_k) {
-  return kLmHeaderBytes + kLmRunningBytes +
-         static_cast<size_t>(nblocks) * top_k * sizeof(uint64_t);
+static size_t lm_workspace(int64_t rows) {
+  const size_t logits = ((static_cast<size_t>(rows) * 4 + 255) / 256) * 256;
+  return kLmHeaderBytes + kLmRunningBytes + kLmCandBytes + logits;
 }
 
 }  // namespace cascade
@@ -209,9 +144,9 @@ using namespace cascade;
 extern "C" size_t cascade_lm_head_workspace_bytes(int64_t rows,
                                                   int64_t top_k) {
   if (rows <= 0 || top_k < 1 || top_k > kLmMaxTopK) return 0;
-  const int rpb = lm_rows_per_block(rows, top_k);
-  if (rpb > kLmMaxRowsPerBlock) return 0;
-  return lm_workspace((rows + rpb - 1) / rpb, top_k);
+  TopkShape shape;
+  if (!topk_shape(rows, top_k, &shape)) return 0;
+  return lm_workspace(rows);
 }
 
 extern "C" int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
@@ -231,34 +166,34 @@ extern "C" int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
   if ((k & 7) != 0 || !aligned16(w) || !aligned16(h) || !aligned16(workspace))
     return CASCADE_EALIGN;
   if (k * 2 > kMaxGemvLdsBytes) return CASCADE_ESHAPE;
-  const int rpb = lm_rows_per_block(rows, top_k);
-  if (rpb > kLmMaxRowsPerBlock) return CASCADE_ESHAPE;
-  const int64_t nblocks = (rows + rpb - 1) / rpb;
-  if (workspace_bytes < lm_workspace(nblocks, top_k)) return CASCADE_EWORKSPACE;
-  LmArgs a{};
-  a.w = static_cast<const uint16_t *>(w);
+  TopkShape shape;
+  if (!topk_shape(rows, top_k, &shape)) return CASCADE_ESHAPE;
+  if (workspace_bytes < lm_workspace(rows)) return CASCADE_EWORKSPACE;
+  char *ws = static_cast<char *>(workspace);
+  float *logits = logits_out != nullptr
+                      ? logits_out
+                      : reinterpret_cast<float *>(ws + kLmHeaderBytes +
+                                                  kLmRunningBytes + kLmCandBytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_logits_gemv(static_cast<const uint16_t *>(w), rows, k,
+                                    static_cast<const uint16_t *>(h), logits, s);
+  if (e != hipSuccess) return e;
+  TopkArgs a{};
+  a.logits = logits;
   a.rows = rows;
-  a.k = k;
   a.row_offset = row_offset;
-  a.h = static_cast<const uint16_t *>(h);
   a.top_k = static_cast<int>(top_k);
   a.first = first_chunk ? 1 : 0;
-  a.rows_per_block = rpb;
-  a.nblocks = static_cast<int>(nblocks);
-  a.logits_out = logits_out;
-  char *ws = static_cast<char *>(workspace);
-  a.counter = reinterpret_cast<uint32_t *>(ws);
+  a.span = shape.span;
+  a.nblocks = shape.nblocks;
   a.running = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes);
   a.cand = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes + kLmRunningBytes);
   a.out_values = out_values;
   a.out_indices = out_indices;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const size_t lds = static_cast<size_t>(k) * 2;
-  if (k == 4096)
-    hipLaunchKernelGGL(lm_head_topk_kernel<8>, dim3(nblocks), dim3(kLmThreads),
-                       lds, s, a);
-  else
-    hipLaunchKernelGGL(lm_head_topk_kernel<0>, dim3(nblocks), dim3(kLmThreads),
-                       lds, s, a);
+  hipLaunchKernelGGL(topk_candidates_kernel, dim3(shape.nblocks),
+                     dim3(kTopkThreads), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kTopkThreads), 0, s, a);
   return hipGetLastError();
 }

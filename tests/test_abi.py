@@ -61,12 +61,13 @@ def test_argument_checks_reject_without_launching():
 
 
 def test_workspace_sizes():
-    # attention: counters + (m, l, acc[128]) per (kv head, split, q head)
-    small = _hip.attention_workspace_bytes(2048)
-    assert small == 256 + 8 * 32 * 4 * (2 + 128) * 4  # 32 splits of 64
-    big = _hip.attention_workspace_bytes(32769)
-    assert big == 256 + 8 * 129 * 4 * (2 + 128) * 4  # 129 splits of 256
-    assert _hip.lm_head_workspace_bytes(16384, 10) == 256 + 512 + 256 * 10 * 8
+    # attention: counters + (m, l, acc[128]) per (kv head, split, q head),
+    # sized for the maximum of 64 splits whatever the length
+    for length in (1, 2048, 32769, 1 << 20):
+        assert _hip.attention_workspace_bytes(length) == 256 + 8 * 64 * 4 * (2 + 128) * 4
+    # LM head: counter, running top-64 keys, 4096 candidate keys, fp32 logits
+    assert _hip.lm_head_workspace_bytes(16384, 10) == 256 + 512 + 4096 * 8 + 16384 * 4
+    assert _hip.lm_head_workspace_bytes(128256, 64) == 256 + 512 + 4096 * 8 + 128256 * 4
     with pytest.raises(ValueError):
         _hip.lm_head_workspace_bytes(16384, 65)
     with pytest.raises(ValueError):
