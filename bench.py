@@ -10,7 +10,10 @@ inputs already resident in HBM.
 
 Also reported (extra keys, not ``value``):
   * roofline of the dominant kernel (the fused gate/up SwiGLU GEMV, 224 MiB
-    per launch), timed live with HIP events on its stream;
+    per launch), timed live in the timed region with HIP events bound to
+    each launch of the kernel on its stream (hipExtLaunchKernel start/stop
+    events: kernel execution only), HBM traffic per launch from the
+    committed FETCH_SIZE / WRITE_SIZE counter summary;
   * streamed: BASELINE config 3 -- full_pinned 16 GB host arena,
     matrix_group units through two 224 MiB slots, streamed vocabulary;
     decode ms/token and the PCIe-inclusive H2D GB/s (skip: --no-streamed);
@@ -53,7 +56,53 @@ def parse_args():
     p.add_argument("--streamed-steps", type=int, default=7)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-seconds", type=float, default=15.0)
+    p.add_argument("--probe", action="store_true",
+                   help="only run the HBM-counter probe: 4 plain device copies "
+                        "of 256 MiB, then 12 gate/up SwiGLU launches over 3 "
+                        "rotating weight copies (for rocprofv3 --pmc runs)")
     return p.parse_args()
+
+
+PROBE_COPY_BYTES = 256 << 20
+TRAFFIC_FILE = ROOT / "profiles" / "gate_up_traffic.txt"
+
+
+def counter_probe():
+    """Known-size copies (counter calibration) then the dominant kernel."""
+
+    import torch
+    from layer_streaming import _hip
+
+    dev = torch.device("cuda:0")
+    src = torch.randn(PROBE_COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        _hip.device_copy(dst, src)
+    torch.cuda.synchronize(dev)
+    log("probe: 4 device copies of {} bytes done".format(PROBE_COPY_BYTES))
+    mats = [(torch.randn(INTER, HIDDEN, device=dev).mul_(0.02).to(torch.bfloat16),
+             torch.randn(INTER, HIDDEN, device=dev).mul_(0.02).to(torch.bfloat16))
+            for _ in range(3)]
+    x = torch.randn(HIDDEN, device=dev).to(torch.bfloat16)
+    norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(INTER, dtype=torch.bfloat16, device=dev)
+    for i in range(12):
+        g, u = mats[i % 3]
+        _hip.gate_up_swiglu(g, u, x, norm, 1e-5, y)
+    torch.cuda.synchronize(dev)
+    log("probe: 12 gate/up launches done")
+
+
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed counter summary."""
+
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(line.split("=", 1)[1])
+    except OSError:
+        return None
+    return None
 
 
 def token_bytes(context):
@@ -266,6 +315,9 @@ def main():
     from layer_streaming import _hip
 
     _hip.load()
+    if args.probe:
+        counter_probe()
+        return
     resident = resident_decode(args)
     ms = resident["ms_per_step"]
     gu_us = resident["gate_up_avg_us"]
@@ -298,13 +350,13 @@ def main():
         "token_hbm_frac_of_peak": round(
             resident["token_hbm_bytes"] / 1e9 / (ms / 1e3) / HBM_PEAK_GBPS, 4),
         "roofline": {
-            "kernel": "gate_up_swiglu GEMV (gemv_kernel<8,2,4,3>), 2x[14336,4096] bf16",
+            "kernel": "gate_up_swiglu GEMV (gemv_kernel<8,2,4,3,true>), 2x[14336,4096] bf16",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "bytes_per_launch": gate_up_bytes(),
             "avg_launch_us": round(gu_us, 3),
             "launches_timed": resident["gate_up_launches"],

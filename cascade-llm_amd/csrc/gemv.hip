@@ -310,20 +310,20 @@ template <int KC, int R, int WAVES, int EPI, bool NT>
 static hipError_t launch_gemv(const GemvArgs &a, hipStream_t stream) {
   const int64_t blocks = (a.n_tiles + WAVES - 1) / WAVES;
   const size_t lds = static_cast<size_t>(a.k) * 2;
-  hipLaunchKernelGGL((gemv_kernel<KC, R, WAVES, EPI, NT>), dim3(blocks),
-                     dim3(WAVES * kWave), lds, stream, a);
-  return hipGetLastError();
+  return launch_kernel(gemv_kernel<KC, R, WAVES, EPI, NT>, dim3(blocks),
+                       dim3(WAVES * kWave), lds, stream, a);
 }
 
-// Launch shapes, from the MI355X sweep of one-shot grids: K = 4096 rows are
+// Launch shapes, from an MI355X sweep of one-shot grids with rotating weight
+// copies (so no launch is served by the 256 MB MALL): K = 4096 rows are
 // 8 KiB (8 loads per lane), K = 14336 rows 28 KiB (28 loads per lane, one
 // row per wave); 8 waves per workgroup except for the fused gate/up tile
-// and the LM head; nontemporal loads for the 1 GB LM head.  Other K use
-// the looped kernel.
+// and the LM head; nontemporal weight loads everywhere (every weight byte
+// is read once per token).  Other K use the looped kernel.
 template <int EPI>
 struct GemvShape {
   static constexpr int WAVES = (EPI == kSwiglu || EPI == kLogits) ? 4 : 8;
-  static constexpr bool NT = EPI == kLogits;
+  static constexpr bool NT = true;
 };
 
 template <int R, int EPI>
@@ -560,10 +560,9 @@ extern "C" int cascade_rmsnorm_bf16(const void *x, const void *weight, void *y,
     return CASCADE_EINVAL;
   if ((n & 7) || !aligned16(x) || !aligned16(weight) || !aligned16(y))
     return CASCADE_EALIGN;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)),
-                     dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t *>(x),
-                     static_cast<const uint16_t *>(weight),
-                     static_cast<uint16_t *>(y), n, eps);
-  return hipGetLastError();
+  return launch_kernel(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)),
+                       dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t *>(x),
+                       static_cast<const uint16_t *>(weight),
+                       static_cast<uint16_t *>(y), n, eps);
 }

@@ -190,10 +190,8 @@ extern "C" int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
   a.cand = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes + kLmRunningBytes);
   a.out_values = out_values;
   a.out_indices = out_indices;
-  hipLaunchKernelGGL(topk_candidates_kernel, dim3(shape.nblocks),
-                     dim3(kTopkThreads), 0, s, a);
-  e = hipGetLastError();
+  e = launch_kernel(topk_candidates_kernel, dim3(shape.nblocks),
+                    dim3(kTopkThreads), 0, s, a);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kTopkThreads), 0, s, a);
-  return hipGetLastError();
+  return launch_kernel(topk_merge_kernel, dim3(1), dim3(kTopkThreads), 0, s, a);
 }

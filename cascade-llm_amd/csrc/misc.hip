@@ -93,11 +93,11 @@ extern "C" int cascade_embedding_gather_bf16(const void *table, int64_t vocab,
     return CASCADE_EINVAL;
   if ((hidden & 7) || !aligned16(table) || !aligned16(out))
     return CASCADE_EALIGN;
-  hipLaunchKernelGGL(embedding_gather_kernel, dim3(static_cast<unsigned>(n_ids)),
-                     dim3(kGatherThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t *>(table), vocab, hidden, ids,
-                     static_cast<uint16_t *>(out), error_flag);
-  return hipGetLastError();
+  return launch_kernel(embedding_gather_kernel,
+                       dim3(static_cast<unsigned>(n_ids)), dim3(kGatherThreads),
+                       0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t *>(table), vocab, hidden, ids,
+                       static_cast<uint16_t *>(out), error_flag);
 }
 
 extern "C" int cascade_memcpy_h2d_async(void *dst, const void *src,
@@ -162,15 +162,34 @@ extern "C" int cascade_event_elapsed_ms(uint64_t start, uint64_t end,
                              reinterpret_cast<hipEvent_t>(end));
 }
 
+namespace cascade {
+namespace {
+thread_local LaunchEvents g_launch_events;
+}  // namespace
+
+LaunchEvents take_launch_events() {
+  const LaunchEvents ev = g_launch_events;
+  g_launch_events = LaunchEvents{};
+  return ev;
+}
+}  // namespace cascade
+
+extern "C" int cascade_time_next_launch(uint64_t start_event,
+                                        uint64_t stop_event) {
+  cascade::g_launch_events.start = reinterpret_cast<hipEvent_t>(start_event);
+  cascade::g_launch_events.stop = reinterpret_cast<hipEvent_t>(stop_event);
+  return 0;
+}
+
 extern "C" int cascade_hbm_read(const void *src, size_t bytes, float *sink,
                                 void *stream) {
   if (src == nullptr || sink == nullptr || bytes == 0) return CASCADE_EINVAL;
   if ((bytes & 15) || !aligned16(src)) return CASCADE_EALIGN;
   const int64_t nvec = static_cast<int64_t>(bytes >> 4);
-  hipLaunchKernelGGL(hbm_read_kernel, dim3(stream_blocks(nvec)),
-                     dim3(kStreamThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const u32x4 *>(src), nvec, sink);
-  return hipGetLastError();
+  return launch_kernel(hbm_read_kernel, dim3(stream_blocks(nvec)),
+                       dim3(kStreamThreads), 0,
+                       static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4 *>(src), nvec, sink);
 }
 
 extern "C" int cascade_device_copy(void *dst, const void *src, size_t bytes,
@@ -178,9 +197,9 @@ extern "C" int cascade_device_copy(void *dst, const void *src, size_t bytes,
   if (dst == nullptr || src == nullptr || bytes == 0) return CASCADE_EINVAL;
   if ((bytes & 15) || !aligned16(src) || !aligned16(dst)) return CASCADE_EALIGN;
   const int64_t nvec = static_cast<int64_t>(bytes >> 4);
-  hipLaunchKernelGGL(device_copy_kernel, dim3(stream_blocks(nvec)),
-                     dim3(kStreamThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<u32x4 *>(dst), static_cast<const u32x4 *>(src),
-                     nvec);
-  return hipGetLastError();
+  return launch_kernel(device_copy_kernel, dim3(stream_blocks(nvec)),
+                       dim3(kStreamThreads), 0,
+                       static_cast<hipStream_t>(stream),
+                       static_cast<u32x4 *>(dst),
+                       static_cast<const u32x4 *>(src), nvec);
 }

@@ -76,6 +76,7 @@ _SIGNATURES = {
     "cascade_event_elapsed_ms": (_INT, [_U64, _U64, ctypes.POINTER(_F)]),
     "cascade_hbm_read": (_INT, [_P, _SZ, _P, _P]),
     "cascade_device_copy": (_INT, [_P, _P, _SZ, _P]),
+    "cascade_time_next_launch": (_INT, [_U64, _U64]),
 }
 
 ABI_VERSION = 1
@@ -520,6 +521,15 @@ class HipEvent:
             except Exception:  # interpreter shutdown
                 pass
             self.handle = 0
+
+
+def time_next_launch(start, stop):
+    """Bind two timing HipEvents (or None) to this thread's next kernel
+    launch through the library: their elapsed time is that kernel's own
+    duration.  ``time_next_launch(None, None)`` clears pending events."""
+
+    call("cascade_time_next_launch", start.handle if start else 0,
+         stop.handle if stop else 0)
 
 
 def stream_wait(stream, event):

@@ -188,6 +188,9 @@ _EXPECTED = {
     "vocab_size": 128256,
 }
 
+# Kernel groups whose entry point launches exactly one kernel.
+_KERNEL_TIMED_GROUPS = frozenset(("gate_up", "qkv", "o_proj", "down_proj"))
+
 
 class Llama31DecodeExecutor:
     """Stateful callbacks consumed by the runtimes (one unpadded request: a
@@ -403,9 +406,7 @@ class Llama31DecodeExecutor:
         half = self.head_dim // 2
         for t, slot in enumerate(self._slots(state)):
             pos = state.positions[t]
-            ev = self._events("qkv")
-            if ev:
-                ev[0].record()
+            ev = self._mark_begin("qkv")
             rc = self._k_qkv(
                 wq, wk, wv, nq, nk, nv, self.hidden, x + t * row, norm, self.eps,
                 cos + 2 * half * pos, sin + 2 * half * pos,
@@ -413,8 +414,7 @@ class Llama31DecodeExecutor:
                 self._kv_pointer(layer, 0, slot) if wk else 0,
                 self._kv_pointer(layer, 1, slot) if wv else 0,
                 stride, stream)
-            if ev:
-                ev[1].record()
+            self._mark_end("qkv", ev, rc)
             _hip.check("cascade_qkv_rope_bf16", rc)
 
     def _attention_o(self, layer, ptrs, state, stream):
@@ -426,32 +426,29 @@ class Llama31DecodeExecutor:
         stride = self.kv_cache.head_stride
         ws, ws_bytes = self._attn_ws.data_ptr(), self._attn_ws.numel()
         for t, slot in enumerate(self._slots(state)):
-            ev = self._events("attention")
-            if ev:
-                ev[0].record()
+            ev = self._mark_begin("attention")
             rc = self._k_attn(self._q_ptr + t * row, k0, v0, stride, slot + 1,
                               self.n_heads, self.n_kv_heads, self.head_dim,
                               self.scale, self._attn_ptr + t * row, ws, ws_bytes,
                               stream)
-            if ev:
-                ev[1].record()
+            self._mark_end("attention", ev, rc)
             _hip.check("cascade_decode_attention_bf16", rc)
-            ev = self._events("o_proj")
-            if ev:
-                ev[0].record()
+            ev = self._mark_begin("o_proj")
             xt = x + t * row
             rc = self._k_residual(wo, self._attn_ptr + t * row, xt, xt,
                                   self.hidden, self.hidden, stream)
-            if ev:
-                ev[1].record()
+            self._mark_end("o_proj", ev, rc)
             _hip.check("cascade_gemv_residual_bf16", rc)
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
 
     def instrument(self, name, launches):
-        """Bracket the next ``launches`` launches of kernel group ``name``
-        ("gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head")
-        with timing events on the launching stream; read them back with
-        :meth:`kernel_times_ms` after a synchronize."""
+        """Time the next ``launches`` launches of kernel group ``name``
+        ("gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head");
+        read them back with :meth:`kernel_times_ms` after a synchronize.
+        The one-kernel groups (gate_up, qkv, o_proj, down_proj) bind the
+        events to the kernel's own execution; attention (main + split merge)
+        and lm_head (GEMV + two top-k kernels) are bracketed by events
+        recorded on the launching stream, which include dispatch time."""
 
         self._instrumented[name] = [
             (_hip.HipEvent(enable_timing=True), _hip.HipEvent(enable_timing=True))
@@ -474,6 +471,23 @@ class Llama31DecodeExecutor:
         self._instrument_next[name] = index + 1
         return pairs[index]
 
+    def _mark_begin(self, name):
+        ev = self._events(name)
+        if ev is not None:
+            if name in _KERNEL_TIMED_GROUPS:
+                _hip.time_next_launch(ev[0], ev[1])
+            else:
+                ev[0].record()
+        return ev
+
+    def _mark_end(self, name, ev, rc):
+        if ev is None:
+            return
+        if name not in _KERNEL_TIMED_GROUPS:
+            ev[1].record()
+        elif rc != 0:
+            _hip.time_next_launch(None, None)
+
     def _gate_up(self, layer, ptrs, state, stream):
         x = state.hidden_states.data_ptr()
         row = 2 * self.hidden
@@ -481,14 +495,11 @@ class Llama31DecodeExecutor:
         norm = self._norm_ptrs[layer][1]
         wg, wu = ptrs["gate_proj"], ptrs["up_proj"]
         for t in range(len(state.positions)):
-            ev = self._events("gate_up")
-            if ev:
-                ev[0].record()
+            ev = self._mark_begin("gate_up")
             rc = self._k_swiglu(wg, wu, self.intermediate, self.hidden, x + t * row,
                                 norm, self.eps, self._inter_ptr + t * inter_row,
                                 stream)
-            if ev:
-                ev[1].record()
+            self._mark_end("gate_up", ev, rc)
             _hip.check("cascade_gate_up_swiglu_bf16", rc)
 
     def _gate(self, layer, ptrs, state, stream):
@@ -517,14 +528,11 @@ class Llama31DecodeExecutor:
         row, inter_row = 2 * self.hidden, 2 * self.intermediate
         wd = ptrs["down_proj"]
         for t in range(len(state.positions)):
-            ev = self._events("down_proj")
-            if ev:
-                ev[0].record()
+            ev = self._mark_begin("down_proj")
             xt = x + t * row
             rc = self._k_residual(wd, self._inter_ptr + t * inter_row, xt, xt,
                                   self.hidden, self.intermediate, stream)
-            if ev:
-                ev[1].record()
+            self._mark_end("down_proj", ev, rc)
             _hip.check("cascade_gemv_residual_bf16", rc)
         if self.capture is not None:
             self.capture.append((layer, state.hidden_states.detach().clone()))
@@ -583,7 +591,6 @@ class Llama31DecodeExecutor:
             head = self.resident["lm_head.weight"]
             vocab, _ = _hip.bf16_weight(head, "lm_head.weight", k=self.hidden)
             size = _hip.lm_head_workspace_bytes(vocab, self.top_k)
-            # zero-filled once; the kernel returns its ticket counter to 0
             self._head_ws = torch.zeros(size, dtype=torch.uint8, device=self.device)
             self._head = (head.data_ptr(), vocab)
         head_ptr, vocab = self._head
@@ -592,15 +599,12 @@ class Llama31DecodeExecutor:
         indices = torch.empty((1, 1, self.top_k), dtype=torch.int64, device=self.device)
         ws, ws_bytes = self._head_ws.data_ptr(), self._head_ws.numel()
         for s in range(count):
-            ev = self._events("lm_head")
-            if ev:
-                ev[0].record()
+            ev = self._mark_begin("lm_head")
             rc = self._k_head(head_ptr, vocab, self.hidden, 0,
                               normed.data_ptr() + 2 * self.hidden * s, self.top_k,
                               1, logits.data_ptr() + 4 * vocab * s, ws, ws_bytes,
                               values.data_ptr(), indices.data_ptr(), stream)
-            if ev:
-                ev[1].record()
+            self._mark_end("lm_head", ev, rc)
             _hip.check("cascade_lm_head_topk_bf16", rc)
         state.logits = logits
         state.topk_values = values

@@ -189,6 +189,17 @@ int cascade_event_elapsed_ms(uint64_t start, uint64_t end, float *ms);
 int cascade_hbm_read(const void *src, size_t bytes, float *sink, void *stream);
 int cascade_device_copy(void *dst, const void *src, size_t bytes, void *stream);
 
+/* Binds two timing events (either may be 0) to the calling thread's next
+ * kernel launch through this library: the start event takes that kernel's
+ * start time and the stop event its end time (hipExtLaunchKernel), so their
+ * elapsed time is the kernel's own duration.  The launch consumes them; an
+ * entry point that fails before launching leaves them pending, and
+ * (0, 0) clears them.  For an entry point that launches several kernels
+ * only the first is timed.  No reference counterpart: the reference brackets
+ * calls with torch.cuda.Event pairs (benchmarks/llama31_8b_m1_bench.py:84-95),
+ * which also time the dispatch.                                             */
+int cascade_time_next_launch(uint64_t start_event, uint64_t stop_event);
+
 #ifdef __cplusplus
 }
 #endif
