@@ -1,23 +1,33 @@
 // GQA decode attention for one query token on gfx950 (split over the
-// sequence, "flash-decoding" style).
+// sequence, "flash-decoding" style), both products on the matrix cores.
 //
-// Grid: (splits, kv_heads).  A workgroup of 8 waves owns one span of
+// Grid: (splits, kv_heads).  A workgroup of 4 waves owns one span of
 // consecutive positions of one KV head and the G = 4 query heads that share
 // it (q head h uses kv head h / G: the repeat_interleave of _repeat_kv,
-// layer_streaming/llama31.py:28-31).
-//
-// Inside a workgroup every wave runs its own online softmax over rows of
-// the span: per pass a wave reads 4*RPL rows of K and V (a 256-byte row is
-// 16 lanes x 16 bytes, so one load instruction covers four rows and every
-// load of the pass is issued before any arithmetic).  The q.k dot of a row
-// is reduced across its 16 lanes with DPP, so every lane of the row holds
-// the score and multiplies its own 8 dims of V: scores, probabilities and
-// the running (max, sum, P.V) stay in registers.  Scores carry
-// scale * log2(e) so exp2 replaces exp.  The waves merge through LDS; with
-// more than one split a second launch merges the splits:
+// layer_streaming/llama31.py:28-31).  Each wave runs its own online softmax
+// over 32-row blocks of the span (blocks wave, wave + 4, ...), the waves
+// merge through LDS, and with more than one split a second launch merges the
+// splits:
 //   out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s,  M = max_s m_s
 // which is exactly softmax(q K^T * scale) V (F.scaled_dot_product_attention
-// without a mask, llama31.py:223-229; is_causal is False at decode).
+// without a mask, llama31.py:223-229; is_causal is False at decode).  Scores
+// carry scale * log2(e) so exp2 replaces exp.
+//
+// One 32-row block is 16 v_mfma_f32_16x16x32_bf16, with the G = 4 query
+// heads as the 16-wide N dimension (12 columns of zeros):
+//   S = K_blk q^T   two 16-row halves x four 32-dim chunks = 8 MFMAs
+//   O += V_blk^T P  eight 16-dim slots, K = the 32 rows      = 8 MFMAs
+// Lane l (c = l % 16, g4 = l / 16) ends up owning the scores of query head c
+// for rows 8 g4 .. 8 g4 + 7 of the block; that is exactly its piece of the
+// P operand, so the softmax moves no data beyond the max over the four lanes
+// of a head.  The row order inside a half (row 8 (i / 4) + 4 hf + i % 4 for
+// MFMA row i) is chosen for that.  V is loaded as whole 256-byte rows (16
+// lanes a row) and transposed in registers with byte permutes: lane l holds
+// dims 8 c .. 8 c + 7 of rows 8 g4 + j, and operand e takes dim 8 c + e of
+// its 8 rows.  P enters the MFMA rounded to bf16; the sum l is kept from the
+// fp32 values.  Rows past the end of the span are loaded from the span's last
+// row (always valid memory) and given a score of -inf.  K and V are read
+// once, with the nontemporal hint.
 #include "cascade_device.h"
 #include "cascade_internal.h"
 
@@ -25,7 +35,8 @@ namespace cascade {
 
 constexpr int kAttnG = 4;
 constexpr int kAttnD = 128;
-constexpr int kAttnWaves = 8;  // waves per workgroup (4 waves per SIMD)
+constexpr int kAttnWaves = 4;   // waves per workgroup
+constexpr int kAttnBlock = 32;  // rows per wave step (the MFMA K of P V)
 constexpr int kAttnMaxSplits = 64;
 constexpr size_t kAttnHeaderBytes = 256;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -43,7 +54,7 @@ struct AttnArgs {
   const uint16_t *v;
   int64_t head_stride;
   int32_t len;
-  int32_t span;     // positions per split
+  int32_t span;     // positions per split (a multiple of kAttnBlock)
   int32_t nsplits;
   float scale_log2;  // scale * log2(e)
   uint16_t *out;
@@ -51,174 +62,140 @@ struct AttnArgs {
   float *part_acc;     // [kv_heads][nsplits][G][D]
 };
 
-template <int RPL>
-struct KvTile {
-  u32x4 k[RPL];
-  u32x4 v[RPL];
-};
-
-// Loads the K / V pieces of one wave pass (rows base + 4i + grp).
-template <int RPL>
-__device__ __forceinline__ void load_tile(KvTile<RPL> &t, const uint16_t *kb,
-                                          const uint16_t *vb, int base, int grp,
-                                          int end) {
-#pragma unroll
-  for (int i = 0; i < RPL; ++i) {
-    const int row = base + 4 * i + grp;
-    if (row < end) {
-      t.k[i] = *reinterpret_cast<const u32x4 *>(kb + static_cast<int64_t>(row) * kAttnD);
-      t.v[i] = *reinterpret_cast<const u32x4 *>(vb + static_cast<int64_t>(row) * kAttnD);
-    } else {
-      t.k[i] = u32x4{0u, 0u, 0u, 0u};
-      t.v[i] = u32x4{0u, 0u, 0u, 0u};
-    }
-  }
+template <bool NT>
+__device__ __forceinline__ u32x4 kv_load(const uint16_t *p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  else
+    return *reinterpret_cast<const u32x4 *>(p);
 }
 
-// Online-softmax update of a wave's (m, l, acc) with one pass of rows.
-template <int RPL>
-__device__ __forceinline__ void attend_tile(const KvTile<RPL> &t,
-                                            const u32x4 (&qv)[kAttnG],
-                                            float scale_log2, int base, int grp,
-                                            int end, float (&m)[kAttnG],
-                                            float (&l)[kAttnG],
-                                            float (&acc)[kAttnG][8]) {
-  constexpr int G = kAttnG;
-  float s[G][RPL];
-  float pmax[G];
+// Operand e of the transposed V block: dword p = (row 2p, row 2p + 1) of
+// dim 8 c + e, from the lane's 8 loaded rows.
+__device__ __forceinline__ u32x4 v_operand(const u32x4 (&vt)[8], int e) {
+  // v_perm_b32 selectors: low halves / high halves of (src1, src0)
+  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+  u32x4 r;
 #pragma unroll
-  for (int h = 0; h < G; ++h) pmax[h] = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < RPL; ++i) {
-    const bool valid = base + 4 * i + grp < end;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float d = row16_sum(dot8_bf16(t.k[i], qv[h], 0.0f)) * scale_log2;
-      s[h][i] = valid ? d : -INFINITY;
-      pmax[h] = fmaxf(pmax[h], s[h][i]);
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    // lanes of one row agree; combine the 4 rows of the wave
-    pmax[h] = fmaxf(pmax[h], __shfl_xor(pmax[h], 16, kWave));
-    pmax[h] = fmaxf(pmax[h], __shfl_xor(pmax[h], 32, kWave));
-    const float mnew = fmaxf(m[h], pmax[h]);
-    // mnew is finite: row `base` of this pass is valid
-    const float alpha = exp2_fast(m[h] - mnew);
-    m[h] = mnew;
-    l[h] *= alpha;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
-  }
-#pragma unroll
-  for (int i = 0; i < RPL; ++i) {
-    float vf[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t pair = t.v[i][e];
-      vf[2 * e] = lo_bf16(pair);
-      vf[2 * e + 1] = hi_bf16(pair);
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float p = exp2_fast(s[h][i] - m[h]);
-      l[h] += p;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
-    }
-  }
+  for (int p = 0; p < 4; ++p)
+    r[p] = __builtin_amdgcn_perm(vt[2 * p + 1][e >> 1], vt[2 * p][e >> 1], sel);
+  return r;
 }
 
-// WAVES waves per workgroup; PREFETCH: the next pass's loads are issued
-// before the current pass is computed (two tiles of registers per wave).
-template <int RPL, int WAVES, bool PREFETCH>
+template <int WAVES, bool NT>
 __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
     AttnArgs a) {
   constexpr int G = kAttnG, D = kAttnD;
-  constexpr int kWaveRows = 4 * RPL;          // rows per wave per pass
-  constexpr int kPassRows = WAVES * kWaveRows;
+  constexpr int kPassRows = WAVES * kAttnBlock;
   const int split = blockIdx.x;
   const int g = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int grp = lane >> 4;  // row of a load instruction (0..3)
-  const int sub = lane & 15;  // 16-byte piece of the row (dims 8*sub ..)
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
   const int begin = split * a.span;
   const int end = min(begin + a.span, a.len);
 
   __shared__ float s_ml[WAVES][G][2];
   __shared__ float s_acc[WAVES][G][D];
 
-  u32x4 qv[G];
-  {
-    const u32x4 *qg = reinterpret_cast<const u32x4 *>(a.q) + g * G * (D / 8);
+  // q operand of dim chunk c: B[8 g4 + j][c16] = q[head c16][32 c + 8 g4 + j]
+  u32x4 qop[4];
 #pragma unroll
-    for (int h = 0; h < G; ++h) qv[h] = qg[h * (D / 8) + sub];
-  }
-  const uint16_t *kb = a.k + g * a.head_stride + sub * 8;
-  const uint16_t *vb = a.v + g * a.head_stride + sub * 8;
+  for (int c = 0; c < 4; ++c)
+    qop[c] = c16 < G ? *reinterpret_cast<const u32x4 *>(
+                           a.q + (g * G + c16) * D + 32 * c + 8 * g4)
+                     : u32x4{0u, 0u, 0u, 0u};
+  const uint16_t *kb = a.k + g * a.head_stride;
+  const uint16_t *vb = a.v + g * a.head_stride;
+  const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
+  const int last = end - 1;
+  const uint32_t head_mask = c16 < G ? 0xffffffffu : 0u;  // zero P columns
 
-  float m[G], l[G], acc[G][8];
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o[8];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.0f;
+  for (int e = 0; e < 8; ++e) o[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int r0 = begin + wave * kAttnBlock; r0 < end; r0 += kPassRows) {
+    u32x4 kt[2][4];
+    u32x4 vt[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = min(r0 + krow + 4 * hf, last);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kt[hf][c] = kv_load<NT>(kb + static_cast<int64_t>(row) * D + 32 * c +
+                                8 * g4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = min(r0 + 8 * g4 + j, last);
+      vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
+    }
+    f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s0 = mfma_16x16x32_bf16(kt[0][c], qop[c], s0);
+      s1 = mfma_16x16x32_bf16(kt[1][c], qop[c], s1);
+    }
+    // s[j]: row r0 + 8 g4 + j, query head c16
+    float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s[j] = r0 + 8 * g4 + j < end ? s[j] * a.scale_log2 : -INFINITY;
+      bmax = fmaxf(bmax, s[j]);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    // finite: row r0 (lane group 0, j = 0) is valid
+    const float mnew = fmaxf(m, bmax);
+    const float alpha = exp2_fast(m - mnew);
+    m = mnew;
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = exp2_fast(s[j] - mnew);
+      psum += p[j];
+    }
+    l = fmaf(l, alpha, psum);
+    u32x4 pop;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pop[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]) & head_mask;
+    if (alpha != 1.0f) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= alpha;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
   }
 
-  int base = begin + wave * kWaveRows;
-  if constexpr (PREFETCH) {
-    KvTile<RPL> cur;
-    if (base < end) load_tile<RPL>(cur, kb, vb, base, grp, end);
-    for (; base < end; base += kPassRows) {
-      KvTile<RPL> nxt;
-      const int nb = base + kPassRows;
-      if (nb < end) load_tile<RPL>(nxt, kb, vb, nb, grp, end);
-      attend_tile<RPL>(cur, qv, a.scale_log2, base, grp, end, m, l, acc);
-      cur = nxt;
-    }
-  } else {
-    for (; base < end; base += kPassRows) {
-      KvTile<RPL> cur;
-      load_tile<RPL>(cur, kb, vb, base, grp, end);
-      attend_tile<RPL>(cur, qv, a.scale_log2, base, grp, end, m, l, acc);
-    }
-  }
-
-  // Sum the wave's 4 row groups (their maxima already agree).
+  // The four lanes of a head share m; sum their l.
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  if (c16 < G) {
+    // o[e][r] = O[dim 8 (4 g4 + r) + e][head c16]
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    l[h] += __shfl_xor(l[h], 16, kWave);
-    l[h] += __shfl_xor(l[h], 32, kWave);
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      acc[h][e] += __shfl_xor(acc[h][e], 16, kWave);
-      acc[h][e] += __shfl_xor(acc[h][e], 32, kWave);
-    }
-  }
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wave][h][sub * 8 + e] = acc[h][e];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      s_ml[wave][h][0] = m[h];
-      s_ml[wave][h][1] = l[h];
+      for (int e = 0; e < 8; ++e)
+        s_acc[wave][c16][8 * (4 * g4 + r) + e] = o[e][r];
+    if (g4 == 0) {
+      s_ml[wave][c16][0] = m;
+      s_ml[wave][c16][1] = l;
     }
   }
   __syncthreads();
 
-  // Merge the waves; output o = (query head h, dim d).  A wave that saw no
-  // rows has m = -inf, l = 0 and weight 0 (wave 0 always sees one).
-  for (int o = tid; o < G * D; o += WAVES * kWave) {
-    const int h = o / D;
-    const int d = o % D;
+  // Merge the waves; output (query head h, dim d).  A wave that saw no rows
+  // has m = -inf, l = 0, acc = 0 and weight 0 (wave 0 always sees one).
+  for (int o_idx = tid; o_idx < G * D; o_idx += WAVES * kWave) {
+    const int h = o_idx / D;
+    const int d = o_idx % D;
     float mm = -INFINITY;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) mm = fmaxf(mm, s_ml[w][h][0]);
@@ -245,11 +222,11 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
 
 // Merge of the splits, one workgroup per (KV head, query head): lane c of
 // wave 0 reads split c's (m, l), so the maximum and the denominator are
-// wave reductions; then each quarter of the workgroup sums every dim over
-// its quarter of the splits (at most 16 independent loads per thread) and
-// the quarters add up in LDS.  A separate launch (rather than a
-// last-workgroup ticket) lets the kernel boundary publish the partials
-// with one L2 writeback instead of one per workgroup.
+// wave reductions; each quarter of the workgroup sums every dim over its
+// quarter of the splits (at most 16 independent loads per thread, issued
+// before the weights are known) and the quarters add up in LDS.  A separate
+// launch (rather than a last-workgroup ticket) lets the kernel boundary
+// publish the partials with one L2 writeback instead of one per workgroup.
 constexpr int kMergeQuarters = 4;
 constexpr int kMergeThreads = kMergeQuarters * kAttnD;
 constexpr int kMergePerQuarter = kAttnMaxSplits / kMergeQuarters;
@@ -266,8 +243,6 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
   __shared__ float s_part[kMergeQuarters][D];
   __shared__ float s_den;
   const int64_t base = static_cast<int64_t>(g) * a.nsplits * G + h;
-  // The partial sums do not depend on the weights: their loads are issued
-  // first, so they are in flight together with wave 0's (m, l) loads.
   float v[kMergePerQuarter];
 #pragma unroll
   for (int i = 0; i < kMergePerQuarter; ++i) {
@@ -304,12 +279,15 @@ struct AttnShape {
   int64_t nsplits;
 };
 
-// Split policy: kAttnMaxSplits splits per KV head (512 workgroups for 8
-// heads) once the sequence is long enough, spans of at least 16 rows.
+// Split policy: at most kAttnMaxSplits splits per KV head (512 workgroups
+// for 8 heads at long contexts), spans a multiple of the 32-row block.  At
+// context 32769 this gives 61 spans of 544 rows (an MI355X sweep of spans
+// 544 .. 1024 rows and 4 / 8 waves per workgroup put this within 0.5 us of
+// the best).
 static AttnShape attention_shape(int64_t len) {
   AttnShape s;
   int64_t span = (len + kAttnMaxSplits - 1) / kAttnMaxSplits;
-  if (span < 16) span = 16;
+  span = (span + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
   s.span = span;
   s.nsplits = (len + span - 1) / span;
   return s;
@@ -373,7 +351,7 @@ extern "C" int cascade_decode_attention_bf16(
   const dim3 grid(static_cast<unsigned>(shape.nsplits),
                   static_cast<unsigned>(n_kv_heads));
   const hipError_t e =
-      launch_kernel(decode_attention_kernel<4, kAttnWaves, false>, grid,
+      launch_kernel(decode_attention_kernel<kAttnWaves, true>, grid,
                     dim3(kAttnWaves * kWave), 0, s, a);
   if (e != hipSuccess || shape.nsplits == 1) return e;
   return launch_kernel(decode_attention_merge_kernel,

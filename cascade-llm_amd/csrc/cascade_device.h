@@ -14,7 +14,9 @@
 namespace cascade {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
@@ -57,6 +59,23 @@ __device__ __forceinline__ float dot8_bf16(u32x4 a, u32x4 b, float acc) {
                                           false);
   }
   return acc;
+}
+
+// D = A B + C, A 16 x 32 and B 32 x 16 bf16, fp32 D and C
+// (v_mfma_f32_16x16x32_bf16).  Lane l holds A[l % 16][8 (l / 16) + j] and
+// B[8 (l / 16) + j][l % 16] as 8 bf16 (j = 0..7, one register quad) and
+// D[4 (l / 16) + r][l % 16] in register r = 0..3.
+__device__ __forceinline__ f32x4 mfma_16x16x32_bf16(u32x4 a, u32x4 b,
+                                                     f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0,
+      0, 0);
+}
+
+// Two floats rounded to bf16 (round to nearest even), lo in bits 0..15.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) |
+         (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -133,12 +133,18 @@ def test_qkv_rope_split_matrices_equal_fused(gpu_device):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("length", [1, 2, 17, 64, 65, 1000, 2048, 8192, 8193, 32769])
-def test_decode_attention_matches_oracle(gpu_device, length):
-    print("attention length={}".format(length), flush=True)
+@pytest.mark.parametrize("length,q_scale", [
+    (1, 1), (2, 1), (17, 1), (32, 1), (33, 1), (64, 1), (65, 1), (129, 1),
+    (1000, 1), (2048, 1), (2049, 1), (8192, 1), (8193, 1), (32769, 1),
+    # sharp softmax: the running maximum moves between blocks and splits
+    (4097, 8), (32769, 8)])
+def test_decode_attention_matches_oracle(gpu_device, length, q_scale):
+    print("attention length={} q_scale={}".format(length, q_scale), flush=True)
     dev = gpu_device
     dim = 128
     q = cases.normal_bf16((32, 1, dim), 61)
+    if q_scale != 1:
+        q = (q.float() * q_scale).to(BF16)
     k = cases.normal_bf16((8, length, dim), 62)
     v = cases.normal_bf16((8, length, dim), 63)
     capacity = length + 3
@@ -154,7 +160,7 @@ def test_decode_attention_matches_oracle(gpu_device, length):
     expected = ref.attention(q, k, v, length - 1).reshape(-1)
     r = cases.compare(out, expected, atol=1e-2, rtol=1e-2)
     assert r["ok"], r
-    # second call on the same workspace (completion counters were reset)
+    # a second call on the same workspace gives the same bits
     out2 = torch.empty_like(out)
     _hip.decode_attention(q.reshape(-1).to(dev), kc.view(-1), vc.view(-1),
                           capacity * dim, length, out2, ws, dim ** -0.5)
