@@ -11,8 +11,9 @@ inputs already resident in HBM.
 Also reported (extra keys, not ``value``):
   * roofline of the dominant kernel (the fused gate/up SwiGLU GEMV, 224 MiB
     per launch), timed live in the timed region with HIP events bound to
-    each launch of the kernel on its stream (hipExtLaunchKernel start/stop
-    events: kernel execution only), HBM traffic per launch from the
+    launches of the kernel on its stream (hipExtLaunchKernel start/stop
+    events: kernel execution only; one launch per token, layer 16, by
+    default, since a timed launch adds a few microseconds of queue time), HBM traffic per launch from the
     committed FETCH_SIZE / WRITE_SIZE counter summary;
   * streamed: BASELINE config 3 -- full_pinned 16 GB host arena,
     matrix_group units through two 224 MiB slots, streamed vocabulary;
@@ -56,6 +57,10 @@ def parse_args():
     p.add_argument("--streamed-steps", type=int, default=7)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-seconds", type=float, default=15.0)
+    p.add_argument("--roofline-stride", type=int, default=LAYERS,
+                   help="time every N-th gate/up launch of the timed region "
+                        "(default: one per token, layer 16; 1 = all; each "
+                        "timed launch adds ~5 us of queue time)")
     p.add_argument("--probe", action="store_true",
                    help="only run the HBM-counter probe: 4 plain device copies "
                         "of 256 MiB, then 12 gate/up SwiGLU launches over 3 "
@@ -154,7 +159,9 @@ def resident_decode(args):
             state = executor.finish(runtime.run(executor, executor.begin(token)))
             token = state.topk_indices.reshape(1, -1)[:, :1]
         torch.cuda.synchronize(dev)
-        executor.instrument("gate_up", args.steps * LAYERS)
+        stride = args.roofline_stride
+        executor.instrument("gate_up", (args.steps * LAYERS + stride - 1) // stride,
+                            stride=stride, offset=(LAYERS // 2) % stride)
         log("config 4: timing {} decode steps".format(args.steps))
         start = time.perf_counter()
         for _ in range(args.steps):

@@ -441,34 +441,41 @@ class Llama31DecodeExecutor:
             _hip.check("cascade_gemv_residual_bf16", rc)
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
 
-    def instrument(self, name, launches):
-        """Time the next ``launches`` launches of kernel group ``name``
-        ("gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head");
-        read them back with :meth:`kernel_times_ms` after a synchronize.
-        The one-kernel groups (gate_up, qkv, o_proj, down_proj) bind the
-        events to the kernel's own execution; attention (main + split merge)
-        and lm_head (GEMV + two top-k kernels) are bracketed by events
-        recorded on the launching stream, which include dispatch time."""
+    def instrument(self, name, launches, stride=1, offset=0):
+        """Time ``launches`` launches of kernel group ``name`` ("gate_up",
+        "qkv", "attention", "o_proj", "down_proj", "lm_head"): of the group's
+        coming launches, numbers offset, offset + stride, ...; read them back
+        with :meth:`kernel_times_ms` after a synchronize.  The one-kernel
+        groups (gate_up, qkv, o_proj, down_proj) bind the events to the
+        kernel's own execution; attention (main + split merge) and lm_head
+        (GEMV + two top-k kernels) are bracketed by events recorded on the
+        launching stream, which include dispatch time.  A timed launch costs
+        a few microseconds of extra queue time (the timestamp packets), so a
+        stride spreads a few samples over a long run."""
 
+        if int(stride) < 1 or int(offset) < 0:
+            raise ValueError("stride must be >= 1 and offset >= 0")
         self._instrumented[name] = [
             (_hip.HipEvent(enable_timing=True), _hip.HipEvent(enable_timing=True))
             for _ in range(int(launches))
         ]
-        self._instrument_next[name] = 0
+        self._instrument_next[name] = [0, 0, int(stride), int(offset)]
 
     def kernel_times_ms(self, name):
         pairs = self._instrumented.get(name, [])
-        used = self._instrument_next.get(name, 0)
+        used = self._instrument_next[name][0] if pairs else 0
         return [a.elapsed_time(b) for a, b in pairs[:used]]
 
     def _events(self, name):
         pairs = self._instrumented.get(name)
         if not pairs:
             return None
-        index = self._instrument_next[name]
-        if index >= len(pairs):
+        state = self._instrument_next[name]  # [timed, seen, stride, offset]
+        index, seen, stride, offset = state
+        state[1] = seen + 1
+        if index >= len(pairs) or seen < offset or (seen - offset) % stride:
             return None
-        self._instrument_next[name] = index + 1
+        state[0] = index + 1
         return pairs[index]
 
     def _mark_begin(self, name):
