@@ -274,6 +274,142 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Causal GQA prefill attention (the is_causal=True SDPA of the prefill call,
+// layer_streaming/llama31.py:223-229): query token t (cache slot past + t)
+// attends to cache positions [0, past + t].
+//
+// One wave owns one KV head and 4 consecutive query tokens; its 16 MFMA
+// columns are (token t0 + c / 4, query head 4 g + c % 4), so the 4 query
+// heads sharing the KV head reuse every K / V fragment.  The wave walks
+// 32-row blocks from position 0 to its last token's position with the
+// decode kernel's block step (scores S = K_blk Q^T, online softmax in
+// registers, O += V_blk^T P, P rounded to bf16 for the MFMA); positions
+// beyond a column's own limit score -inf.  No split and no merge: a wave
+// finishes its columns and writes them.  Workgroups run the latest tokens
+// (the longest walks) first.
+constexpr int kPrefillTokens = 4;  // query tokens per wave
+
+struct PrefillArgs {
+  const uint16_t *q;  // [tokens, n_q_heads * D]
+  const uint16_t *k;  // position 0 of KV head 0
+  const uint16_t *v;
+  int64_t head_stride;
+  int32_t past;
+  int32_t tokens;
+  int32_t q_row;  // n_q_heads * D
+  int32_t groups;  // ceil(tokens / kPrefillTokens)
+  float scale_log2;
+  uint16_t *out;  // [tokens, n_q_heads * D]
+};
+
+template <bool NT>
+__global__ __launch_bounds__(kAttnWaves *kWave) void prefill_attention_kernel(
+    PrefillArgs a) {
+  constexpr int G = kAttnG, D = kAttnD;
+  const int g = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int group =
+      (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) *
+          kAttnWaves + wave;
+  if (group >= a.groups) return;  // no barriers in this kernel
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int tq = group * kPrefillTokens + (c16 >> 2);
+  const int hq = g * G + (c16 & 3);
+  const int tq_load = min(tq, a.tokens - 1);
+  const int limit = a.past + tq;  // inclusive
+  const int t_last = min(group * kPrefillTokens + kPrefillTokens - 1,
+                         a.tokens - 1);
+  const int end = a.past + t_last + 1;
+  const int last = end - 1;
+
+  u32x4 qop[4];
+  const uint16_t *qrow = a.q + static_cast<int64_t>(tq_load) * a.q_row + hq * D;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    qop[c] = *reinterpret_cast<const u32x4 *>(qrow + 32 * c + 8 * g4);
+  const uint16_t *kb = a.k + g * a.head_stride;
+  const uint16_t *vb = a.v + g * a.head_stride;
+  const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
+
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int r0 = 0; r0 < end; r0 += kAttnBlock) {
+    u32x4 kt[2][4];
+    u32x4 vt[8];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = min(r0 + krow + 4 * hf, last);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kt[hf][c] = kv_load<NT>(kb + static_cast<int64_t>(row) * D + 32 * c +
+                                8 * g4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = min(r0 + 8 * g4 + j, last);
+      vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
+    }
+    f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s0 = mfma_16x16x32_bf16(kt[0][c], qop[c], s0);
+      s1 = mfma_16x16x32_bf16(kt[1][c], qop[c], s1);
+    }
+    // s[j]: position r0 + 8 g4 + j, column c16
+    float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s[j] = r0 + 8 * g4 + j <= limit ? s[j] * a.scale_log2 : -INFINITY;
+      bmax = fmaxf(bmax, s[j]);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    // finite from the first block on: position 0 is valid for every column
+    const float mnew = fmaxf(m, bmax);
+    const float alpha = exp2_fast(m - mnew);
+    m = mnew;
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = exp2_fast(s[j] - mnew);
+      psum += p[j];
+    }
+    l = fmaf(l, alpha, psum);
+    u32x4 pop;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pop[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+    if (alpha != 1.0f) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= alpha;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
+  }
+
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  if (tq >= a.tokens) return;
+  const float inv = 1.0f / l;
+  // o[e][r] = O[dim 8 (4 g4 + r) + e][column c16]
+  uint16_t *orow = a.out + static_cast<int64_t>(tq) * a.q_row + hq * D;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      packed[i] = pack_bf16x2(o[2 * i][r] * inv, o[2 * i + 1][r] * inv);
+    *reinterpret_cast<u32x4 *>(orow + 8 * (4 * g4 + r)) = packed;
+  }
+}
+
 struct AttnShape {
   int64_t span;
   int64_t nsplits;
@@ -357,4 +493,41 @@ extern "C" int cascade_decode_attention_bf16(
   return launch_kernel(decode_attention_merge_kernel,
                        dim3(static_cast<unsigned>(n_kv_heads * kAttnG)),
                        dim3(kMergeThreads), 0, s, a);
+}
+
+extern "C" int cascade_prefill_attention_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, int64_t past, int64_t tokens, int64_t n_q_heads,
+    int64_t n_kv_heads, int64_t head_dim, float scale, void *out,
+    void *stream) {
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
+      out == nullptr)
+    return CASCADE_EINVAL;
+  if (tokens <= 0 || past < 0 || past + tokens > (int64_t{1} << 30) ||
+      n_kv_heads <= 0 || n_kv_heads > 65535)
+    return CASCADE_EINVAL;
+  if (head_dim != kAttnD || n_q_heads != n_kv_heads * kAttnG)
+    return CASCADE_ESHAPE;
+  if (kv_head_stride < (past + tokens) * head_dim) return CASCADE_EINVAL;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) ||
+      !aligned16(out) || (kv_head_stride & 7))
+    return CASCADE_EALIGN;
+  PrefillArgs a{};
+  a.q = static_cast<const uint16_t *>(q);
+  a.k = static_cast<const uint16_t *>(k_cache);
+  a.v = static_cast<const uint16_t *>(v_cache);
+  a.head_stride = kv_head_stride;
+  a.past = static_cast<int32_t>(past);
+  a.tokens = static_cast<int32_t>(tokens);
+  a.q_row = static_cast<int32_t>(n_q_heads * head_dim);
+  a.groups = static_cast<int32_t>((tokens + kPrefillTokens - 1) / kPrefillTokens);
+  a.scale_log2 = scale * kLog2e;
+  a.out = static_cast<uint16_t *>(out);
+  const int64_t blocks = (a.groups + kAttnWaves - 1) / kAttnWaves;
+  const dim3 grid(static_cast<unsigned>(blocks),
+                  static_cast<unsigned>(n_kv_heads));
+  // K / V rows are re-read by every later query token: keep them cached
+  return launch_kernel(prefill_attention_kernel<false>, grid,
+                       dim3(kAttnWaves * kWave), 0,
+                       static_cast<hipStream_t>(stream), a);
 }

@@ -58,6 +58,22 @@ _SIGNATURES = {
         _INT,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P],
     ),
+    "cascade_gemm_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "cascade_gemm_residual_bf16": (
+        _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "cascade_gemm_f32out_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "cascade_gate_up_swiglu_gemm_bf16": (
+        _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "cascade_gate_silu_gemm_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "cascade_up_mul_gemm_bf16": (
+        _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "cascade_qkv_rope_gemm_bf16": (
+        _INT,
+        [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P,
+         _P, _P, _I64, _I64, _P],
+    ),
+    "cascade_prefill_attention_bf16": (
+        _INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P]),
     "cascade_lm_head_workspace_bytes": (_SZ, [_I64, _I64]),
     "cascade_lm_head_topk_bf16": (
         _INT,
@@ -367,6 +383,158 @@ def up_mul(w_up, x, norm_weight, eps, gate, out, stream=None):
     call("cascade_up_mul_bf16", w_up.data_ptr(), n, k, x.data_ptr(),
          0 if norm_weight is None else norm_weight.data_ptr(), float(eps),
          gate.data_ptr(), out.data_ptr(), stream_handle(stream))
+    return out
+
+
+# ------------------------------------------------------ prefill (M > 1)
+
+
+def _rows(x, name, k):
+    """Validate a token-row operand [.., M, K] and return M."""
+
+    _bf16(x, name)
+    if x.numel() % k or x.numel() == 0:
+        raise ValueError("{} is not a whole number of {}-wide rows".format(name, k))
+    return x.numel() // k
+
+
+def gemm(x, weight, out, stream=None):
+    """out[M, N] = bf16(x[M, K] . weight[N, K]^T) on the matrix cores."""
+
+    n, k = _matrix(weight, "weight")
+    m = _rows(x, "x", k)
+    _bf16(out, "out", m * n)
+    call("cascade_gemm_bf16", x.data_ptr(), weight.data_ptr(), out.data_ptr(),
+         m, n, k, stream_handle(stream))
+    return out
+
+
+def gemm_residual(x, weight, residual, out, stream=None):
+    """out = bf16(residual + bf16(x . weight^T)); out may be residual."""
+
+    n, k = _matrix(weight, "weight")
+    m = _rows(x, "x", k)
+    _bf16(residual, "residual", m * n)
+    _bf16(out, "out", m * n)
+    call("cascade_gemm_residual_bf16", x.data_ptr(), weight.data_ptr(),
+         residual.data_ptr(), out.data_ptr(), m, n, k, stream_handle(stream))
+    return out
+
+
+def gemm_f32out(x, weight, out, stream=None):
+    """fp32 out[M, N] = x . weight^T (no rounding; LM-head logits)."""
+
+    n, k = _matrix(weight, "weight")
+    m = _rows(x, "x", k)
+    require_device(out, "out", torch.float32, m * n)
+    call("cascade_gemm_f32out_bf16", x.data_ptr(), weight.data_ptr(),
+         out.data_ptr(), m, n, k, stream_handle(stream))
+    return out
+
+
+def gate_up_swiglu_gemm(x, w_gate, w_up, out, stream=None):
+    n, k = _matrix(w_gate, "w_gate")
+    if tuple(_matrix(w_up, "w_up")) != (n, k):
+        raise ValueError("gate and up matrices differ in shape")
+    m = _rows(x, "x", k)
+    _bf16(out, "out", m * n)
+    call("cascade_gate_up_swiglu_gemm_bf16", x.data_ptr(), w_gate.data_ptr(),
+         w_up.data_ptr(), out.data_ptr(), m, n, k, stream_handle(stream))
+    return out
+
+
+def gate_silu_gemm(x, w_gate, out, stream=None):
+    n, k = _matrix(w_gate, "w_gate")
+    m = _rows(x, "x", k)
+    _bf16(out, "out", m * n)
+    call("cascade_gate_silu_gemm_bf16", x.data_ptr(), w_gate.data_ptr(),
+         out.data_ptr(), m, n, k, stream_handle(stream))
+    return out
+
+
+def up_mul_gemm(x, w_up, gate, out, stream=None):
+    n, k = _matrix(w_up, "w_up")
+    m = _rows(x, "x", k)
+    _bf16(gate, "gate", m * n)
+    _bf16(out, "out", m * n)
+    call("cascade_up_mul_gemm_bf16", x.data_ptr(), w_up.data_ptr(),
+         gate.data_ptr(), out.data_ptr(), m, n, k, stream_handle(stream))
+    return out
+
+
+def _kv_span_ok(buf, name, heads, kv_head_stride, end_slot, head_dim=128):
+    require_device(buf, name, torch.bfloat16, contiguous=False)
+    if kv_head_stride < end_slot * head_dim:
+        raise ValueError("{}: slot {} is outside the head stride".format(
+            name, end_slot - 1))
+    end = buf.storage_offset() + (heads - 1) * kv_head_stride + end_slot * head_dim
+    if end > buf.untyped_storage().nbytes() // 2:
+        raise ValueError("{} cannot hold {} heads up to slot {}".format(
+            name, heads, end_slot))
+
+
+def qkv_rope_gemm(x, wq, wk, wv, rope_cos, rope_sin, pos0, q_out, k_out,
+                  v_out, kv_head_stride, slot0, stream=None):
+    """Q/K/V GEMMs of M token rows + RoPE + KV write.
+
+    rope_cos / rope_sin are whole [positions, 64] bf16 tables; row r uses
+    position pos0 + r and cache slot slot0 + r; k_out / v_out start at
+    position 0 of KV head 0 of the layer's cache.
+    """
+
+    k = None
+    sizes = []
+    for name, w in (("wq", wq), ("wk", wk), ("wv", wv)):
+        if w is None:
+            sizes.append(0)
+            continue
+        n, kk = _matrix(w, name)
+        if k is not None and kk != k:
+            raise ValueError("q/k/v matrices disagree on K")
+        k = kk
+        sizes.append(n)
+    if k is None:
+        raise ValueError("at least one of wq, wk, wv is required")
+    nq, nk, nv = sizes
+    m = _rows(x, "x", k)
+    positions = 0
+    if nq or nk:
+        _bf16(rope_cos, "rope_cos")
+        _bf16(rope_sin, "rope_sin", rope_cos.numel())
+        positions = rope_cos.numel() // 64
+    if nq:
+        _bf16(q_out, "q_out", m * nq)
+    if nk:
+        _kv_span_ok(k_out, "k_out", nk // 128, kv_head_stride, slot0 + m)
+    if nv:
+        _kv_span_ok(v_out, "v_out", nv // 128, kv_head_stride, slot0 + m)
+
+    def ptr(t, used=True):
+        return t.data_ptr() if (used and t is not None) else 0
+
+    call("cascade_qkv_rope_gemm_bf16", x.data_ptr(), m, ptr(wq), ptr(wk),
+         ptr(wv), nq, nk, nv, k, ptr(rope_cos, nq or nk),
+         ptr(rope_sin, nq or nk), positions, int(pos0), ptr(q_out, nq),
+         ptr(k_out, nk), ptr(v_out, nv), int(kv_head_stride), int(slot0),
+         stream_handle(stream))
+
+
+def prefill_attention(q, k_cache, v_cache, kv_head_stride, past, tokens, out,
+                      scale, n_q_heads=32, n_kv_heads=8, head_dim=128,
+                      stream=None):
+    """Causal GQA attention of ``tokens`` query rows at slots past .. past +
+    tokens - 1 over a layer cache (views from position 0 of KV head 0)."""
+
+    width = n_q_heads * head_dim
+    _bf16(q, "q", tokens * width)
+    _bf16(out, "out", tokens * width)
+    for name, buf in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _kv_span_ok(buf, name, n_kv_heads, kv_head_stride, past + tokens,
+                    head_dim)
+    call("cascade_prefill_attention_bf16", q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), int(kv_head_stride), int(past), int(tokens),
+         n_q_heads, n_kv_heads, head_dim, float(scale), out.data_ptr(),
+         stream_handle(stream))
     return out
 
 

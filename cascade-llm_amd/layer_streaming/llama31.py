@@ -19,9 +19,18 @@ Operation -> kernels (reference lines in parentheses):
   down_proj  cascade_gemv_residual_bf16 (:272-279)
   finish     cascade_rmsnorm_bf16 + the LM head (cascade_lm_head_topk_bf16,
       resident head or VocabStreamingRuntime) (:324-349)
-A prefill of S tokens runs the per-token kernels for t = 0..S-1 inside each
-unit; token t attends to positions <= past + t, which is the causal SDPA of
-the reference's prefill (:223-229).
+A call with S > 1 tokens at consecutive positions (every prefill the
+reference makes) runs each matrix once over all S token rows on the matrix
+cores: cascade_rmsnorm_bf16 over the rows, then
+  qkv        cascade_qkv_rope_gemm_bf16 (projections, RoPE, KV write)
+  o_proj     cascade_prefill_attention_bf16 (causal: token t attends to
+      positions <= past + t, the is_causal SDPA of :223-229) then
+      cascade_gemm_residual_bf16
+  gate_up    cascade_gate_up_swiglu_gemm_bf16 (or the silu / mul halves)
+  down_proj  cascade_gemm_residual_bf16
+  finish     (resident head) cascade_gemm_f32out_bf16 for the logits of
+      every position, as the reference's F.linear over [1, S, H]
+Position ids with gaps run the per-token kernels for t = 0..S-1 instead.
 """
 
 from dataclasses import dataclass, field
@@ -189,7 +198,11 @@ _EXPECTED = {
 }
 
 # Kernel groups whose entry point launches exactly one kernel.
-_KERNEL_TIMED_GROUPS = frozenset(("gate_up", "qkv", "o_proj", "down_proj"))
+_KERNEL_TIMED_GROUPS = frozenset((
+    "gate_up", "qkv", "o_proj", "down_proj",
+    # prefill (S > 1 tokens): one MFMA GEMM / attention launch per unit
+    "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_gate", "gemm_up", "gemm_down",
+    "gemm_lm_head", "prefill_attention"))
 
 
 class Llama31DecodeExecutor:
@@ -254,6 +267,15 @@ class Llama31DecodeExecutor:
         self._k_mul = lib.cascade_up_mul_bf16
         self._k_rmsnorm = lib.cascade_rmsnorm_bf16
         self._k_head = lib.cascade_lm_head_topk_bf16
+        self._k_qkv_gemm = lib.cascade_qkv_rope_gemm_bf16
+        self._k_prefill_attn = lib.cascade_prefill_attention_bf16
+        self._k_gemm_residual = lib.cascade_gemm_residual_bf16
+        self._k_swiglu_gemm = lib.cascade_gate_up_swiglu_gemm_bf16
+        self._k_silu_gemm = lib.cascade_gate_silu_gemm_bf16
+        self._k_mul_gemm = lib.cascade_up_mul_gemm_bf16
+        self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
+        self._batched = False
+        self._first_slot = 0
         self._unit_cache = {}
         self._instrumented = {}
         self._instrument_next = {}
@@ -281,6 +303,7 @@ class Llama31DecodeExecutor:
             (tokens, self.config.intermediate_size), dtype=bf16, device=dev)
         self._normed = torch.empty((tokens, self.hidden), dtype=bf16, device=dev)
         self._q_ptr = self._q.data_ptr()
+        self._normed_ptr = self._normed.data_ptr()
         self._attn_ptr = self._attn.data_ptr()
         self._gate_ptr = self._gate_buf.data_ptr()
         self._inter_ptr = self._inter.data_ptr()
@@ -544,6 +567,113 @@ class Llama31DecodeExecutor:
         if self.capture is not None:
             self.capture.append((layer, state.hidden_states.detach().clone()))
 
+    # ------------------------------------------- batched (S > 1) launches
+    # One launch per matrix over all S token rows (MFMA GEMMs).  The
+    # normalised rows are computed by the unit that opens a block (q_proj /
+    # qkv / layer for the input norm, gate_proj / gate_up for the
+    # post-attention norm) and reused by the matrices that follow it, as the
+    # reference reuses layer_values["normalized"] (llama31.py:169-180,
+    # :252-271).
+
+    def _norm_rows(self, state, norm_ptr, stream):
+        rc = self._k_rmsnorm(state.hidden_states.data_ptr(), norm_ptr,
+                             self._normed_ptr, len(state.positions),
+                             self.hidden, self.eps, stream)
+        _hip.check("cascade_rmsnorm_bf16", rc)
+
+    def _qkv_rows(self, layer, ptrs, state, stream):
+        wq = ptrs.get("q_proj", 0)
+        wk = ptrs.get("k_proj", 0)
+        wv = ptrs.get("v_proj", 0)
+        if wq:
+            self._norm_rows(state, self._norm_ptrs[layer][0], stream)
+        nkv = self.n_kv_heads * self.head_dim
+        rope = self.rope
+        ev = self._mark_begin("gemm_qkv")
+        rc = self._k_qkv_gemm(
+            self._normed_ptr, len(state.positions), wq, wk, wv,
+            self.hidden if wq else 0, nkv if wk else 0, nkv if wv else 0,
+            self.hidden, rope.cos.data_ptr(), rope.sin.data_ptr(),
+            rope.capacity, state.positions[0], self._q_ptr if wq else 0,
+            self._kv_pointer(layer, 0, 0) if wk else 0,
+            self._kv_pointer(layer, 1, 0) if wv else 0,
+            self.kv_cache.head_stride, self._first_slot, stream)
+        self._mark_end("gemm_qkv", ev, rc)
+        _hip.check("cascade_qkv_rope_gemm_bf16", rc)
+
+    def _attention_o_rows(self, layer, ptrs, state, stream):
+        tokens = len(state.positions)
+        ev = self._mark_begin("prefill_attention")
+        rc = self._k_prefill_attn(
+            self._q_ptr, self._kv_pointer(layer, 0, 0),
+            self._kv_pointer(layer, 1, 0), self.kv_cache.head_stride,
+            self._first_slot, tokens, self.n_heads, self.n_kv_heads,
+            self.head_dim, self.scale, self._attn_ptr, stream)
+        self._mark_end("prefill_attention", ev, rc)
+        _hip.check("cascade_prefill_attention_bf16", rc)
+        x = state.hidden_states.data_ptr()
+        ev = self._mark_begin("gemm_o")
+        rc = self._k_gemm_residual(self._attn_ptr, ptrs["o_proj"], x, x, tokens,
+                                   self.hidden, self.hidden, stream)
+        self._mark_end("gemm_o", ev, rc)
+        _hip.check("cascade_gemm_residual_bf16", rc)
+        self.kv_cache.set_length(layer, self._first_slot + tokens)
+
+    def _gate_up_rows(self, layer, ptrs, state, stream):
+        tokens = len(state.positions)
+        wg, wu = ptrs.get("gate_proj", 0), ptrs.get("up_proj", 0)
+        if wg:
+            self._norm_rows(state, self._norm_ptrs[layer][1], stream)
+        if wg and wu:
+            ev = self._mark_begin("gemm_gate_up")
+            rc = self._k_swiglu_gemm(self._normed_ptr, wg, wu, self._inter_ptr,
+                                     tokens, self.intermediate, self.hidden,
+                                     stream)
+            self._mark_end("gemm_gate_up", ev, rc)
+            _hip.check("cascade_gate_up_swiglu_gemm_bf16", rc)
+        elif wg:
+            ev = self._mark_begin("gemm_gate")
+            rc = self._k_silu_gemm(self._normed_ptr, wg, self._gate_ptr, tokens,
+                                   self.intermediate, self.hidden, stream)
+            self._mark_end("gemm_gate", ev, rc)
+            _hip.check("cascade_gate_silu_gemm_bf16", rc)
+        else:
+            ev = self._mark_begin("gemm_up")
+            rc = self._k_mul_gemm(self._normed_ptr, wu, self._gate_ptr,
+                                  self._inter_ptr, tokens, self.intermediate,
+                                  self.hidden, stream)
+            self._mark_end("gemm_up", ev, rc)
+            _hip.check("cascade_up_mul_gemm_bf16", rc)
+
+    def _down_rows(self, layer, ptrs, state, stream):
+        x = state.hidden_states.data_ptr()
+        ev = self._mark_begin("gemm_down")
+        rc = self._k_gemm_residual(self._inter_ptr, ptrs["down_proj"], x, x,
+                                   len(state.positions), self.hidden,
+                                   self.intermediate, stream)
+        self._mark_end("gemm_down", ev, rc)
+        _hip.check("cascade_gemm_residual_bf16", rc)
+        if self.capture is not None:
+            self.capture.append((layer, state.hidden_states.detach().clone()))
+
+    def _call_batched(self, layer, op, ptrs, state, stream):
+        if op == "layer":
+            self._qkv_rows(layer, ptrs, state, stream)
+            self._attention_o_rows(layer, ptrs, state, stream)
+            self._gate_up_rows(layer, ptrs, state, stream)
+            self._down_rows(layer, ptrs, state, stream)
+        elif op in ("qkv", "q_proj", "k_proj", "v_proj"):
+            self._qkv_rows(layer, ptrs, state, stream)
+        elif op == "o_proj":
+            self._attention_o_rows(layer, ptrs, state, stream)
+        elif op in ("gate_up", "gate_proj", "up_proj"):
+            self._gate_up_rows(layer, ptrs, state, stream)
+        elif op == "down_proj":
+            self._down_rows(layer, ptrs, state, stream)
+        else:
+            raise ValueError("unknown Llama operation {}".format(op))
+        return state
+
     def __call__(self, unit, weights, state):
         layer = unit.layer_index
         op = unit.operation
@@ -552,6 +682,11 @@ class Llama31DecodeExecutor:
         if layer == 0 and op in ("qkv", "q_proj", "layer"):
             # slot of the first token of this call, fixed for all layers
             self._first_slot = self.kv_cache.sequence_length()
+            positions = state.positions
+            self._batched = len(positions) > 1 and positions == tuple(
+                range(positions[0], positions[0] + len(positions)))
+        if self._batched:
+            return self._call_batched(layer, op, ptrs, state, stream)
         if op == "layer":
             self._qkv(layer, ptrs, state, stream)
             self._attention_o(layer, ptrs, state, stream)
@@ -605,7 +740,18 @@ class Llama31DecodeExecutor:
         values = torch.empty((1, 1, self.top_k), dtype=torch.float32, device=self.device)
         indices = torch.empty((1, 1, self.top_k), dtype=torch.int64, device=self.device)
         ws, ws_bytes = self._head_ws.data_ptr(), self._head_ws.numel()
-        for s in range(count):
+        first = 0
+        if count > 1:
+            # every position's logits in one GEMM (the reference's F.linear
+            # over [1, S, H]); the last row is recomputed below together
+            # with its top-k, so its logits and top-k agree bit for bit
+            ev = self._mark_begin("gemm_lm_head")
+            rc = self._k_f32_gemm(normed.data_ptr(), head_ptr, logits.data_ptr(),
+                                  count, vocab, self.hidden, stream)
+            self._mark_end("gemm_lm_head", ev, rc)
+            _hip.check("cascade_gemm_f32out_bf16", rc)
+            first = count - 1
+        for s in range(first, count):
             ev = self._mark_begin("lm_head")
             rc = self._k_head(head_ptr, vocab, self.hidden, 0,
                               normed.data_ptr() + 2 * self.hidden * s, self.top_k,

@@ -129,6 +129,67 @@ int cascade_decode_attention_bf16(const void *q, const void *k_cache,
                                   float scale, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream);
 
+/* ------------------------------------------------------ prefill (M > 1)
+ * MFMA GEMMs over the token rows of a prefill call: Y[M, N] =
+ * epilogue(X[M, K] . W[N, K]^T), X row-major [M, K] (already normalised:
+ * run cascade_rmsnorm_bf16 over the rows first), W row-major [N, K],
+ * fp32 accumulation, K a multiple of 64, M >= 1, any N >= 1 (the fused
+ * SwiGLU GEMM needs n_half a multiple of 64, the QKV GEMM whole heads).
+ * The epilogues round at the same points as the GEMV family above.  Each
+ * replaces F.linear with a [1, S, K] input, layer_streaming/llama31.py:
+ * 241-279, when the call carries S > 1 tokens.                             */
+int cascade_gemm_bf16(const void *x, const void *w, void *y, int64_t m,
+                      int64_t n, int64_t k, void *stream);
+/* y[M, N] = bf16(residual + bf16(X . W^T)); y may alias residual
+ * (o_proj / down_proj, llama31.py:246-251, :272-279).                      */
+int cascade_gemm_residual_bf16(const void *x, const void *w,
+                               const void *residual, void *y, int64_t m,
+                               int64_t n, int64_t k, void *stream);
+/* fp32 y[M, N] = X . W^T, not rounded: the resident LM head over every
+ * position, F.linear(normalized, lm_head).float() (llama31.py:330-334).    */
+int cascade_gemm_f32out_bf16(const void *x, const void *w, float *y,
+                             int64_t m, int64_t n, int64_t k, void *stream);
+/* y = bf16(bf16(silu(bf16(X . Wg^T))) * bf16(X . Wu^T)), y [M, n_half]
+ * (llama31.py:252-275, gate and up in one unit).                           */
+int cascade_gate_up_swiglu_gemm_bf16(const void *x, const void *w_gate,
+                                     const void *w_up, void *y, int64_t m,
+                                     int64_t n_half, int64_t k, void *stream);
+/* Matrix-granularity halves: y = bf16(silu(bf16(X . Wg^T))) and
+ * y = bf16(gate * bf16(X . Wu^T)).                                         */
+int cascade_gate_silu_gemm_bf16(const void *x, const void *w_gate, void *y,
+                                int64_t m, int64_t n, int64_t k, void *stream);
+int cascade_up_mul_gemm_bf16(const void *x, const void *w_up,
+                             const void *gate, void *y, int64_t m, int64_t n,
+                             int64_t k, void *stream);
+/* Q/K/V projections of M tokens + RoPE + KV-cache write.  Row r is the
+ * token at position pos0 + r (RoPE) and cache slot slot0 + r.  q rows go to
+ * q_out [M, nq]; K / V head h of row r to k_out / v_out + h *
+ * kv_head_stride + (slot0 + r) * 128.  rope_cos / rope_sin are [positions,
+ * 64] bf16 tables with rope_positions rows (pos0 + M <= rope_positions);
+ * kv_head_stride >= (slot0 + M) * 128.  Any of nq, nk, nv may be 0.
+ * Replaces F.linear q/k/v, the rotary embedding and SimpleKVCache.append of
+ * the prefill call (llama31.py:44-50, :206-218, :241-245).                 */
+int cascade_qkv_rope_gemm_bf16(const void *x, int64_t m, const void *wq,
+                               const void *wk, const void *wv, int64_t nq,
+                               int64_t nk, int64_t nv, int64_t k,
+                               const void *rope_cos, const void *rope_sin,
+                               int64_t rope_positions, int64_t pos0,
+                               void *q_out, void *k_out, void *v_out,
+                               int64_t kv_head_stride, int64_t slot0,
+                               void *stream);
+/* Causal GQA attention of `tokens` query rows q [tokens, n_q_heads * 128]:
+ * query row t (cache slot past + t) attends to positions [0, past + t] of
+ * the layer cache (layout as cascade_decode_attention_bf16), out [tokens,
+ * n_q_heads * 128] bf16.  head_dim 128, n_q_heads = 4 n_kv_heads.
+ * Replaces _repeat_kv + F.scaled_dot_product_attention(is_causal=True),
+ * llama31.py:213-229 (the reference's prefill has past = 0).               */
+int cascade_prefill_attention_bf16(const void *q, const void *k_cache,
+                                   const void *v_cache, int64_t kv_head_stride,
+                                   int64_t past, int64_t tokens,
+                                   int64_t n_q_heads, int64_t n_kv_heads,
+                                   int64_t head_dim, float scale, void *out,
+                                   void *stream);
+
 /* ------------------------------------------------------ LM head + top-k
  * One vocabulary chunk: logits[r] = W[r] . h (fp32, not rounded to bf16) for
  * rows r < rows, then an exact running top-k over everything seen since the

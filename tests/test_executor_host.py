@@ -146,6 +146,81 @@ class FakeKernels:
         return 0
 
 
+    # -------------------------------------- batched (S > 1) entry points
+
+    def qkv_gemm(self, x, m, wq, wk, wv, nq, nk, nv, k, cos, sin, positions,
+                 pos0, q_out, k_out, v_out, stride, slot0, stream):
+        self.calls.append("qkv_gemm")
+        n = at(x, m * k).view(m, k)  # rows are already normalised
+        if nq or nk:
+            c = at(cos, positions * 64).view(positions, 64)[pos0:pos0 + m]
+            s = at(sin, positions * 64).view(positions, 64)[pos0:pos0 + m]
+            c, s = torch.cat((c, c), -1), torch.cat((s, s), -1)
+        for w, rows, rope, write in ((wq, nq, True, "q"), (wk, nk, True, "k"),
+                                     (wv, nv, False, "v")):
+            if not rows:
+                continue
+            y = ref.linear(n, at(w, rows * k).view(rows, k))
+            y = y.view(m, rows // 128, 128).transpose(0, 1)
+            if rope:
+                y = ref.apply_rope(y, c, s)
+            if write == "q":
+                at(q_out, m * rows).copy_(y.transpose(0, 1).reshape(-1))
+            else:
+                base = k_out if write == "k" else v_out
+                for h in range(rows // 128):
+                    at(base + 2 * (h * stride + slot0 * 128), m * 128).copy_(
+                        y[h].reshape(-1))
+        return 0
+
+    def prefill_attention(self, q, k0, v0, stride, past, tokens, hq, hkv, dim,
+                          scale, out, stream):
+        self.calls.append("prefill_attention")
+        length = past + tokens
+        keys = torch.stack([at(k0 + 2 * h * stride, length * dim).view(length, dim)
+                            for h in range(hkv)])
+        vals = torch.stack([at(v0 + 2 * h * stride, length * dim).view(length, dim)
+                            for h in range(hkv)])
+        qq = at(q, tokens * hq * dim).view(tokens, hq, dim).transpose(0, 1)
+        at(out, tokens * hq * dim).copy_(
+            ref.attention(qq, keys, vals, past).reshape(-1))
+        return 0
+
+    def gemm_residual(self, x, w, res, y, m, n, k, stream):
+        self.calls.append("gemm_residual")
+        out = at(res, m * n).view(m, n) + ref.linear(at(x, m * k).view(m, k),
+                                                     at(w, n * k).view(n, k))
+        at(y, m * n).copy_(out.reshape(-1))
+        return 0
+
+    def swiglu_gemm(self, x, wg, wu, y, m, n, k, stream):
+        self.calls.append("swiglu_gemm")
+        xx = at(x, m * k).view(m, k)
+        out = F.silu(ref.linear(xx, at(wg, n * k).view(n, k))) * ref.linear(
+            xx, at(wu, n * k).view(n, k))
+        at(y, m * n).copy_(out.reshape(-1))
+        return 0
+
+    def silu_gemm(self, x, wg, y, m, n, k, stream):
+        self.calls.append("silu_gemm")
+        out = F.silu(ref.linear(at(x, m * k).view(m, k), at(wg, n * k).view(n, k)))
+        at(y, m * n).copy_(out.reshape(-1))
+        return 0
+
+    def mul_gemm(self, x, wu, gate, y, m, n, k, stream):
+        self.calls.append("mul_gemm")
+        out = at(gate, m * n).view(m, n) * ref.linear(at(x, m * k).view(m, k),
+                                                      at(wu, n * k).view(n, k))
+        at(y, m * n).copy_(out.reshape(-1))
+        return 0
+
+    def f32_gemm(self, x, w, y, m, n, k, stream):
+        self.calls.append("f32_gemm")
+        out = at(x, m * k).view(m, k).double() @ at(w, n * k).view(n, k).double().t()
+        at(y, m * n, torch.float32).copy_(out.float().reshape(-1))
+        return 0
+
+
 class HostResident:
     """CPU stand-in for ResidentDeviceArena (views into the host store)."""
 
@@ -202,6 +277,10 @@ def make_executor(monkeypatch, plan, store):
     ex._k_qkv, ex._k_attn, ex._k_residual = fakes.qkv, fakes.attention, fakes.residual
     ex._k_swiglu, ex._k_silu, ex._k_mul = fakes.swiglu, fakes.silu, fakes.mul
     ex._k_rmsnorm, ex._k_head = fakes.rmsnorm, fakes.head
+    ex._k_qkv_gemm, ex._k_prefill_attn = fakes.qkv_gemm, fakes.prefill_attention
+    ex._k_gemm_residual, ex._k_swiglu_gemm = fakes.gemm_residual, fakes.swiglu_gemm
+    ex._k_silu_gemm, ex._k_mul_gemm = fakes.silu_gemm, fakes.mul_gemm
+    ex._k_f32_gemm = fakes.f32_gemm
     return ex, fakes
 
 
@@ -245,10 +324,16 @@ def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
         assert torch.equal(k[0], oracle.caches[layer]["k"])
         assert torch.equal(v[0], oracle.caches[layer]["v"])
     per_token = {"matrix_group": 5, "matrix": 8, "layer": 5}[granularity]
-    # per layer and token: qkv launch(es), attention, o residual, MLP, down;
-    # finish: one rmsnorm plus one LM-head launch per position
-    layers = LAYERS * per_token * (len(prompt) + 3)
-    assert len(fakes.calls) == layers + (1 + len(prompt)) + 3 * 2
+    # prefill, per layer: input norm, q/k/v GEMM(s), causal attention,
+    # o GEMM, post-attention norm, MLP GEMM(s), down GEMM
+    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7}[granularity]
+    # decode, per layer and token: qkv launch(es), attention, o residual,
+    # MLP, down; finish: one rmsnorm, then (prefill) one logits GEMM over
+    # every position and one LM-head launch for the last
+    assert fakes.calls.count("prefill_attention") == LAYERS
+    assert fakes.calls.count("f32_gemm") == 1
+    expected = (LAYERS * per_prefill + 3) + 3 * (LAYERS * per_token + 2)
+    assert len(fakes.calls) == expected
 
 
 def test_rope_table_equals_oracle_cos_sin():

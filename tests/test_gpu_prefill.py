@@ -1,0 +1,272 @@
+"""Prefill kernels (S > 1 token rows): the MFMA GEMM family and causal GQA
+attention against the CPU oracle on seeded inputs.
+
+Tolerances: a bf16 GEMM result is a bf16 rounding of an fp32 accumulation,
+so it must lie within one bf16 ulp plus an fp32 accumulation bound of the
+float64 product of the same bf16 operands:
+    |y - exact| <= ulp_bf16(exact) + 2^-22 * sum_k |x_k w_k|
+(the oracle's F.linear is held to the same bound in the same test, so the
+bound pins nothing that a correct CPU restatement would fail); fp32 logits
+within 1e-4 absolute + 1e-4 relative of a float64 product; composed bf16
+results
+(residual, SwiGLU, RoPE, attention) within the north-star bound
+|a - b| <= 2e-2 + 1e-2 |b| (attention: 1e-2 + 1e-2 |b|, as the decode
+kernel's test); integer placement (which KV slots are written) exact.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from layer_streaming import _hip
+from oracle import cases
+from oracle import llama_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+DIM = 128
+
+
+def linear_bound_report(actual, x, w):
+    """Worst ratio of |actual - exact| to ulp_bf16(exact) + 2^-22 sum|x w|."""
+
+    exact = ref.linear_exact(x, w)
+    absdot = x.float().abs() @ w.float().abs().t()
+    mag = exact.abs().clamp_min(1e-30)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    bound = ulp + absdot.double() * 2.0 ** -22
+    ratio = (actual.double().cpu().reshape(exact.shape) - exact).abs() / bound
+    return float(ratio.max())
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (2048, 4096, 4096), (6, 6144, 4096), (130, 1024, 4096), (2, 128, 64),
+    (257, 4096, 14336), (1, 256, 4096), (300, 28672, 4096),
+    (5, 1000, 4096), (129, 200, 128)])
+def test_gemm_matches_oracle(gpu_device, m, n, k):
+    print("gemm m={} n={} k={}".format(m, n, k), flush=True)
+    dev = gpu_device
+    x = cases.normal_bf16((m, k), 101)
+    w = cases.normal_bf16((n, k), 102, 0.02)
+    y = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm(x.to(dev), w.to(dev), y)
+    oracle = ref.linear(x, w)
+    gpu_ratio = linear_bound_report(y, x, w)
+    oracle_ratio = linear_bound_report(oracle, x, w)
+    print("bound ratio gpu {:.3f} oracle {:.3f}".format(gpu_ratio, oracle_ratio),
+          flush=True)
+    assert oracle_ratio <= 1.0
+    assert gpu_ratio <= 1.0
+    # and against the oracle itself
+    r = cases.compare(y, oracle)
+    assert r["ok"], r
+
+
+def test_gemm_f32out_matches_float64(gpu_device):
+    dev = gpu_device
+    m, n, k = 37, 128256 // 8, 4096
+    x = cases.normal_bf16((m, k), 103)
+    w = cases.normal_bf16((n, k), 104, 0.02)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _hip.gemm_f32out(x.to(dev), w.to(dev), y)
+    expected = ref.linear_exact(x, w).float()
+    r = cases.compare(y, expected, atol=1e-4, rtol=1e-4)
+    assert r["ok"], r
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (6, 4096, 14336),
+                                   (129, 4096, 14336)])
+def test_gemm_residual_matches_oracle(gpu_device, m, n, k):
+    dev = gpu_device
+    x = cases.normal_bf16((m, k), 111)
+    w = cases.normal_bf16((n, k), 112, 0.02)
+    res = cases.normal_bf16((m, n), 113)
+    y = res.to(dev)  # in place, as the executor uses it
+    _hip.gemm_residual(x.to(dev), w.to(dev), y, y)
+    expected = res + ref.linear(x, w)
+    r = cases.compare(y, expected)
+    assert r["ok"], r
+    # W = I: y = bf16(res + x) exactly, torch's bf16 add
+    eye = torch.eye(n, dtype=BF16, device=dev)
+    xs = cases.normal_bf16((m, n), 114, 3.0)
+    out = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm_residual(xs.to(dev), eye, res.to(dev), out)
+    assert torch.equal(out.cpu(), res + xs)
+
+
+@pytest.mark.parametrize("m", [2, 6, 200, 700])
+def test_swiglu_gemm_fused_and_split_match_oracle(gpu_device, m):
+    dev = gpu_device
+    inter, hidden = 14336, 4096
+    x = cases.normal_bf16((m, hidden), 121)
+    wg = cases.normal_bf16((inter, hidden), 122, 0.02)
+    wu = cases.normal_bf16((inter, hidden), 123, 0.02)
+    gate = F.silu(ref.linear(x, wg))
+    expected = gate * ref.linear(x, wu)
+    xd, wgd, wud = x.to(dev), wg.to(dev), wu.to(dev)
+    fused = torch.empty((m, inter), dtype=BF16, device=dev)
+    _hip.gate_up_swiglu_gemm(xd, wgd, wud, fused)
+    r = cases.compare(fused, expected)
+    assert r["ok"], r
+    g = torch.empty((m, inter), dtype=BF16, device=dev)
+    split = torch.empty((m, inter), dtype=BF16, device=dev)
+    _hip.gate_silu_gemm(xd, wgd, g)
+    _hip.up_mul_gemm(xd, wud, g, split)
+    r = cases.compare(g, gate)
+    assert r["ok"], r
+    assert torch.equal(fused.cpu(), split.cpu())
+
+
+def _rope_tables(positions):
+    inv = ref.llama3_inv_freq(DIM)
+    cos, sin = ref.rope_cos_sin(inv, list(range(positions)))
+    return cos[:, :64].contiguous(), sin[:, :64].contiguous()
+
+
+@pytest.mark.parametrize("m,pos0", [(6, 0), (2048, 0), (33, 4000), (2, 32766)])
+def test_qkv_rope_gemm_matches_oracle(gpu_device, m, pos0):
+    print("qkv_rope_gemm m={} pos0={}".format(m, pos0), flush=True)
+    dev = gpu_device
+    hidden, kv = 4096, 1024
+    x = cases.normal_bf16((m, hidden), 131)
+    wq = cases.normal_bf16((hidden, hidden), 132, 0.02)
+    wk = cases.normal_bf16((kv, hidden), 133, 0.02)
+    wv = cases.normal_bf16((kv, hidden), 134, 0.02)
+    table_cos, table_sin = _rope_tables(pos0 + m + 5)
+    slot0 = 3  # cache slots are not positions: a different offset on purpose
+    capacity = slot0 + m + 7
+    kc = torch.zeros((8, capacity, DIM), dtype=BF16, device=dev)
+    vc = torch.zeros_like(kc)
+    q = torch.empty((m, hidden), dtype=BF16, device=dev)
+    _hip.qkv_rope_gemm(x.to(dev), wq.to(dev), wk.to(dev), wv.to(dev),
+                       table_cos.to(dev), table_sin.to(dev), pos0, q,
+                       kc.view(-1), vc.view(-1), capacity * DIM, slot0)
+    cos, sin = ref.rope_cos_sin(ref.llama3_inv_freq(DIM),
+                                list(range(pos0, pos0 + m)))
+    eq = ref.apply_rope(ref.linear(x, wq).view(m, 32, DIM).transpose(0, 1), cos, sin)
+    ek = ref.apply_rope(ref.linear(x, wk).view(m, 8, DIM).transpose(0, 1), cos, sin)
+    ev = ref.linear(x, wv).view(m, 8, DIM).transpose(0, 1)
+    kcpu, vcpu = kc.cpu(), vc.cpu()
+    for got, exp in ((q.cpu(), eq.transpose(0, 1).reshape(m, -1)),
+                     (kcpu[:, slot0:slot0 + m], ek), (vcpu[:, slot0:slot0 + m], ev)):
+        r = cases.compare(got, exp)
+        assert r["ok"], r
+    # only slots slot0 .. slot0 + m - 1 were written
+    for buf in (kcpu, vcpu):
+        assert int(buf[:, :slot0].abs().sum()) == 0
+        assert int(buf[:, slot0 + m:].abs().sum()) == 0
+
+
+def test_qkv_rope_gemm_split_matrices_equal_fused(gpu_device):
+    # matrix granularity: q, k, v in three launches == one fused launch
+    dev = gpu_device
+    m, hidden, kv = 70, 4096, 1024
+    x = cases.normal_bf16((m, hidden), 141).to(dev)
+    wq = cases.normal_bf16((hidden, hidden), 142, 0.02).to(dev)
+    wk = cases.normal_bf16((kv, hidden), 143, 0.02).to(dev)
+    wv = cases.normal_bf16((kv, hidden), 144, 0.02).to(dev)
+    c, s = (t.to(dev) for t in _rope_tables(m + 10))
+    outs = []
+    for split in (False, True):
+        kc = torch.zeros((8, 128, DIM), dtype=BF16, device=dev)
+        vc = torch.zeros_like(kc)
+        q = torch.zeros((m, hidden), dtype=BF16, device=dev)
+        args = (c, s, 10)
+        if split:
+            _hip.qkv_rope_gemm(x, wq, None, None, *args, q, None, None, 128 * DIM, 5)
+            _hip.qkv_rope_gemm(x, None, wk, None, *args, None, kc.view(-1), None,
+                               128 * DIM, 5)
+            _hip.qkv_rope_gemm(x, None, None, wv, *args, None, None, vc.view(-1),
+                               128 * DIM, 5)
+        else:
+            _hip.qkv_rope_gemm(x, wq, wk, wv, *args, q, kc.view(-1), vc.view(-1),
+                               128 * DIM, 5)
+        outs.append((q.cpu(), kc.cpu(), vc.cpu()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_gemm_row_matches_gemv_rounding(gpu_device):
+    # one token through the GEMM and through the GEMV: both are valid fp32
+    # summation orders of the same bf16 products, so they agree to 1 ulp
+    dev = gpu_device
+    x = cases.normal_bf16((1, 4096), 151).to(dev)
+    w = cases.normal_bf16((4096, 4096), 152, 0.02).to(dev)
+    a = torch.empty((1, 4096), dtype=BF16, device=dev)
+    b = torch.empty(4096, dtype=BF16, device=dev)
+    _hip.gemm(x, w, a)
+    _hip.gemv(w, x.reshape(-1), b)
+    xc, wc = x.cpu(), w.cpu()
+    assert linear_bound_report(a, xc, wc) <= 1.0
+    assert linear_bound_report(b.reshape(1, -1), xc, wc) <= 1.0
+
+
+@pytest.mark.parametrize("past,tokens,q_scale", [
+    (0, 1, 1), (0, 2, 1), (0, 5, 1), (0, 33, 1), (0, 130, 1), (0, 2048, 1),
+    (0, 2048, 8), (100, 7, 1), (4000, 45, 4)])
+def test_prefill_attention_matches_oracle(gpu_device, past, tokens, q_scale):
+    print("prefill attention past={} tokens={} q_scale={}".format(
+        past, tokens, q_scale), flush=True)
+    dev = gpu_device
+    length = past + tokens
+    q = cases.normal_bf16((32, tokens, DIM), 161)
+    if q_scale != 1:
+        q = (q.float() * q_scale).to(BF16)
+    k = cases.normal_bf16((8, length, DIM), 162)
+    v = cases.normal_bf16((8, length, DIM), 163)
+    capacity = length + 9
+    kc = torch.zeros((8, capacity, DIM), dtype=BF16, device=dev)
+    vc = torch.zeros_like(kc)
+    kc[:, :length].copy_(k.to(dev))
+    vc[:, :length].copy_(v.to(dev))
+    qrows = q.transpose(0, 1).reshape(tokens, 32 * DIM).contiguous()
+    out = torch.empty((tokens, 32 * DIM), dtype=BF16, device=dev)
+    _hip.prefill_attention(qrows.to(dev), kc.view(-1), vc.view(-1),
+                           capacity * DIM, past, tokens, out, DIM ** -0.5)
+    expected = ref.attention(q, k, v, past)
+    r = cases.compare(out, expected, atol=1e-2, rtol=1e-2)
+    assert r["ok"], r
+
+
+def test_prefill_attention_first_token_is_value_row(gpu_device):
+    # token 0 of a prefill sees position 0 only: its output is V[0] exactly
+    dev = gpu_device
+    tokens = 40
+    q = cases.normal_bf16((tokens, 32 * DIM), 171).to(dev)
+    kc = cases.normal_bf16((8, tokens, DIM), 172).to(dev)
+    vc = cases.normal_bf16((8, tokens, DIM), 173).to(dev)
+    out = torch.empty((tokens, 32 * DIM), dtype=BF16, device=dev)
+    _hip.prefill_attention(q, kc.view(-1), vc.view(-1), tokens * DIM, 0, tokens,
+                           out, DIM ** -0.5)
+    expected = vc[:, 0].repeat_interleave(4, dim=0).reshape(-1)
+    assert torch.equal(out[0].cpu(), expected.cpu())
+
+
+def test_prefill_argument_errors_raise(gpu_device):
+    dev = gpu_device
+    x = torch.zeros((4, 4096), dtype=BF16, device=dev)
+    w = torch.zeros((128, 4000), dtype=BF16, device=dev)  # K not a multiple of 64
+    y = torch.zeros((4, 128), dtype=BF16, device=dev)
+    with pytest.raises(_hip.HipCallError):
+        _hip.gemm(torch.zeros((4, 4000), dtype=BF16, device=dev), w, y)
+    with pytest.raises(_hip.HipCallError):  # n_half not a multiple of 64
+        wg = torch.zeros((100, 4096), dtype=BF16, device=dev)
+        _hip.gate_up_swiglu_gemm(x, wg, wg, torch.zeros((4, 100), dtype=BF16,
+                                                        device=dev))
+    w = torch.zeros((128, 4096), dtype=BF16, device=dev)
+    y = torch.zeros((4, 128), dtype=BF16, device=dev)
+    with pytest.raises(ValueError):
+        _hip.gemm(x.cpu(), w, y)  # host tensor never reaches a kernel
+    # a RoPE table too short for the rows: rejected before any launch
+    c = torch.zeros((3, 64), dtype=BF16, device=dev)
+    kc = torch.zeros((8, 16, DIM), dtype=BF16, device=dev)
+    q = torch.zeros((4, 4096), dtype=BF16, device=dev)
+    wq = torch.zeros((4096, 4096), dtype=BF16, device=dev)
+    with pytest.raises(_hip.HipCallError):
+        _hip.qkv_rope_gemm(x, wq, None, None, c, c, 0, q, None, None, 16 * DIM, 0)
+    # KV slots beyond the head stride: rejected
+    wk = torch.zeros((1024, 4096), dtype=BF16, device=dev)
+    with pytest.raises(ValueError):
+        _hip.qkv_rope_gemm(x, None, wk, None, c, c, 0, None, kc.view(-1), None,
+                           16 * DIM, 14)
