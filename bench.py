@@ -18,6 +18,12 @@ Also reported (extra keys, not ``value``):
   * streamed: BASELINE config 3 -- full_pinned 16 GB host arena,
     matrix_group units through two 224 MiB slots, streamed vocabulary;
     decode ms/token and the PCIe-inclusive H2D GB/s (skip: --no-streamed);
+  * prefill: BASELINE config 5 -- a 2048-token random-ID prompt through the
+    pinned_staging store with matrix granularity and the streamed
+    vocabulary (pageable arena -> pinned staging slots -> two 128 MiB device
+    slots), prefill ms and H2D GB/s, and every prefill GEMM / attention
+    launch of the timed run bound to HIP events: per-matrix TFLOP/s and the
+    fraction of the bf16 dense MFMA peak (skip: --no-prefill);
   * cpu_baseline: the CPU oracle on this host's cores on a bounded sample
     (skip: --no-cpu-baseline).
 
@@ -37,6 +43,7 @@ sys.path.insert(0, str(ROOT / "cascade-llm_amd"))
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, vendor peak
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, vendor figure
 PCIE_PEAK_GBPS = 63.0   # PCIe Gen5 x16 per direction, vendor figure
 HIDDEN, INTER, VOCAB, LAYERS = 4096, 14336, 128256, 32
 KV_BYTES_PER_POS_LAYER = 2 * 8 * 128 * 2
@@ -55,6 +62,9 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-streamed", action="store_true")
     p.add_argument("--streamed-steps", type=int, default=7)
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--prefill-tokens", type=int, default=2048)
+    p.add_argument("--prefill-repeats", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-seconds", type=float, default=15.0)
     p.add_argument("--roofline-stride", type=int, default=LAYERS,
@@ -255,6 +265,120 @@ def streamed_decode(args):
     return result
 
 
+# Prefill launch groups of the matrix granularity and their [N, K] shapes.
+# The q / k / v projections share the "gemm_qkv" group (launch order q, k, v
+# in every layer).
+PREFILL_GEMMS = (
+    ("q_proj", "gemm_qkv", 0, (HIDDEN, HIDDEN)),
+    ("k_proj", "gemm_qkv", 1, (1024, HIDDEN)),
+    ("v_proj", "gemm_qkv", 2, (1024, HIDDEN)),
+    ("o_proj", "gemm_o", None, (HIDDEN, HIDDEN)),
+    ("gate_proj", "gemm_gate", None, (INTER, HIDDEN)),
+    ("up_proj", "gemm_up", None, (INTER, HIDDEN)),
+    ("down_proj", "gemm_down", None, (HIDDEN, INTER)),
+)
+
+
+def prefill_streamed(args):
+    """one 2048-token prefill in pinned_staging mode."""
+
+    import torch
+    from layer_streaming import (
+        DoubleBufferRuntime,
+        Llama31Config,
+        Llama31DecodeExecutor,
+        ResidentDeviceArena,
+        VocabStreamingRuntime,
+        build_llama31_8b_plan,
+        create_weight_store,
+    )
+
+    dev = torch.device("cuda:0")
+    tokens = args.prefill_tokens
+    plan = build_llama31_8b_plan("matrix", stream_vocab=True)
+    log("config 5: pageable {:.1f} GB arena, {} MiB slots".format(
+        plan.host_arena_bytes / 1e9, plan.slot_bytes >> 20))
+    store = create_weight_store(plan, "pinned_staging")
+    store.fill_random(seed=args.seed, device=dev)
+    resident = ResidentDeviceArena(plan, store, dev)
+    runtime = DoubleBufferRuntime(plan, store, resident, dev, profile=True)
+    vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
+    executor = Llama31DecodeExecutor(Llama31Config(), resident, vocab_runtime=vocab,
+                                     top_k=10)
+    executor.reserve(tokens + 1)
+    gen = torch.Generator().manual_seed(args.seed + 1)
+    prompt = torch.randint(0, VOCAB, (1, tokens), generator=gen).to(dev)
+    walls, profiles, staging = [], [], []
+    groups = {"gemm_qkv": 3 * LAYERS, "gemm_o": LAYERS, "gemm_gate": LAYERS,
+              "gemm_up": LAYERS, "gemm_down": LAYERS,
+              "prefill_attention": LAYERS}
+    repeats = args.prefill_repeats
+    with torch.inference_mode():
+        for rep in range(1 + repeats):
+            executor.kv_cache.clear()
+            if rep == repeats:
+                for name, count in groups.items():
+                    executor.instrument(name, count)
+            torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            state = executor.finish(runtime.run(executor, executor.begin(prompt)))
+            torch.cuda.synchronize(dev)
+            wall = (time.perf_counter() - t0) * 1000.0
+            log("config 5: prefill {} {:.1f} ms".format(rep, wall))
+            if rep == 0:
+                continue  # warm-up
+            walls.append(wall)
+            profiles.append(runtime.last_profile)
+    times = {name: executor.kernel_times_ms(name) for name in groups}
+    gemms = {}
+    total_ms = 0.0
+    for name, group, phase, (n, k) in PREFILL_GEMMS:
+        ms = times[group]
+        if phase is not None:
+            ms = ms[phase::3]
+        avg = statistics.mean(ms)
+        total_ms += sum(ms)
+        tflops = 2.0 * tokens * n * k / (avg * 1e-3) / 1e12
+        gemms[name] = {"m_n_k": [tokens, n, k], "avg_us": round(1000 * avg, 1),
+                       "tflops": round(tflops, 1),
+                       "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    attn = times["prefill_attention"]
+    attn_flops = 4.0 * 32 * 128 * tokens * (tokens + 1) / 2
+    attn_tflops = attn_flops / (statistics.mean(attn) * 1e-3) / 1e12
+    bytes_prefill = plan.stream_bytes_per_token + VOCAB * HIDDEN * 2
+    median = statistics.median(walls)
+    result = {
+        "workload": "BASELINE config 5: {}-token random-ID prompt, pinned_staging "
+                    "(pageable arena + pinned staging slots), matrix granularity, "
+                    "2 x {} MiB device slots, streamed vocab; 1 warm-up + {} "
+                    "prefills".format(tokens, plan.slot_bytes >> 20, repeats),
+        "prefill_ms_median": round(median, 2),
+        "prefill_ms_min": round(min(walls), 2),
+        "prompt_tokens_per_s": round(tokens / (median / 1e3), 1),
+        "h2d_bytes": bytes_prefill,
+        "pcie_inclusive_gbps": round(bytes_prefill / 1e9 / (median / 1e3), 2),
+        "transformer_h2d_gbps_median": round(statistics.median(
+            p["h2d_effective_gbps"] for p in profiles), 2),
+        "transformer_compute_event_sum_ms": round(statistics.median(
+            p["compute_event_sum_ms"] for p in profiles), 2),
+        "staging_copy_sum_ms": round(statistics.median(
+            p.get("staging_event_sum_ms", 0.0) for p in profiles), 1),
+        "gemm": gemms,
+        "gemm_sum_ms": round(total_ms, 2),
+        "gemm_tflops": round(2.0 * tokens * 218103808 * LAYERS / (total_ms * 1e-3)
+                             / 1e12, 1),
+        "attention": {"avg_us": round(1000 * statistics.mean(attn), 1),
+                      "tflops": round(attn_tflops, 1),
+                      "mfma_frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+        "last_token": int(state.topk_indices.reshape(-1)[0]),
+    }
+    store.close()
+    del executor, vocab, runtime, resident, store
+    torch.cuda.empty_cache()
+    return result
+
+
 def cpu_baseline(args):
     """The CPU oracle on this host: one decode token at context 32768 is
     timed as (32 x one decoder layer) + the full LM head, on a bounded
@@ -378,6 +502,8 @@ def main():
             **{k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()},
             "pcie_peak_gbps": PCIE_PEAK_GBPS,
         }
+    if not args.no_prefill:
+        line["prefill"] = prefill_streamed(args)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(line), flush=True)

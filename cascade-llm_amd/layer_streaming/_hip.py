@@ -90,6 +90,7 @@ _SIGNATURES = {
     "cascade_event_synchronize": (_INT, [_U64]),
     "cascade_event_query": (_INT, [_U64]),
     "cascade_event_elapsed_ms": (_INT, [_U64, _U64, ctypes.POINTER(_F)]),
+    "cascade_host_copy": (_INT, [_P, _P, _SZ, _INT]),
     "cascade_hbm_read": (_INT, [_P, _SZ, _P, _P]),
     "cascade_device_copy": (_INT, [_P, _P, _SZ, _P]),
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
@@ -641,6 +642,34 @@ def memcpy_h2d_async(dst, src, nbytes, stream):
         raise ValueError("copy larger than the destination")
     call("cascade_memcpy_h2d_async", dst.data_ptr(), src.data_ptr(),
          int(nbytes), stream_handle(stream))
+
+
+def default_copy_threads():
+    """Threads for host staging copies: this process's CPUs, at most 16."""
+
+    try:
+        cpus = len(os.sched_getaffinity(0))
+    except AttributeError:  # not Linux
+        cpus = os.cpu_count() or 1
+    return max(1, min(16, cpus))
+
+
+def host_copy(dst, src, threads=None):
+    """dst.copy_(src) for contiguous host tensors of equal byte size, with
+    the library's multi-threaded non-temporal memcpy (the GIL is released
+    for the duration of the copy)."""
+
+    for name, t in (("dst", dst), ("src", src)):
+        if not isinstance(t, torch.Tensor) or t.device.type != "cpu":
+            raise ValueError("{} must be a host tensor".format(name))
+        if not t.is_contiguous():
+            raise ValueError("{} must be contiguous".format(name))
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("host_copy needs equal byte sizes")
+    call("cascade_host_copy", dst.data_ptr(), src.data_ptr(), nbytes,
+         int(threads or default_copy_threads()))
+    return dst
 
 
 class HipEvent:

@@ -138,7 +138,7 @@ class VocabStreamingRuntime:
         if ready_event is not None:
             ready_event.synchronize()
         target = self.head_staging_slots[slot_index][: source.numel()]
-        target.copy_(source)
+        _hip.host_copy(target, source, getattr(self.store, "copy_threads", None))
         return target
 
     def _workspace(self, top_k):

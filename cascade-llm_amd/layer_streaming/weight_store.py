@@ -7,7 +7,9 @@ API and behaviour follow the reference (layer_streaming/weight_store.py):
 * ``PinnedStagingWeightStore`` keeps a pageable arena plus ``slot_count``
   page-locked staging slots filled by worker threads; a worker first waits on
   ``reuse_event`` (the H2D copy that last read its slot) and then copies the
-  unit in (:209-298).
+  unit in (:209-298) with the library's multi-threaded non-temporal memcpy
+  (``cascade_host_copy``; ``copy_threads`` threads, default this process's
+  CPUs up to 16) instead of one tensor copy.
 * ``load_checkpoint`` fills the arena from a local safetensors file or
   sharded index with key and shape checks (:20-38, :109-171).
 * ``tensor_factory`` is injectable for tests (:55).
@@ -25,6 +27,7 @@ import time
 
 import torch
 
+from . import _hip
 from .plan import ModelPlan
 
 __all__ = [
@@ -266,9 +269,11 @@ class FullPinnedWeightStore(BaseWeightStore):
 class PinnedStagingWeightStore(BaseWeightStore):
     """Pageable full store plus reusable page-locked staging slots."""
 
-    def __init__(self, plan, allocate=True, tensor_factory=None, worker_count=2):
+    def __init__(self, plan, allocate=True, tensor_factory=None, worker_count=2,
+                 copy_threads=None):
         self.staging_slots = None
         self.worker_count = int(worker_count)
+        self.copy_threads = int(copy_threads or _hip.default_copy_threads())
         self._executor = None
         self._profile_lock = threading.Lock()
         self._stage_durations_ms = []
@@ -307,7 +312,7 @@ class PinnedStagingWeightStore(BaseWeightStore):
             # The slot is free once the H2D copy that last read it is done.
             reuse_event.synchronize()
         target = self.staging_slots[slot_index][: unit.elements]
-        target.copy_(self.unit_source(unit))
+        _hip.host_copy(target, self.unit_source(unit), self.copy_threads)
         elapsed = (time.perf_counter() - started) * 1000.0
         with self._profile_lock:
             self._stage_durations_ms.append(elapsed)

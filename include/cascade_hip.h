@@ -241,6 +241,15 @@ int cascade_event_synchronize(uint64_t event);
 int cascade_event_query(uint64_t event);
 int cascade_event_elapsed_ms(uint64_t start, uint64_t end, float *ms);
 
+/* Host memcpy of `bytes` from src to dst (non-overlapping host memory)
+ * with `threads` threads (1..64: the caller plus a persistent pool), 2 MiB
+ * pieces, non-temporal stores; returns when the copy is complete.  Calls
+ * from several threads are serialised.  No HIP call is made.
+ * Replaces the pageable -> pinned staging copy of PinnedStagingWeightStore
+ * (layer_streaming/weight_store.py:258-268) and of the streamed LM head
+ * (layer_streaming/vocab.py:143-147).                                      */
+int cascade_host_copy(void *dst, const void *src, size_t bytes, int threads);
+
 /* ----------------------------------------------------------- measurement
  * Streaming-read kernel: sums `bytes` of device memory (16-byte loads) into
  * *sink; used to measure achievable HBM read bandwidth (no reference
