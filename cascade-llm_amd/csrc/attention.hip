@@ -118,9 +118,8 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int r0 = begin + wave * kAttnBlock; r0 < end; r0 += kPassRows) {
-    u32x4 kt[2][4];
-    u32x4 vt[8];
+  // K rows of the block as two MFMA halves, V rows as 8 whole rows per lane
+  auto load_block = [&](int r0, u32x4 (&kt)[2][4], u32x4 (&vt)[8]) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int row = min(r0 + krow + 4 * hf, last);
@@ -134,6 +133,9 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
       const int row = min(r0 + 8 * g4 + j, last);
       vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
     }
+  };
+
+  auto block_step = [&](int r0, const u32x4 (&kt)[2][4], const u32x4 (&vt)[8]) {
     f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -172,6 +174,13 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
+  };
+
+  for (int r0 = begin + wave * kAttnBlock; r0 < end; r0 += kPassRows) {
+    u32x4 kt[2][4];
+    u32x4 vt[8];
+    load_block(r0, kt, vt);
+    block_step(r0, kt, vt);
   }
 
   // The four lanes of a head share m; sum their l.

@@ -314,15 +314,22 @@ static hipError_t launch_gemv(const GemvArgs &a, hipStream_t stream) {
                        dim3(WAVES * kWave), lds, stream, a);
 }
 
-// Launch shapes, from an MI355X sweep of one-shot grids with rotating weight
-// copies (so no launch is served by the 256 MB MALL): K = 4096 rows are
-// 8 KiB (8 loads per lane), K = 14336 rows 28 KiB (28 loads per lane, one
-// row per wave); 8 waves per workgroup except for the fused gate/up tile
-// and the LM head; nontemporal weight loads everywhere (every weight byte
-// is read once per token).  Other K use the looped kernel.
+// Launch shapes, from MI355X sweeps of back-to-back launches over rotating
+// weight copies (so no launch is served by the 256 MB MALL).  K = 4096 rows
+// are 8 KiB (8 loads per lane), K = 14336 rows 28 KiB (28 loads per lane).
+// Where a matrix is only one workgroup deep per CU, the grid is sized to
+// exactly 256 workgroups -- one per CU, so no CU reads twice the share of
+// another: q|k|v (6144 rows) as 12 waves x 2 rows, o_proj and down_proj
+// (4096 rows) as 16 waves x 1 row.  Deep grids: gate/up (3584 workgroups)
+// uses 4 waves x 2 rows, the LM head 2 waves x 1 row (64128 workgroups,
+// launch_logits_gemv); everything else 8 waves x 2 rows.
+// Nontemporal weight loads everywhere (every weight byte is read once per
+// token).  Other K use the looped kernel.
 template <int EPI>
 struct GemvShape {
-  static constexpr int WAVES = (EPI == kSwiglu || EPI == kLogits) ? 4 : 8;
+  static constexpr int WAVES = (EPI == kSwiglu || EPI == kLogits) ? 4
+                               : EPI == kQkvRope                 ? 12
+                                                                 : 8;
   static constexpr bool NT = true;
 };
 
@@ -330,6 +337,17 @@ template <int R, int EPI>
 static hipError_t dispatch_gemv(const GemvArgs &a, hipStream_t stream) {
   constexpr int W = GemvShape<EPI>::WAVES;
   constexpr bool NT = GemvShape<EPI>::NT;
+  if constexpr (R == 1 && EPI == kResidual) {
+    // o_proj / down_proj: 4096 rows -> 256 workgroups of 16 rows, as 16
+    // one-row waves (K = 4096) or 8 two-row waves (K = 14336: 56 loads per
+    // lane in flight, within the register file at 2 waves per SIMD)
+    if (a.k == 4096) return launch_gemv<8, 1, 16, EPI, NT>(a, stream);
+    if (a.k == 14336) {
+      GemvArgs b = a;
+      b.n_tiles = (a.n0 + 1) / 2;
+      return launch_gemv<28, 2, 8, EPI, NT>(b, stream);
+    }
+  }
   if (a.k == 4096) return launch_gemv<8, R, W, EPI, NT>(a, stream);
   if constexpr (R == 1) {
     if (a.k == 14336) return launch_gemv<28, 1, 8, EPI, NT>(a, stream);
@@ -353,6 +371,12 @@ hipError_t launch_logits_gemv(const uint16_t *w, int64_t rows, int64_t k,
   a.k = k;
   a.x = h;
   a.yf = logits;
+  if (k == 4096) {
+    // one row per wave, two waves per workgroup: 7.4 TB/s over the 1 GB
+    // head on MI355X (2 rows x 4 waves: 6.8 TB/s)
+    a.n_tiles = rows;
+    return launch_gemv<8, 1, 2, kLogits, true>(a, stream);
+  }
   a.n_tiles = (rows + 1) / 2;
   return dispatch_gemv<2, kLogits>(a, stream);
 }
@@ -388,10 +412,6 @@ extern "C" int cascade_gemv_residual_bf16(const void *w, const void *x,
   a.y = static_cast<uint16_t *>(y);
   a.aux = static_cast<const uint16_t *>(residual);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (k == 4096) {
-    a.n_tiles = (n + 1) / 2;
-    return dispatch_gemv<2, kResidual>(a, s);
-  }
   a.n_tiles = n;
   return dispatch_gemv<1, kResidual>(a, s);
 }
