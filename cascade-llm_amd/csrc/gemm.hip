@@ -8,21 +8,22 @@
 // input (layer_streaming/llama31.py:241-279 during the prefill call, and the
 // resident LM head, llama31.py:330-334).
 //
-// Tiling.  A workgroup of 4 waves computes a 128 x 128 output tile; K is
-// walked in 64-deep slabs staged through LDS (double buffered, one barrier
-// per slab: the next slab's global loads are issued before the current
-// slab's MFMAs and written to the other buffer after them).  Each wave owns
-// 64 rows x 64 columns = 4 x 4 v_mfma_f32_16x16x32_bf16 tiles; per slab it
-// reads 8 A and 8 B fragments (16 bytes a lane) from LDS and issues 32
-// MFMAs.  LDS rows are padded to 72 bf16 (144 bytes) so the 16 rows a
-// fragment read touches start 4 banks apart.
+// Tiling.  A workgroup of 4 waves computes a BM x 128 output tile (BM = 128,
+// or 64 when 128-row tiles would leave CUs idle: short prompts and the
+// N = 1024 K / V projections); K is walked in 64-deep slabs staged through
+// LDS (double buffered, one barrier per slab: the next slab's global loads
+// are issued before the current slab's MFMAs and written to the other
+// buffer after them).  Each wave owns 64 rows x 64 (or 32) columns of
+// v_mfma_f32_16x16x32_bf16 fragments and reads its A and B fragments (16
+// bytes a lane) from LDS.  LDS rows are padded to 160 bytes, which makes
+// the fragment reads and the staging writes free of bank conflicts.
 //
-// A wave's 64 columns are not contiguous: column block j (16 wide) of wave
-// wn is at 32 wn + 16 (j & 1) + 64 (j >> 1) of the tile, so blocks j and
-// j + 2 of one lane hold columns c and c + 64.  That pairs the two halves
-// of a head (RoPE's rotate_half) and, with gate rows in tile columns 0..63
-// and up rows in 64..127, a gate and its up value, so those epilogues need
-// no data exchange.
+// A wave's columns are not contiguous: its first-half fragments and its
+// second-half fragments sit 64 columns apart, so fragment j and j + H of
+// one lane hold columns c and c + 64.  That pairs the two halves of a head
+// (RoPE's rotate_half) and, with gate rows in tile columns 0..63 and up
+// rows in 64..127, a gate and its up value, so those epilogues need no data
+// exchange.
 //
 // Tile order.  Workgroups are dispatched round-robin over the 8 XCDs (each
 // with its own L2); workgroup b runs logical tile (b % 8) * (grid / 8) +
@@ -55,15 +56,10 @@ enum GemmEpilogue : int {
   kGemmF32 = 6,
 };
 
-constexpr int kTileM = 128;
 constexpr int kTileN = 128;
 constexpr int kTileK = 64;
 constexpr int kGemmWaves = 4;
 constexpr int kGemmThreads = kGemmWaves * kWave;
-constexpr int kLdsRow = kTileK + 8;           // bf16 elements per LDS row
-constexpr int kLdsTile = kTileM * kLdsRow;    // one operand tile (128 rows)
-constexpr int kRowsPerPass = kGemmThreads / 8;  // 8 x 16 B pieces per row
-constexpr int kPasses = kTileM / kRowsPerPass;  // 4 loads per operand
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 constexpr int kGemmHead = 128;
@@ -140,32 +136,52 @@ __device__ __forceinline__ const uint16_t *gemm_w_row(const GemmArgs &a,
   }
 }
 
-// Column of tile column-block j (0..3) of wave column wn for lane row lr.
+// Tile shapes.  Every tile is 128 columns wide (one head of q|k|v, or 64
+// gate + 64 up rows); BM rows of X are split over WM x WN = 4 waves, each
+// owning FM x FN fragments of 16 x 16.
+template <int BM_, int WM_, int WN_>
+struct GemmTile {
+  static constexpr int BM = BM_;
+  static constexpr int WM = WM_;
+  static constexpr int WN = WN_;
+  static constexpr int FM = BM / WM / 16;
+  static constexpr int FN = kTileN / WN / 16;
+  static constexpr int H = FN / 2;  // fragments per half tile
+  static_assert(WM * WN == kGemmWaves, "four waves");
+};
+using GemmTile128 = GemmTile<128, 2, 2>;  // waves of 64 x 64
+using GemmTile64 = GemmTile<64, 1, 4>;    // waves of 64 x 32
+
+// Tile column of fragment j of wave column wn for lane row lr.  A wave's
+// first-half fragments (j < H) and second-half fragments (j >= H) sit 64
+// columns apart, so fragment j and j + H of one lane hold columns c and
+// c + 64: the two halves of a RoPE head, or a gate row and its up row.
+template <class T>
 __device__ __forceinline__ int gemm_col(int wn, int j, int lr) {
-  return 32 * wn + 16 * (j & 1) + 64 * (j >> 1) + lr;
+  return 16 * T::H * wn + 16 * (j % T::H) + 64 * (j / T::H) + lr;
 }
 
-template <int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, int tm, int tn,
-                                              int wm, int wn, int lane,
-                                              const f32x4 (&acc)[4][4]) {
+template <int EPI, class T>
+__device__ __forceinline__ void gemm_epilogue(
+    const GemmArgs &a, int tm, int tn, int wm, int wn, int lane,
+    const f32x4 (&acc)[T::FM][T::FN]) {
   const int lr = lane & 15;
   const int lq = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < T::FM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t row = static_cast<int64_t>(tm) * kTileM + 64 * wm + 16 * i +
-                          4 * lq + r;
+      const int64_t row = static_cast<int64_t>(tm) * T::BM +
+                          (T::BM / T::WM) * wm + 16 * i + 4 * lq + r;
       if (row >= a.m) continue;
       if constexpr (EPI == kGemmQkvRope) {
         const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
         const int64_t pos = a.pos0 + row;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int d = gemm_col(wn, j, lr);  // 0..63
+        for (int j = 0; j < T::H; ++j) {
+          const int d = gemm_col<T>(wn, j, lr);  // 0..63
           const float xa = round_bf16(acc[i][j][r]);
-          const float xb = round_bf16(acc[i][j + 2][r]);
+          const float xb = round_bf16(acc[i][j + T::H][r]);
           uint16_t oa, ob;
           if (tn < hq + hk) {
             // x*cos + rotate_half(x)*sin, products and sum rounded to bf16
@@ -193,19 +209,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, int tm, int tn,
         }
       } else if constexpr (EPI == kGemmSwiglu) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < T::H; ++j) {
           const int64_t col =
-              static_cast<int64_t>(tn) * kGemmHalfHead + gemm_col(wn, j, lr);
+              static_cast<int64_t>(tn) * kGemmHalfHead + gemm_col<T>(wn, j, lr);
           const float g = round_bf16(acc[i][j][r]);
-          const float u = round_bf16(acc[i][j + 2][r]);
+          const float u = round_bf16(acc[i][j + T::H][r]);
           const float s = round_bf16(gemm_silu(g));
           a.y[row * a.ldy + col] = f32_to_bf16(s * u);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < T::FN; ++j) {
           const int64_t col =
-              static_cast<int64_t>(tn) * kTileN + gemm_col(wn, j, lr);
+              static_cast<int64_t>(tn) * kTileN + gemm_col<T>(wn, j, lr);
           if (col >= a.n0) continue;
           const int64_t at = row * a.ldy + col;
           if constexpr (EPI == kGemmF32) {
@@ -230,110 +246,132 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, int tm, int tn,
   }
 }
 
-template <int EPI>
+// LDS rows are kTileK + kGemmPad bf16 (160 bytes): with that stride the
+// fragment reads (16 rows, one 16-byte piece each) and the staging writes
+// are free of bank conflicts on gfx950 (SQ_LDS_BANK_CONFLICT = 0; 144-byte
+// rows: 0.5 conflicts per access).
+constexpr int kGemmPad = 16;
+constexpr int kGemmRow = kTileK + kGemmPad;
+constexpr int kGemmPieces = kTileK / 8;                  // 16-byte pieces per row
+constexpr int kGemmRowsPass = kGemmThreads / kGemmPieces;  // 32 rows per pass
+
+template <int EPI, class T>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kLdsTile];
+  constexpr int kXPass = T::BM / kGemmRowsPass;  // X loads per thread
+  constexpr int kWPass = kTileN / kGemmRowsPass;  // W loads per thread
+  __shared__ __attribute__((aligned(16))) uint16_t lds_x[2][T::BM * kGemmRow];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_w[2][kTileN * kGemmRow];
   int tm, tn;
   if (!gemm_tile(a, tm, tn)) return;  // whole workgroup: no barrier skipped
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int wm = wave / T::WN;
+  const int wn = wave % T::WN;
   const int lr = lane & 15;
   const int lk = (lane >> 4) * 8;
 
   // Global -> LDS staging: thread t moves 16-byte piece t % 8 of rows
-  // t / 8 + 32 p (p = 0..3) of both operands.  X rows past m repeat row
-  // m - 1 (valid memory; their results are not stored).
-  const int piece = tid & 7;
-  const int srow = tid >> 3;
-  const uint16_t *xrow[kPasses];
-  const uint16_t *wrow[kPasses];
+  // t / 8 + 32 p of each operand.  X rows past m repeat row m - 1 (valid
+  // memory; their results are not stored).
+  const int piece = tid % kGemmPieces;
+  const int srow = tid / kGemmPieces;
+  const uint16_t *xrow[kXPass];
+  const uint16_t *wrow[kWPass];
 #pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int r = srow + kRowsPerPass * p;
-    int64_t xr = static_cast<int64_t>(tm) * kTileM + r;
+  for (int p = 0; p < kXPass; ++p) {
+    int64_t xr = static_cast<int64_t>(tm) * T::BM + srow + kGemmRowsPass * p;
     xr = xr < a.m ? xr : a.m - 1;
     xrow[p] = a.x + xr * a.k + piece * 8;
-    wrow[p] = gemm_w_row<EPI>(a, tn, r) + piece * 8;
   }
+#pragma unroll
+  for (int p = 0; p < kWPass; ++p)
+    wrow[p] = gemm_w_row<EPI>(a, tn, srow + kGemmRowsPass * p) + piece * 8;
 
-  f32x4 acc[4][4];
+  f32x4 acc[T::FM][T::FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  u32x4 rx[kPasses], rw[kPasses];
+  const int lds_at = srow * kGemmRow + piece * 8;
+  u32x4 rx[kXPass], rw[kWPass];
+  auto load_slab = [&](int slab) {
+    const int64_t k0 = static_cast<int64_t>(slab) * kTileK;
 #pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    rx[p] = *reinterpret_cast<const u32x4 *>(xrow[p]);
-    rw[p] = *reinterpret_cast<const u32x4 *>(wrow[p]);
-  }
-  const int lds_at = srow * kLdsRow + piece * 8;
+    for (int p = 0; p < kXPass; ++p)
+      rx[p] = *reinterpret_cast<const u32x4 *>(xrow[p] + k0);
 #pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    *reinterpret_cast<u32x4 *>(&lds[0][0][lds_at + p * kRowsPerPass * kLdsRow]) = rx[p];
-    *reinterpret_cast<u32x4 *>(&lds[0][1][lds_at + p * kRowsPerPass * kLdsRow]) = rw[p];
-  }
-  __syncthreads();
-
-  const int slabs = static_cast<int>(a.k / kTileK);
-  for (int s = 0; s < slabs; ++s) {
-    const int cur = s & 1;
-    const bool more = s + 1 < slabs;
-    if (more) {
-      const int64_t k0 = static_cast<int64_t>(s + 1) * kTileK;
+    for (int p = 0; p < kWPass; ++p)
+      rw[p] = *reinterpret_cast<const u32x4 *>(wrow[p] + k0);
+  };
+  auto store_slab = [&](int buf) {
 #pragma unroll
-      for (int p = 0; p < kPasses; ++p) {
-        rx[p] = *reinterpret_cast<const u32x4 *>(xrow[p] + k0);
-        rw[p] = *reinterpret_cast<const u32x4 *>(wrow[p] + k0);
-      }
-    }
-    const uint16_t *la = lds[cur][0];
-    const uint16_t *lb = lds[cur][1];
+    for (int p = 0; p < kXPass; ++p)
+      *reinterpret_cast<u32x4 *>(&lds_x[buf][lds_at + p * kGemmRowsPass * kGemmRow]) = rx[p];
+#pragma unroll
+    for (int p = 0; p < kWPass; ++p)
+      *reinterpret_cast<u32x4 *>(&lds_w[buf][lds_at + p * kGemmRowsPass * kGemmRow]) = rw[p];
+  };
+  auto compute = [&](int buf) {
+    const uint16_t *la = lds_x[buf] + (T::BM / T::WM) * wm * kGemmRow;
+    const uint16_t *lb = lds_w[buf];
 #pragma unroll
     for (int ks = 0; ks < kTileK / 32; ++ks) {
-      u32x4 af[4], bfr[4];
+      u32x4 af[T::FM], bfr[T::FN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < T::FM; ++i)
         af[i] = *reinterpret_cast<const u32x4 *>(
-            la + (64 * wm + 16 * i + lr) * kLdsRow + 32 * ks + lk);
+            la + (16 * i + lr) * kGemmRow + 32 * ks + lk);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < T::FN; ++j)
         bfr[j] = *reinterpret_cast<const u32x4 *>(
-            lb + gemm_col(wn, j, lr) * kLdsRow + 32 * ks + lk);
+            lb + gemm_col<T>(wn, j, lr) * kGemmRow + 32 * ks + lk);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < T::FN; ++j)
           acc[i][j] = mfma_16x16x32_bf16(af[i], bfr[j], acc[i][j]);
     }
-    if (more) {
-      const int nxt = cur ^ 1;
-#pragma unroll
-      for (int p = 0; p < kPasses; ++p) {
-        *reinterpret_cast<u32x4 *>(&lds[nxt][0][lds_at + p * kRowsPerPass * kLdsRow]) = rx[p];
-        *reinterpret_cast<u32x4 *>(&lds[nxt][1][lds_at + p * kRowsPerPass * kLdsRow]) = rw[p];
-      }
-    }
+  };
+
+  // The next slab's global loads are in flight during this slab's MFMAs;
+  // they land in the other LDS buffer, one barrier per slab.
+  const int slabs = static_cast<int>(a.k / kTileK);
+  load_slab(0);
+  store_slab(0);
+  __syncthreads();
+  for (int s = 0; s < slabs; ++s) {
+    const bool more = s + 1 < slabs;
+    if (more) load_slab(s + 1);
+    compute(s & 1);
+    if (more) store_slab((s + 1) & 1);
     __syncthreads();
   }
-  gemm_epilogue<EPI>(a, tm, tn, wm, wn, lane, acc);
+  gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
 }
 
-template <int EPI>
-static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
-  const int64_t tiles_m = (a.m + kTileM - 1) / kTileM;
+template <int EPI, class T>
+static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+  const int64_t tiles_m = (a.m + T::BM - 1) / T::BM;
   const int64_t tiles = tiles_m * tiles_n;
   if (tiles > (int64_t{1} << 30)) return static_cast<hipError_t>(CASCADE_ESHAPE);
   a.tiles_m = static_cast<int32_t>(tiles_m);
   a.tiles_n = static_cast<int32_t>(tiles_n);
   a.tiles = static_cast<int32_t>(tiles);
   const int64_t grid = (tiles + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(gemm_kernel<EPI>, dim3(static_cast<unsigned>(grid)),
+  return launch_kernel(gemm_kernel<EPI, T>, dim3(static_cast<unsigned>(grid)),
                        dim3(kGemmThreads), 0, s, a);
+}
+
+// 128-row tiles unless they would leave CUs idle: at most 64 rows of X
+// (short prefills) or fewer 128-row tiles than the 256 CUs (the K / V
+// projections, N = 1024, at M = 2048) take 64-row tiles.
+template <int EPI>
+static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+  const int64_t tiles128 = (a.m + 127) / 128 * tiles_n;
+  if (a.m <= 64 || tiles128 < 256) return launch_tiles<EPI, GemmTile64>(a, tiles_n, s);
+  return launch_tiles<EPI, GemmTile128>(a, tiles_n, s);
 }
 
 // Shared argument checks: X [m, k], K a multiple of the 64-deep slab.
