@@ -288,16 +288,22 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
 // layer_streaming/llama31.py:223-229): query token t (cache slot past + t)
 // attends to cache positions [0, past + t].
 //
-// One wave owns one KV head and 4 consecutive query tokens; its 16 MFMA
-// columns are (token t0 + c / 4, query head 4 g + c % 4), so the 4 query
-// heads sharing the KV head reuse every K / V fragment.  The wave walks
+// One wave owns one KV head and NB x 4 consecutive query tokens: NB blocks
+// of 16 MFMA columns, column c of block b being (token t0 + 4 b + c / 4,
+// query head 4 g + c % 4), so the 4 query heads sharing the KV head and the
+// NB token groups reuse every K / V fragment the wave loads.  The wave walks
 // 32-row blocks from position 0 to its last token's position with the
 // decode kernel's block step (scores S = K_blk Q^T, online softmax in
 // registers, O += V_blk^T P, P rounded to bf16 for the MFMA); positions
 // beyond a column's own limit score -inf.  No split and no merge: a wave
 // finishes its columns and writes them.  Workgroups run the latest tokens
 // (the longest walks) first.
-constexpr int kPrefillTokens = 4;  // query tokens per wave
+// Two column blocks per wave, at most 256 registers (2 waves per SIMD):
+// 150 us per layer at S = 2048 on MI355X (one block: 240 us; four blocks:
+// 157 us at one wave per SIMD, spills when held to two).
+constexpr int kPrefillBlocks = 2;                    // MFMA column blocks per wave
+constexpr int kPrefillTokens = 4 * kPrefillBlocks;  // query tokens per wave
+constexpr int kPrefillWavesPerSimd = 2;
 
 struct PrefillArgs {
   const uint16_t *q;  // [tokens, n_q_heads * D]
@@ -307,15 +313,16 @@ struct PrefillArgs {
   int32_t past;
   int32_t tokens;
   int32_t q_row;  // n_q_heads * D
-  int32_t groups;  // ceil(tokens / kPrefillTokens)
+  int32_t groups;  // ceil(tokens / (4 NB))
   float scale_log2;
   uint16_t *out;  // [tokens, n_q_heads * D]
 };
 
-template <bool NT>
-__global__ __launch_bounds__(kAttnWaves *kWave) void prefill_attention_kernel(
+template <bool NT, int NB, int WPE>
+__global__ __launch_bounds__(kAttnWaves *kWave)
+__attribute__((amdgpu_waves_per_eu(WPE))) void prefill_attention_kernel(
     PrefillArgs a) {
-  constexpr int G = kAttnG, D = kAttnD;
+  constexpr int G = kAttnG, D = kAttnD, TOK = 4 * NB;
   const int g = blockIdx.y;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -325,28 +332,37 @@ __global__ __launch_bounds__(kAttnWaves *kWave) void prefill_attention_kernel(
   if (group >= a.groups) return;  // no barriers in this kernel
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
-  const int tq = group * kPrefillTokens + (c16 >> 2);
   const int hq = g * G + (c16 & 3);
-  const int tq_load = min(tq, a.tokens - 1);
-  const int limit = a.past + tq;  // inclusive
-  const int t_last = min(group * kPrefillTokens + kPrefillTokens - 1,
-                         a.tokens - 1);
+  const int t_last = min(group * TOK + TOK - 1, a.tokens - 1);
   const int end = a.past + t_last + 1;
   const int last = end - 1;
 
-  u32x4 qop[4];
-  const uint16_t *qrow = a.q + static_cast<int64_t>(tq_load) * a.q_row + hq * D;
+  int tq[NB], limit[NB];
+  u32x4 qop[NB][4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    qop[c] = *reinterpret_cast<const u32x4 *>(qrow + 32 * c + 8 * g4);
+  for (int b = 0; b < NB; ++b) {
+    tq[b] = group * TOK + 4 * b + (c16 >> 2);
+    limit[b] = a.past + tq[b];  // inclusive
+    const int tq_load = min(tq[b], a.tokens - 1);
+    const uint16_t *qrow =
+        a.q + static_cast<int64_t>(tq_load) * a.q_row + hq * D;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      qop[b][c] = *reinterpret_cast<const u32x4 *>(qrow + 32 * c + 8 * g4);
+  }
   const uint16_t *kb = a.k + g * a.head_stride;
   const uint16_t *vb = a.v + g * a.head_stride;
   const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
 
-  float m = -INFINITY, l = 0.0f;
-  f32x4 o[8];
+  float m[NB], l[NB];
+  f32x4 o[NB][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b = 0; b < NB; ++b) {
+    m[b] = -INFINITY;
+    l[b] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[b][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
   for (int r0 = 0; r0 < end; r0 += kAttnBlock) {
     u32x4 kt[2][4];
@@ -364,58 +380,68 @@ __global__ __launch_bounds__(kAttnWaves *kWave) void prefill_attention_kernel(
       const int row = min(r0 + 8 * g4 + j, last);
       vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
     }
-    f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+    u32x4 vop[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      s0 = mfma_16x16x32_bf16(kt[0][c], qop[c], s0);
-      s1 = mfma_16x16x32_bf16(kt[1][c], qop[c], s1);
+    for (int e = 0; e < 8; ++e) vop[e] = v_operand(vt, e);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s0 = mfma_16x16x32_bf16(kt[0][c], qop[b][c], s0);
+        s1 = mfma_16x16x32_bf16(kt[1][c], qop[b][c], s1);
+      }
+      // s[j]: position r0 + 8 g4 + j, column c16 of block b
+      float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        s[j] = r0 + 8 * g4 + j <= limit[b] ? s[j] * a.scale_log2 : -INFINITY;
+        bmax = fmaxf(bmax, s[j]);
+      }
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+      // finite from the first block on: position 0 is valid for every column
+      const float mnew = fmaxf(m[b], bmax);
+      const float alpha = exp2_fast(m[b] - mnew);
+      m[b] = mnew;
+      float p[8], psum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = exp2_fast(s[j] - mnew);
+        psum += p[j];
+      }
+      l[b] = fmaf(l[b], alpha, psum);
+      u32x4 pop;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pop[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+      if (alpha != 1.0f) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[b][e] *= alpha;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o[b][e] = mfma_16x16x32_bf16(vop[e], pop, o[b][e]);
     }
-    // s[j]: position r0 + 8 g4 + j, column c16
-    float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-    float bmax = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      s[j] = r0 + 8 * g4 + j <= limit ? s[j] * a.scale_log2 : -INFINITY;
-      bmax = fmaxf(bmax, s[j]);
-    }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
-    // finite from the first block on: position 0 is valid for every column
-    const float mnew = fmaxf(m, bmax);
-    const float alpha = exp2_fast(m - mnew);
-    m = mnew;
-    float p[8], psum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[j] = exp2_fast(s[j] - mnew);
-      psum += p[j];
-    }
-    l = fmaf(l, alpha, psum);
-    u32x4 pop;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pop[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-    if (alpha != 1.0f) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] *= alpha;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
   }
 
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
-  if (tq >= a.tokens) return;
-  const float inv = 1.0f / l;
-  // o[e][r] = O[dim 8 (4 g4 + r) + e][column c16]
-  uint16_t *orow = a.out + static_cast<int64_t>(tq) * a.q_row + hq * D;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    u32x4 packed;
+  for (int b = 0; b < NB; ++b) {
+    float lb = l[b];
+    lb += __shfl_xor(lb, 16, kWave);
+    lb += __shfl_xor(lb, 32, kWave);
+    if (tq[b] >= a.tokens) continue;
+    const float inv = 1.0f / lb;
+    // o[b][e][r] = O[dim 8 (4 g4 + r) + e][column c16 of block b]
+    uint16_t *orow = a.out + static_cast<int64_t>(tq[b]) * a.q_row + hq * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      packed[i] = pack_bf16x2(o[2 * i][r] * inv, o[2 * i + 1][r] * inv);
-    *reinterpret_cast<u32x4 *>(orow + 8 * (4 * g4 + r)) = packed;
+    for (int r = 0; r < 4; ++r) {
+      u32x4 packed;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        packed[i] = pack_bf16x2(o[b][2 * i][r] * inv, o[b][2 * i + 1][r] * inv);
+      *reinterpret_cast<u32x4 *>(orow + 8 * (4 * g4 + r)) = packed;
+    }
   }
 }
 
@@ -536,7 +562,7 @@ extern "C" int cascade_prefill_attention_bf16(
   const dim3 grid(static_cast<unsigned>(blocks),
                   static_cast<unsigned>(n_kv_heads));
   // K / V rows are re-read by every later query token: keep them cached
-  return launch_kernel(prefill_attention_kernel<false>, grid,
+  return launch_kernel(prefill_attention_kernel<false, kPrefillBlocks, kPrefillWavesPerSimd>, grid,
                        dim3(kAttnWaves * kWave), 0,
                        static_cast<hipStream_t>(stream), a);
 }

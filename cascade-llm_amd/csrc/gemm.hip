@@ -255,7 +255,7 @@ constexpr int kGemmRow = kTileK + kGemmPad;
 constexpr int kGemmPieces = kTileK / 8;                  // 16-byte pieces per row
 constexpr int kGemmRowsPass = kGemmThreads / kGemmPieces;  // 32 rows per pass
 
-template <int EPI, class T>
+template <int EPI, class T, int DEPTH>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   constexpr int kXPass = T::BM / kGemmRowsPass;  // X loads per thread
   constexpr int kWPass = kTileN / kGemmRowsPass;  // W loads per thread
@@ -295,8 +295,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int lds_at = srow * kGemmRow + piece * 8;
-  u32x4 rx[kXPass], rw[kWPass];
-  auto load_slab = [&](int slab) {
+  auto load_slab = [&](int slab, u32x4 (&rx)[kXPass], u32x4 (&rw)[kWPass]) {
     const int64_t k0 = static_cast<int64_t>(slab) * kTileK;
 #pragma unroll
     for (int p = 0; p < kXPass; ++p)
@@ -305,7 +304,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     for (int p = 0; p < kWPass; ++p)
       rw[p] = *reinterpret_cast<const u32x4 *>(wrow[p] + k0);
   };
-  auto store_slab = [&](int buf) {
+  auto store_slab = [&](int buf, const u32x4 (&rx)[kXPass],
+                        const u32x4 (&rw)[kWPass]) {
 #pragma unroll
     for (int p = 0; p < kXPass; ++p)
       *reinterpret_cast<u32x4 *>(&lds_x[buf][lds_at + p * kGemmRowsPass * kGemmRow]) = rx[p];
@@ -335,18 +335,41 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     }
   };
 
-  // The next slab's global loads are in flight during this slab's MFMAs;
-  // they land in the other LDS buffer, one barrier per slab.
   const int slabs = static_cast<int>(a.k / kTileK);
-  load_slab(0);
-  store_slab(0);
-  __syncthreads();
-  for (int s = 0; s < slabs; ++s) {
-    const bool more = s + 1 < slabs;
-    if (more) load_slab(s + 1);
-    compute(s & 1);
-    if (more) store_slab((s + 1) & 1);
+  if constexpr (DEPTH == 1) {
+    // The next slab's global loads are in flight during this slab's MFMAs;
+    // they land in the other LDS buffer, one barrier per slab.
+    u32x4 rx[kXPass], rw[kWPass];
+    load_slab(0, rx, rw);
+    store_slab(0, rx, rw);
     __syncthreads();
+    for (int s = 0; s < slabs; ++s) {
+      const bool more = s + 1 < slabs;
+      if (more) load_slab(s + 1, rx, rw);
+      compute(s & 1);
+      if (more) store_slab((s + 1) & 1, rx, rw);
+      __syncthreads();
+    }
+  } else {
+    // Two register sets: slab s + 2 loads while slab s computes and slab
+    // s + 1 (loaded a slab earlier) goes to the other LDS buffer.
+    u32x4 r0x[kXPass], r0w[kWPass], r1x[kXPass], r1w[kWPass];
+    load_slab(0, r0x, r0w);
+    if (slabs > 1) load_slab(1, r1x, r1w);
+    store_slab(0, r0x, r0w);
+    __syncthreads();
+    for (int s = 0; s < slabs;) {
+      if (s + 2 < slabs) load_slab(s + 2, r0x, r0w);
+      compute(0);
+      if (s + 1 < slabs) store_slab(1, r1x, r1w);
+      __syncthreads();
+      if (++s >= slabs) break;
+      if (s + 2 < slabs) load_slab(s + 2, r1x, r1w);
+      compute(1);
+      if (s + 1 < slabs) store_slab(0, r0x, r0w);
+      __syncthreads();
+      ++s;
+    }
   }
   gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
 }
@@ -360,7 +383,7 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   a.tiles_n = static_cast<int32_t>(tiles_n);
   a.tiles = static_cast<int32_t>(tiles);
   const int64_t grid = (tiles + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(gemm_kernel<EPI, T>, dim3(static_cast<unsigned>(grid)),
+  return launch_kernel(gemm_kernel<EPI, T, 1>, dim3(static_cast<unsigned>(grid)),
                        dim3(kGemmThreads), 0, s, a);
 }
 
