@@ -150,8 +150,7 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
       s[j] = r0 + 8 * g4 + j < end ? s[j] * a.scale_log2 : -INFINITY;
       bmax = fmaxf(bmax, s[j]);
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = xor32_max(xor16_max(bmax));
     // finite: row r0 (lane group 0, j = 0) is valid
     const float mnew = fmaxf(m, bmax);
     const float alpha = exp2_fast(m - mnew);
@@ -184,8 +183,7 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
   }
 
   // The four lanes of a head share m; sum their l.
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
+  l = xor32_sum(xor16_sum(l));
   if (c16 < G) {
     // o[e][r] = O[dim 8 (4 g4 + r) + e][head c16]
 #pragma unroll
@@ -399,8 +397,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_attention_kernel(
         s[j] = r0 + 8 * g4 + j <= limit[b] ? s[j] * a.scale_log2 : -INFINITY;
         bmax = fmaxf(bmax, s[j]);
       }
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+      bmax = xor32_max(xor16_max(bmax));
       // finite from the first block on: position 0 is valid for every column
       const float mnew = fmaxf(m[b], bmax);
       const float alpha = exp2_fast(m[b] - mnew);
@@ -428,8 +425,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_attention_kernel(
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     float lb = l[b];
-    lb += __shfl_xor(lb, 16, kWave);
-    lb += __shfl_xor(lb, 32, kWave);
+    lb = xor32_sum(xor16_sum(lb));
     if (tq[b] >= a.tokens) continue;
     const float inv = 1.0f / lb;
     // o[b][e][r] = O[dim 8 (4 g4 + r) + e][column c16 of block b]

@@ -78,28 +78,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
          (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
-
+// Wave-wide reductions.  Inside each 16-lane DPP row the values combine
+// through four DPP moves (quad_perm [1,0,3,2] and [2,3,0,1] within each
+// quad, row_half_mirror between the quads of a half row, row_mirror between
+// the halves); the four row results are then read with v_readlane and
+// combined in a fixed order.  Every lane returns the same (wave-uniform)
+// result.  All 64 lanes must be active.  (A __shfl_xor butterfly lowers to
+// six dependent LDS-crossbar permutes; these reductions sit on the tail of
+// every GEMV and top-k pass.)
 template <int CTRL>
 __device__ __forceinline__ float dpp_float(float v) {
   return __int_as_float(
       __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_float(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 // Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane of
-// the row receives the sum.  quad_perm [1,0,3,2] and [2,3,0,1] sum each
-// quad, row_half_mirror pairs the two quads of each half row, row_mirror
-// pairs the two halves.
+// the row receives the sum.
 __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_float<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_float<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -108,15 +112,82 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
-    uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
-    uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-    v = o > v ? o : v;
-  }
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_float<0xB1>(v));
+  v = fmaxf(v, dpp_float<0x4E>(v));
+  v = fmaxf(v, dpp_float<0x141>(v));
+  v = fmaxf(v, dpp_float<0x140>(v));
   return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (lane_float(v, 0) + lane_float(v, 16)) +
+         (lane_float(v, 32) + lane_float(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_float(v, 0), lane_float(v, 16)),
+               fmaxf(lane_float(v, 32), lane_float(v, 48)));
+}
+
+// Lane l combined with lane l ^ 16 (l ^ 32): v_permlane16_swap_b32 /
+// v_permlane32_swap_b32 (gfx950) with one register as both operands return,
+// in an order that depends on the lane, the lane's own value and its
+// partner's, so a commutative combine gives the same result in both lanes.
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+  const uint32_t lo = dpp_u32<CTRL>(static_cast<uint32_t>(v));
+  const uint32_t hi = dpp_u32<CTRL>(static_cast<uint32_t>(v >> 32));
+  const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+  return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int lane) {
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = dpp_max_u64<0xB1>(v);
+  v = dpp_max_u64<0x4E>(v);
+  v = dpp_max_u64<0x141>(v);
+  v = dpp_max_u64<0x140>(v);
+  uint64_t best = lane_u64(v, 0);
+#pragma unroll
+  for (int r = 1; r < 4; ++r) {
+    const uint64_t o = lane_u64(v, 16 * r);
+    best = o > best ? o : best;
+  }
+  return best;
 }
 
 // ---------------------------------------------------------------------------
