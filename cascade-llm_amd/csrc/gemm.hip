@@ -251,12 +251,12 @@ __device__ __forceinline__ void gemm_epilogue(
 // are free of bank conflicts on gfx950 (SQ_LDS_BANK_CONFLICT = 0; 144-byte
 // rows: 0.5 conflicts per access).
 constexpr int kGemmPad = 16;
-constexpr int kGemmRow = kTileK + kGemmPad;
-constexpr int kGemmPieces = kTileK / 8;                  // 16-byte pieces per row
-constexpr int kGemmRowsPass = kGemmThreads / kGemmPieces;  // 32 rows per pass
 
-template <int EPI, class T, int DEPTH>
+template <int EPI, class T, int DEPTH, int BK = kTileK>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
+  constexpr int kGemmRow = BK + kGemmPad;
+  constexpr int kGemmPieces = BK / 8;                        // 16-byte pieces per row
+  constexpr int kGemmRowsPass = kGemmThreads / kGemmPieces;  // rows per load pass
   constexpr int kXPass = T::BM / kGemmRowsPass;  // X loads per thread
   constexpr int kWPass = kTileN / kGemmRowsPass;  // W loads per thread
   __shared__ __attribute__((aligned(16))) uint16_t lds_x[2][T::BM * kGemmRow];
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 
   const int lds_at = srow * kGemmRow + piece * 8;
   auto load_slab = [&](int slab, u32x4 (&rx)[kXPass], u32x4 (&rw)[kWPass]) {
-    const int64_t k0 = static_cast<int64_t>(slab) * kTileK;
+    const int64_t k0 = static_cast<int64_t>(slab) * BK;
 #pragma unroll
     for (int p = 0; p < kXPass; ++p)
       rx[p] = *reinterpret_cast<const u32x4 *>(xrow[p] + k0);
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     const uint16_t *la = lds_x[buf] + (T::BM / T::WM) * wm * kGemmRow;
     const uint16_t *lb = lds_w[buf];
 #pragma unroll
-    for (int ks = 0; ks < kTileK / 32; ++ks) {
+    for (int ks = 0; ks < BK / 32; ++ks) {
       u32x4 af[T::FM], bfr[T::FN];
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     }
   };
 
-  const int slabs = static_cast<int>(a.k / kTileK);
+  const int slabs = static_cast<int>(a.k / BK);
   if constexpr (DEPTH == 1) {
     // The next slab's global loads are in flight during this slab's MFMAs;
     // they land in the other LDS buffer, one barrier per slab.
