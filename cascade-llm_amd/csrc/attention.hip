@@ -28,6 +28,8 @@
 // fp32 values.  Rows past the end of the span are loaded from the span's last
 // row (always valid memory) and given a score of -inf.  K and V are read
 // once, with the nontemporal hint.
+#include <cfloat>
+
 #include "cascade_device.h"
 #include "cascade_internal.h"
 
@@ -283,25 +285,49 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
 
 // ---------------------------------------------------------------------------
 // Causal GQA prefill attention (the is_causal=True SDPA of the prefill call,
-// layer_streaming/llama31.py:223-229): query token t (cache slot past + t)
-// attends to cache positions [0, past + t].
+// layer_streaming/llama31.py:219-229 with _repeat_kv at :28-31): query token
+// t (cache slot past + t) attends to cache positions [0, past + t].
 //
-// One wave owns one KV head and NB x 4 consecutive query tokens: NB blocks
-// of 16 MFMA columns, column c of block b being (token t0 + 4 b + c / 4,
-// query head 4 g + c % 4), so the 4 query heads sharing the KV head and the
-// NB token groups reuse every K / V fragment the wave loads.  The wave walks
-// 32-row blocks from position 0 to its last token's position with the
-// decode kernel's block step (scores S = K_blk Q^T, online softmax in
-// registers, O += V_blk^T P, P rounded to bf16 for the MFMA); positions
-// beyond a column's own limit score -inf.  No split and no merge: a wave
-// finishes its columns and writes them.  Workgroups run the latest tokens
-// (the longest walks) first.
-// Two column blocks per wave, at most 256 registers (2 waves per SIMD):
-// 150 us per layer at S = 2048 on MI355X (one block: 240 us; four blocks:
-// 157 us at one wave per SIMD, spills when held to two).
-constexpr int kPrefillBlocks = 2;                    // MFMA column blocks per wave
-constexpr int kPrefillTokens = 4 * kPrefillBlocks;  // query tokens per wave
-constexpr int kPrefillWavesPerSimd = 2;
+// Columns.  A wave owns 4 NB consecutive query tokens of one KV head: NB
+// blocks of 16 MFMA columns, column c of block b being (token t0 + 4 b +
+// c / 4, query head 4 g + c % 4), so the 4 query heads sharing the KV head
+// reuse every K / V fragment.  Per 32-row block of positions the wave runs
+//   S = K_blk Q^T  (two 16-row tiles x four 32-dim chunks, per column block)
+//   online softmax in registers (scores carry scale * log2 e; exp2)
+//   O += V_blk^T P (eight 16-dim tiles; P rounded to bf16 for the MFMA)
+// and positions past a column's own limit score -inf.
+//
+// Balance.  Tokens are cut into units of 4 waves x 4 NB tokens; unit u needs
+// blocks [0, len(u)), len growing along the causal triangle.  Workgroup
+// (pair p, KV head g) has 8 waves in two halves: half 0 walks unit A = p and
+// then the first `split` blocks of unit B = U - 1 - p, half 1 walks B's
+// blocks [split, len(B)); `split` evens the two walks, so all workgroups do
+// about the same work.  B's two partial softmax states are merged through
+// LDS at the end (m, l, o of half 0 rescaled onto half 1's).
+//
+// Staging.  A half walks its blocks in lockstep; each block is moved once
+// into LDS by buffer loads straight to LDS (no staging registers), K two
+// blocks ahead of use and V one block ahead, so that in step j a wave reads
+// block j's V fragments while its K Q^T products run and block j + 1's K
+// fragments while the P V products run.  Each buffer parity is its own
+// __shared__ array and the loop is unrolled by two: the compiler can see
+// that a step's LDS reads never alias the loads in flight, and waits for
+// them only at the step's closing barrier.  LDS layout of a staged 32-row
+// block (8 KB): 16-byte slot 32 ch + (r ^ 8 (ch & 1)) holds chunk ch (dims
+// 8 ch .. 8 ch + 7) of block row r.  The K fragment reads (16 lanes: rows
+// 0-15 or 16-31 of one chunk) and the transposed V reads (32 lanes: 8 rows x
+// 2 adjacent chunks) then hit distinct banks, and each read of a step is one
+// per-lane base plus an immediate offset.
+//
+// Softmax.  The running maximum moves only when a block's maximum exceeds it
+// by more than kLazyRescale (log2 units); o and l share the stale maximum,
+// so the result is unchanged and most rescales are skipped.
+//
+// MI355X, S = 2048 (config 5, one layer): 55 us, against 150 us for one wave
+// per (4 NB tokens) reading K / V from L2 with no balancing.
+constexpr int kPrefillBlocks = 2;                         // MFMA column blocks per wave
+constexpr int kPrefillUnit = kAttnWaves * 4 * kPrefillBlocks;  // query tokens per unit
+constexpr float kLazyRescale = 8.0f;
 
 struct PrefillArgs {
   const uint16_t *q;  // [tokens, n_q_heads * D]
@@ -310,135 +336,272 @@ struct PrefillArgs {
   int64_t head_stride;
   int32_t past;
   int32_t tokens;
-  int32_t q_row;  // n_q_heads * D
-  int32_t groups;  // ceil(tokens / (4 NB))
+  int32_t q_row;     // n_q_heads * D
+  int32_t units;     // ceil(tokens / kPrefillUnit)
+  int32_t kv_heads;
   float scale_log2;
   uint16_t *out;  // [tokens, n_q_heads * D]
 };
 
-template <bool NT, int NB, int WPE>
-__global__ __launch_bounds__(kAttnWaves *kWave)
-__attribute__((amdgpu_waves_per_eu(WPE))) void prefill_attention_kernel(
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, result lane i element j is
+// element i % 4 of the 8 bytes addressed by lane 4 j + i / 4 (checked on
+// gfx950).
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4 *)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+template <int NB>
+__global__ __launch_bounds__(2 * kAttnWaves * kWave)
+__attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
     PrefillArgs a) {
   constexpr int G = kAttnG, D = kAttnD, TOK = 4 * NB;
-  const int g = blockIdx.y;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int group =
-      (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) *
-          kAttnWaves + wave;
-  if (group >= a.groups) return;  // no barriers in this kernel
+  constexpr int UNIT = kAttnWaves * TOK;
+  constexpr int BUF = kAttnBlock * D;
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf0[2][BUF];  // [half]
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf1[2][BUF];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf0[2][BUF];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf1[2][BUF];
+  __shared__ f32x4 mo[kAttnWaves][NB * 8][kWave];  // half 0's partial o of B
+  __shared__ float2 mml[kAttnWaves][NB][kWave];    // and its m, l
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int half = wave / kAttnWaves;
+  const int w4 = wave % kAttnWaves;
+  const int g = static_cast<int>(blockIdx.x) % a.kv_heads;
+  const int pair = static_cast<int>(blockIdx.x) / a.kv_heads;
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
   const int hq = g * G + (c16 & 3);
-  const int t_last = min(group * TOK + TOK - 1, a.tokens - 1);
-  const int end = a.past + t_last + 1;
-  const int last = end - 1;
+  const float c = a.scale_log2;
 
-  int tq[NB], limit[NB];
+  const int ub = a.units - 1 - pair;
+  const int ua = pair < ub ? pair : -1;  // the middle unit of an odd count walks alone
+  auto unit_len = [&](int u) {
+    return u < 0 ? 0
+                 : (a.past + min(u * UNIT + UNIT - 1, a.tokens - 1)) / kAttnBlock + 1;
+  };
+  const int len_a = unit_len(ua), len_b = unit_len(ub);
+  const int split = (len_b - len_a) / 2;
+  const int steps = max(len_a + split, len_b - split);
+  auto block_at = [&](int j) {
+    if (half == 1) return j < len_b - split ? split + j : -1;
+    if (j < len_a) return j;
+    return j < len_a + split ? j - len_a : -1;
+  };
+
+  // block loads: instruction i (0..7) of a block fills slots 64 i .. 64 i + 63,
+  // i.e. chunks 2 i, 2 i + 1 of all 32 rows; lane L takes chunk
+  // 2 i + L / 32 of row (L % 32) ^ (8 (L / 32)).  Wave w4 issues i = 2 w4, 2 w4 + 1.
+  const int last_row = a.past + a.tokens - 1;
+  const int ld_row = (lane & 31) ^ (8 * (lane >> 5));
+  const int ld_chunk_bytes = 16 * (lane >> 5);
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.k + g * a.head_stride), 0, (last_row + 1) * D * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.v + g * a.head_stride), 0, (last_row + 1) * D * 2, 0x00020000);
+  auto load_block = [&](__amdgpu_buffer_rsrc_t rsrc, uint16_t *dst, int blk) {
+    const int voff = min(blk * kAttnBlock + ld_row, last_row) * (D * 2) + ld_chunk_bytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = 2 * w4 + h;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (__attribute__((address_space(3))) void *)(dst + 64 * 8 * i), 16,
+          voff, 32 * i, 0, 0);
+    }
+  };
+
+  // fragment read bases (bytes within a block buffer)
+  //  K: tile hf, dims 32 cc + 8 g4 ..: slot kv_slot(16 hf + c16, 4 cc + g4)
+  //     = 128 cc + 16 hf + [32 g4 + (c16 ^ 8 (g4 & 1))]
+  //  V: lane k = 4 j + q of group g4, half h, tile e: row 16 h + 4 g4 + j,
+  //     dims 16 e + 4 q: slot kv_slot(16 h + 4 g4 + j, 2 e + q / 2), + 8 (q & 1) bytes
+  //     = 64 e + 16 h + [32 (q / 2) + ((4 g4 + j) ^ 8 (q / 2))]
+  const int k_base = 16 * (32 * g4 + (c16 ^ (8 * (g4 & 1))));
+  const int vq = c16 & 3, vj = c16 >> 2;
+  const int v_base = 16 * (32 * (vq >> 1) + ((4 * g4 + vj) ^ (8 * (vq >> 1)))) + 8 * (vq & 1);
+
+  int tq[NB], limit[NB], lim_min = 0;
   u32x4 qop[NB][4];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    tq[b] = group * TOK + 4 * b + (c16 >> 2);
-    limit[b] = a.past + tq[b];  // inclusive
-    const int tq_load = min(tq[b], a.tokens - 1);
-    const uint16_t *qrow =
-        a.q + static_cast<int64_t>(tq_load) * a.q_row + hq * D;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      qop[b][c] = *reinterpret_cast<const u32x4 *>(qrow + 32 * c + 8 * g4);
-  }
-  const uint16_t *kb = a.k + g * a.head_stride;
-  const uint16_t *vb = a.v + g * a.head_stride;
-  const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
-
   float m[NB], l[NB];
   f32x4 o[NB][8];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    m[b] = -INFINITY;
-    l[b] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[b][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-
-  for (int r0 = 0; r0 < end; r0 += kAttnBlock) {
-    u32x4 kt[2][4];
-    u32x4 vt[8];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int row = min(r0 + krow + 4 * hf, last);
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        kt[hf][c] = kv_load<NT>(kb + static_cast<int64_t>(row) * D + 32 * c +
-                                8 * g4);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = min(r0 + 8 * g4 + j, last);
-      vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
-    }
-    u32x4 vop[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vop[e] = v_operand(vt, e);
+  auto begin_unit = [&](int u) {
+    const int t0 = u * UNIT + w4 * TOK;
+    lim_min = a.past + t0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+      tq[b] = t0 + 4 * b + (c16 >> 2);
+      limit[b] = a.past + tq[b];
+      const int tq_load = min(tq[b], a.tokens - 1);
+      const uint16_t *qrow =
+          a.q + static_cast<int64_t>(tq_load) * a.q_row + hq * D;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        s0 = mfma_16x16x32_bf16(kt[0][c], qop[b][c], s0);
-        s1 = mfma_16x16x32_bf16(kt[1][c], qop[b][c], s1);
+      for (int cc = 0; cc < 4; ++cc)
+        qop[b][cc] = *reinterpret_cast<const u32x4 *>(qrow + 32 * cc + 8 * g4);
+      m[b] = -FLT_MAX;  // finite: a column with no valid row yet keeps alpha = 1
+      l[b] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[b][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  auto write_out = [&]() {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float lb = xor32_sum(xor16_sum(l[b]));
+      if (tq[b] >= a.tokens) continue;
+      const float inv = 1.0f / lb;
+      // o[b][e][r] = O[dim 16 e + 4 g4 + r][column c16 of block b]
+      uint16_t *orow = a.out + static_cast<int64_t>(tq[b]) * a.q_row + hq * D;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint2 packed;
+        packed.x = pack_bf16x2(o[b][e][0] * inv, o[b][e][1] * inv);
+        packed.y = pack_bf16x2(o[b][e][2] * inv, o[b][e][3] * inv);
+        *reinterpret_cast<uint2 *>(orow + 16 * e + 4 * g4) = packed;
       }
-      // s[j]: position r0 + 8 g4 + j, column c16 of block b
-      float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-      float bmax = -INFINITY;
+    }
+  };
+  auto read_k = [&](const uint16_t *buf, u32x4 (&kt)[2][4]) {
+    const char *base = reinterpret_cast<const char *>(buf) + k_base;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        s[j] = r0 + 8 * g4 + j <= limit[b] ? s[j] * a.scale_log2 : -INFINITY;
-        bmax = fmaxf(bmax, s[j]);
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        kt[hf][cc] = *reinterpret_cast<const u32x4 *>(base + 2048 * cc + 256 * hf);
+  };
+  auto read_v = [&](const uint16_t *buf, u32x4 (&vf)[8]) {
+    const char *base = reinterpret_cast<const char *>(buf) + v_base;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint2 t = lds_read_tr16(
+            reinterpret_cast<const uint16_t *>(base + 1024 * e + 256 * h));
+        vf[e][2 * h] = t.x;
+        vf[e][2 * h + 1] = t.y;
       }
-      bmax = xor32_max(xor16_max(bmax));
-      // finite from the first block on: position 0 is valid for every column
-      const float mnew = fmaxf(m[b], bmax);
-      const float alpha = exp2_fast(m[b] - mnew);
-      m[b] = mnew;
-      float p[8], psum = 0.0f;
+  };
+
+  bool a_open = half == 0 && len_a > 0;
+  begin_unit(a_open ? ua : ub);
+  u32x4 kt[2][4];
+  {
+    const int b0 = block_at(0), b1 = block_at(1);
+    if (b0 >= 0) {
+      load_block(k_rsrc, kbuf0[half], b0);
+      load_block(v_rsrc, vbuf0[half], b0);
+    }
+    if (b1 >= 0) load_block(k_rsrc, kbuf1[half], b1);
+    __syncthreads();
+    if (b0 >= 0) read_k(kbuf0[half], kt);
+    __syncthreads();  // kbuf0 is refilled in step 0
+  }
+  // step j, parity P = j & 1: K_{j+2} -> kbuf[P], V_{j+1} -> vbuf[1-P];
+  // reads V_j from vbuf[P] and K_{j+1} from kbuf[1-P]
+  auto step = [&](int j, uint16_t *k_here, const uint16_t *k_next,
+                  const uint16_t *v_here, uint16_t *v_next) {
+    const int blk = block_at(j);
+    const int nb1 = block_at(j + 1);
+    const int nb2 = block_at(j + 2);
+    if (nb2 >= 0) load_block(k_rsrc, k_here, nb2);
+    if (nb1 >= 0) load_block(v_rsrc, v_next, nb1);
+    if (blk >= 0) {
+      const int r0 = blk * kAttnBlock;
+      u32x4 vf[8];
+      read_v(v_here, vf);
+      // s[b][4 hf + r]: block row 16 hf + 4 g4 + r, column c16 of block b
+      float s[NB][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        p[j] = exp2_fast(s[j] - mnew);
-        psum += p[j];
+      for (int b = 0; b < NB; ++b) {
+        f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          s0 = mfma_16x16x32_bf16(kt[0][cc], qop[b][cc], s0);
+          s1 = mfma_16x16x32_bf16(kt[1][cc], qop[b][cc], s1);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[b][r] = s0[r];
+          s[b][4 + r] = s1[r];
+        }
       }
-      l[b] = fmaf(l[b], alpha, psum);
-      u32x4 pop;
+      if (r0 + kAttnBlock - 1 > lim_min) {  // wave-uniform: a diagonal block
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pop[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-      if (alpha != 1.0f) {
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[b][e] *= alpha;
+          for (int jj = 0; jj < 8; ++jj)
+            if (r0 + 16 * (jj >> 2) + 4 * g4 + (jj & 3) > limit[b]) s[b][jj] = -INFINITY;
       }
+      u32x4 pop[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        float bmax = max_f32(max_f32(max_f32(s[b][0], s[b][1]), max_f32(s[b][2], s[b][3])),
+                             max_f32(max_f32(s[b][4], s[b][5]), max_f32(s[b][6], s[b][7])));
+        bmax = xor32_max(xor16_max(bmax)) * c;
+        if (bmax > m[b] + kLazyRescale) {
+          const float alpha = exp2_fast(m[b] - bmax);
+          m[b] = bmax;
+          l[b] *= alpha;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[b][e] *= alpha;
+        }
+        const float nm = -m[b];
+        float p[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) p[jj] = exp2_fast(fmaf(s[b][jj], c, nm));
+        // P enters the MFMA rounded to bf16; l sums the fp32 values
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+          pop[b][i2] = pack_bf16x2(p[2 * i2], p[2 * i2 + 1]);
+          l[b] += p[2 * i2] + p[2 * i2 + 1];
+        }
+      }
+      if (nb1 >= 0) read_k(k_next, kt);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        o[b][e] = mfma_16x16x32_bf16(vop[e], pop, o[b][e]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) o[b][e] = mfma_16x16x32_bf16(vf[e], pop[b], o[b][e]);
+    }
+    if (a_open && j + 1 == len_a) {  // half 0 leaves A; kt already holds B's block 0
+      write_out();
+      a_open = false;
+      begin_unit(ub);
+    }
+    __syncthreads();
+  };
+  for (int j = 0; j < steps; j += 2) {
+    step(j, kbuf0[half], kbuf1[half], vbuf0[half], vbuf1[half]);
+    if (j + 1 < steps) step(j + 1, kbuf1[half], kbuf0[half], vbuf1[half], vbuf0[half]);
+  }
+  if (a_open) write_out();
+  if (split > 0) {  // workgroup-uniform
+    if (half == 0) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        mml[w4][b][lane] = make_float2(m[b], l[b]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mo[w4][b * 8 + e][lane] = o[b][e];
+      }
+    }
+    __syncthreads();
+    if (half == 1) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float2 ml = mml[w4][b][lane];
+        const float mx = fmaxf(ml.x, m[b]);
+        const float ax = exp2_fast(ml.x - mx), ay = exp2_fast(m[b] - mx);
+        l[b] = ml.y * ax + l[b] * ay;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[b][e] = mo[w4][b * 8 + e][lane] * ax + o[b][e] * ay;
+      }
     }
   }
-
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    float lb = l[b];
-    lb = xor32_sum(xor16_sum(lb));
-    if (tq[b] >= a.tokens) continue;
-    const float inv = 1.0f / lb;
-    // o[b][e][r] = O[dim 8 (4 g4 + r) + e][column c16 of block b]
-    uint16_t *orow = a.out + static_cast<int64_t>(tq[b]) * a.q_row + hq * D;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      u32x4 packed;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        packed[i] = pack_bf16x2(o[b][2 * i][r] * inv, o[b][2 * i + 1][r] * inv);
-      *reinterpret_cast<u32x4 *>(orow + 8 * (4 * g4 + r)) = packed;
-    }
-  }
+  if (half == 1) write_out();
 }
 
 struct AttnShape {
@@ -534,7 +697,8 @@ extern "C" int cascade_prefill_attention_bf16(
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       out == nullptr)
     return CASCADE_EINVAL;
-  if (tokens <= 0 || past < 0 || past + tokens > (int64_t{1} << 30) ||
+  // positions < 2^24: per-head byte offsets of the buffer loads are 32-bit
+  if (tokens <= 0 || past < 0 || past + tokens > (int64_t{1} << 24) ||
       n_kv_heads <= 0 || n_kv_heads > 65535)
     return CASCADE_EINVAL;
   if (head_dim != kAttnD || n_q_heads != n_kv_heads * kAttnG)
@@ -551,14 +715,16 @@ extern "C" int cascade_prefill_attention_bf16(
   a.past = static_cast<int32_t>(past);
   a.tokens = static_cast<int32_t>(tokens);
   a.q_row = static_cast<int32_t>(n_q_heads * head_dim);
-  a.groups = static_cast<int32_t>((tokens + kPrefillTokens - 1) / kPrefillTokens);
+  a.units = static_cast<int32_t>((tokens + kPrefillUnit - 1) / kPrefillUnit);
+  a.kv_heads = static_cast<int32_t>(n_kv_heads);
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<uint16_t *>(out);
-  const int64_t blocks = (a.groups + kAttnWaves - 1) / kAttnWaves;
-  const dim3 grid(static_cast<unsigned>(blocks),
-                  static_cast<unsigned>(n_kv_heads));
-  // K / V rows are re-read by every later query token: keep them cached
-  return launch_kernel(prefill_attention_kernel<false, kPrefillBlocks, kPrefillWavesPerSimd>, grid,
-                       dim3(kAttnWaves * kWave), 0,
+  // one workgroup per (unit pair, KV head); consecutive workgroups take
+  // consecutive KV heads
+  const int64_t workgroups = (a.units + 1) / 2 * n_kv_heads;
+  if (workgroups > 0x7fffffff) return CASCADE_EINVAL;
+  return launch_kernel(prefill_attention_kernel<kPrefillBlocks>,
+                       dim3(static_cast<unsigned>(workgroups)),
+                       dim3(2 * kAttnWaves * kWave), 0,
                        static_cast<hipStream_t>(stream), a);
 }

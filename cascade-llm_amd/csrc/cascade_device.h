@@ -73,9 +73,14 @@ __device__ __forceinline__ f32x4 mfma_16x16x32_bf16(u32x4 a, u32x4 b,
 }
 
 // Two floats rounded to bf16 (round to nearest even), lo in bits 0..15.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to a (lo, hi) bf16 pair, round-to-nearest-even: one
+// v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) |
-         (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  return __builtin_bit_cast(
+      uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 // Wave-wide reductions.  Inside each 16-lane DPP row the values combine
@@ -136,16 +141,23 @@ __device__ __forceinline__ float wave_max(float v) {
 // v_permlane32_swap_b32 (gfx950) with one register as both operands return,
 // in an order that depends on the lane, the lane's own value and its
 // partner's, so a commutative combine gives the same result in both lanes.
+// IEEE-754 2019 maximum (NaN-propagating): one v_maximum3_f32 on gfx950,
+// with no quieting of the inputs that fmaxf's maxNum semantics needs.
+// Softmax scores are finite or -inf, where both agree.
+__device__ __forceinline__ float max_f32(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+
 __device__ __forceinline__ float xor16_max(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
                                                   __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_f32(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
                                                   __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_f32(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float xor16_sum(float v) {

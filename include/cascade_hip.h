@@ -180,7 +180,8 @@ int cascade_qkv_rope_gemm_bf16(const void *x, int64_t m, const void *wq,
 /* Causal GQA attention of `tokens` query rows q [tokens, n_q_heads * 128]:
  * query row t (cache slot past + t) attends to positions [0, past + t] of
  * the layer cache (layout as cascade_decode_attention_bf16), out [tokens,
- * n_q_heads * 128] bf16.  head_dim 128, n_q_heads = 4 n_kv_heads.
+ * n_q_heads * 128] bf16.  head_dim 128, n_q_heads = 4 n_kv_heads,
+ * past + tokens <= 2^24.
  * Replaces _repeat_kv + F.scaled_dot_product_attention(is_causal=True),
  * llama31.py:213-229 (the reference's prefill has past = 0).               */
 int cascade_prefill_attention_bf16(const void *q, const void *k_cache,

@@ -58,6 +58,15 @@ def test_argument_checks_reject_without_launching():
     assert lib.cascade_lm_head_topk_bf16(16, 100, 4096, 0, 16, 65, 1, None, 16,
                                          1 << 20, 16, 16, None) == 1001
     assert lib.cascade_memcpy_h2d_async(None, None, 0, None) == 1001
+    # prefill attention: cache positions past + tokens are limited to 2^24,
+    # head_dim to 128 and n_q_heads to 4 n_kv_heads
+    pos = 1 << 24
+    assert lib.cascade_prefill_attention_bf16(16, 16, 16, pos * 128, pos - 2, 4,
+                                              32, 8, 128, 0.1, 16, None) == 1001
+    assert lib.cascade_prefill_attention_bf16(16, 16, 16, 64 * 128, 0, 4,
+                                              32, 8, 64, 0.1, 16, None) == 1003
+    assert lib.cascade_prefill_attention_bf16(16, 16, 16, 64 * 128, 0, 4,
+                                              16, 8, 128, 0.1, 16, None) == 1003
 
 
 def test_workspace_sizes():

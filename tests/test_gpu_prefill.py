@@ -202,12 +202,17 @@ def test_gemm_row_matches_gemv_rounding(gpu_device):
     assert linear_bound_report(b.reshape(1, -1), xc, wc) <= 1.0
 
 
-@pytest.mark.parametrize("past,tokens,q_scale", [
-    (0, 1, 1), (0, 2, 1), (0, 5, 1), (0, 33, 1), (0, 130, 1), (0, 2048, 1),
-    (0, 2048, 8), (100, 7, 1), (4000, 45, 4)])
-def test_prefill_attention_matches_oracle(gpu_device, past, tokens, q_scale):
-    print("prefill attention past={} tokens={} q_scale={}".format(
-        past, tokens, q_scale), flush=True)
+# 32-token units are paired (unit p with unit U - 1 - p); 96 tokens leave a
+# middle unit that walks alone, past > 0 makes every walk long, slack 0 puts
+# the last cache row at the very end of the allocation
+@pytest.mark.parametrize("past,tokens,q_scale,slack", [
+    (0, 1, 1, 9), (0, 2, 1, 9), (0, 5, 1, 9), (0, 33, 1, 9), (0, 96, 1, 9),
+    (0, 130, 1, 9), (0, 2048, 1, 9), (0, 2048, 8, 9), (100, 7, 1, 9),
+    (4000, 45, 4, 9), (1000, 300, 1, 0), (0, 77, 1, 0)])
+def test_prefill_attention_matches_oracle(gpu_device, past, tokens, q_scale,
+                                          slack):
+    print("prefill attention past={} tokens={} q_scale={} slack={}".format(
+        past, tokens, q_scale, slack), flush=True)
     dev = gpu_device
     length = past + tokens
     q = cases.normal_bf16((32, tokens, DIM), 161)
@@ -215,7 +220,7 @@ def test_prefill_attention_matches_oracle(gpu_device, past, tokens, q_scale):
         q = (q.float() * q_scale).to(BF16)
     k = cases.normal_bf16((8, length, DIM), 162)
     v = cases.normal_bf16((8, length, DIM), 163)
-    capacity = length + 9
+    capacity = length + slack
     kc = torch.zeros((8, capacity, DIM), dtype=BF16, device=dev)
     vc = torch.zeros_like(kc)
     kc[:, :length].copy_(k.to(dev))
