@@ -10,13 +10,28 @@
 //
 // Tiling.  A workgroup of 4 waves computes a BM x 128 output tile (BM = 128,
 // or 64 when 128-row tiles would leave CUs idle: short prompts and the
-// N = 1024 K / V projections); K is walked in 64-deep slabs staged through
-// LDS (double buffered, one barrier per slab: the next slab's global loads
-// are issued before the current slab's MFMAs and written to the other
-// buffer after them).  Each wave owns 64 rows x 64 (or 32) columns of
-// v_mfma_f32_16x16x32_bf16 fragments and reads its A and B fragments (16
-// bytes a lane) from LDS.  LDS rows are padded to 160 bytes, which makes
-// the fragment reads and the staging writes free of bank conflicts.
+// N = 1024 K / V projections); K is walked in 64-deep slabs.  Each wave
+// owns 64 rows x 64 (or 32) columns of v_mfma_f32_16x16x32_bf16 fragments
+// and reads its A and B fragments (16 bytes a lane) from LDS.
+//
+// Staging.  Slabs move global -> LDS by buffer loads that write LDS
+// themselves (buffer_load_dwordx4 ... lds: no staging registers, no
+// ds_write), into two slab buffers.  Slab s: each wave waits (vmcnt) for
+// its own loads of slab s, one barrier publishes slab s to the workgroup
+// and frees slab s - 1's buffer, the loads of slab s + 1 go out, and slab
+// s's MFMAs run while they fly.  Each buffer is its own __shared__ array
+// and the loop is unrolled by two, so the compiler can tell a slab's LDS
+// reads from the loads in flight and adds no waits of its own.  (With three
+// or four buffers this compiler falls back to waiting for every load in
+// flight at each barrier, so deeper staging does not pay.)
+//
+// LDS layout of a slab: 128-byte rows (64 bf16) back to back; 16-byte
+// chunk c of row r sits at chunk c ^ ((r / 2) % 8).  A fragment read (16
+// lanes: 16 consecutive rows, one chunk) then hits 16 distinct 16-byte bank
+// groups, each read is a per-lane base plus an immediate offset, and a load
+// instruction (64 lanes x 16 bytes) fills 8 whole rows, so its lanes read
+// whole 128-byte row segments.  Rows past m (X) or past a matrix's rows (W)
+// read as zeros through the buffer bounds; their results are not stored.
 //
 // A wave's columns are not contiguous: its first-half fragments and its
 // second-half fragments sit 64 columns apart, so fragment j and j + H of
@@ -41,6 +56,8 @@
 //   swiglu    bf16(bf16(silu(bf16(g))) * bf16(u))
 //   silu / mul  the matrix-granularity halves of swiglu
 //   f32       fp32 output (LM-head logits, not rounded)
+#include <algorithm>
+
 #include "cascade_device.h"
 #include "cascade_internal.h"
 
@@ -104,36 +121,6 @@ __device__ __forceinline__ bool gemm_tile(const GemmArgs &a, int &tm, int &tn) {
   tm = first + r % gm;
   tn = r / gm;
   return true;
-}
-
-// Weight row feeding tile column r (0..127) of tile column-block tn.
-template <int EPI>
-__device__ __forceinline__ const uint16_t *gemm_w_row(const GemmArgs &a,
-                                                      int tn, int r) {
-  if constexpr (EPI == kGemmSwiglu) {
-    const int64_t i = static_cast<int64_t>(tn) * kGemmHalfHead + (r & 63);
-    return (r < 64 ? a.w0 : a.w1) + i * a.k;
-  } else if constexpr (EPI == kGemmQkvRope) {
-    const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
-    const uint16_t *base;
-    int64_t lh;
-    if (tn < hq) {
-      base = a.w0;
-      lh = tn;
-    } else if (tn < hq + hk) {
-      base = a.w1;
-      lh = tn - hq;
-    } else {
-      base = a.w2;
-      lh = tn - hq - hk;
-    }
-    return base + (lh * kGemmHead + r) * a.k;
-  } else {
-    // rows past n (a partial last tile) repeat row n - 1; not stored
-    int64_t row = static_cast<int64_t>(tn) * kTileN + r;
-    row = row < a.n0 ? row : a.n0 - 1;
-    return a.w0 + row * a.k;
-  }
 }
 
 // Tile shapes.  Every tile is 128 columns wide (one head of q|k|v, or 64
@@ -246,47 +233,110 @@ __device__ __forceinline__ void gemm_epilogue(
   }
 }
 
-// LDS rows are kTileK + kGemmPad bf16 (160 bytes): with that stride the
-// fragment reads (16 rows, one 16-byte piece each) and the staging writes
-// are free of bank conflicts on gfx950 (SQ_LDS_BANK_CONFLICT = 0; 144-byte
-// rows: 0.5 conflicts per access).
-constexpr int kGemmPad = 16;
+// Slab geometry (see the staging and layout notes at the top).
+template <int BK>
+struct DmaSlab {
+  static constexpr int CH = BK / 8;         // 16-byte chunks per row
+  static constexpr int ROWB = 2 * BK;       // bytes per row
+  static constexpr int RPB = 256 / ROWB;    // rows per 256-byte bank cycle
+  static constexpr int RPI = 1024 / ROWB;   // rows per load instruction
+  static_assert(BK == 32 || BK == 64, "slab depth");
+};
 
-template <int EPI, class T, int DEPTH, int BK = kTileK>
+// Buffer resource over [base, base + bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const uint16_t *base,
+                                                           int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0,
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+template <int EPI, class T, int BK = kTileK>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
-  constexpr int kGemmRow = BK + kGemmPad;
-  constexpr int kGemmPieces = BK / 8;                        // 16-byte pieces per row
-  constexpr int kGemmRowsPass = kGemmThreads / kGemmPieces;  // rows per load pass
-  constexpr int kXPass = T::BM / kGemmRowsPass;  // X loads per thread
-  constexpr int kWPass = kTileN / kGemmRowsPass;  // W loads per thread
-  __shared__ __attribute__((aligned(16))) uint16_t lds_x[2][T::BM * kGemmRow];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_w[2][kTileN * kGemmRow];
+  using L = DmaSlab<BK>;
+  constexpr int XI = T::BM * L::ROWB / 1024;  // load instructions per X slab
+  constexpr int WI = kTileN * L::ROWB / 1024;
+  constexpr int XW = XI / kGemmWaves, WW = WI / kGemmWaves;  // per wave
+  static_assert(XI % kGemmWaves == 0 && WI % kGemmWaves == 0, "whole loads per wave");
+  constexpr int XB = T::BM * BK, WB = kTileN * BK;  // bf16 per slab buffer
+  // one array per slab buffer (X slab, then W slab)
+  __shared__ __attribute__((aligned(16))) uint16_t sb0[XB + WB];
+  __shared__ __attribute__((aligned(16))) uint16_t sb1[XB + WB];
   int tm, tn;
   if (!gemm_tile(a, tm, tn)) return;  // whole workgroup: no barrier skipped
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wave / T::WN;
   const int wn = wave % T::WN;
   const int lr = lane & 15;
-  const int lk = (lane >> 4) * 8;
+  const int g4 = lane >> 4;
+  const int64_t k_bytes = a.k * 2;
 
-  // Global -> LDS staging: thread t moves 16-byte piece t % 8 of rows
-  // t / 8 + 32 p of each operand.  X rows past m repeat row m - 1 (valid
-  // memory; their results are not stored).
-  const int piece = tid % kGemmPieces;
-  const int srow = tid / kGemmPieces;
-  const uint16_t *xrow[kXPass];
-  const uint16_t *wrow[kWPass];
-#pragma unroll
-  for (int p = 0; p < kXPass; ++p) {
-    int64_t xr = static_cast<int64_t>(tm) * T::BM + srow + kGemmRowsPass * p;
-    xr = xr < a.m ? xr : a.m - 1;
-    xrow[p] = a.x + xr * a.k + piece * 8;
+  // operands as buffer resources; W instruction i reads matrix wsel(i)
+  const __amdgpu_buffer_rsrc_t xr = gemm_rsrc(a.x, a.m * k_bytes);
+  const uint16_t *wbase0, *wbase1;
+  int64_t wrows0, wrows1, wrow0, wrow1;  // rows of each matrix, first tile row in it
+  if constexpr (EPI == kGemmSwiglu) {
+    wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kGemmHalfHead;
+    wbase1 = a.w1; wrows1 = a.n0; wrow1 = wrow0;
+  } else if constexpr (EPI == kGemmQkvRope) {
+    const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
+    if (tn < hq) {
+      wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kGemmHead;
+    } else if (tn < hq + hk) {
+      wbase0 = a.w1; wrows0 = a.n1; wrow0 = (tn - hq) * kGemmHead;
+    } else {
+      wbase0 = a.w2; wrows0 = a.n2; wrow0 = (tn - hq - hk) * kGemmHead;
+    }
+    wbase1 = wbase0; wrows1 = wrows0; wrow1 = wrow0;
+  } else {
+    wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kTileN;
+    wbase1 = wbase0; wrows1 = wrows0; wrow1 = wrow0;
   }
+  const __amdgpu_buffer_rsrc_t wr0 = gemm_rsrc(wbase0, wrows0 * k_bytes);
+  const __amdgpu_buffer_rsrc_t wr1 = gemm_rsrc(wbase1, wrows1 * k_bytes);
+
+  // lane part of a load: row L / CH of the instruction's RPI rows, physical
+  // chunk L % CH, i.e. logical chunk (L % CH) ^ f(row); f depends on the
+  // instruction only through its parity (BK = 64)
+  const int ld_r = lane / L::CH;
+  auto ld_off = [&](int parity) {
+    const int f = ((L::RPI * parity + ld_r) / L::RPB) % L::CH;
+    return ld_r * static_cast<int>(k_bytes) + 16 * ((lane % L::CH) ^ f);
+  };
+  const int ld_off0 = ld_off(0), ld_off1 = ld_off(1);
+
+  // The whole byte offset goes in voffset: the buffer range check covers
+  // voffset (not soffset), so rows past the end read as zeros instead of
+  // leaving the allocation.  Offsets stay below 2^31 (checked on the host).
+  auto load_slab = [&](int slab, uint16_t *dx, uint16_t *dw) {
+    const int kb = slab * BK * 2;
 #pragma unroll
-  for (int p = 0; p < kWPass; ++p)
-    wrow[p] = gemm_w_row<EPI>(a, tn, srow + kGemmRowsPass * p) + piece * 8;
+    for (int h = 0; h < XW; ++h) {
+      const int i = wave * XW + h;
+      const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xr, (__attribute__((address_space(3))) void *)(dx + i * 512), 16,
+          ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb, 0, 0, 0);
+    }
+#pragma unroll
+    for (int h = 0; h < WW; ++h) {
+      const int i = wave * WW + h;
+      const int trow = L::RPI * i;  // tile row of the instruction
+      const bool second = EPI == kGemmSwiglu && trow >= kGemmHalfHead;
+      const int64_t row = (second ? wrow1 : wrow0) + (second ? trow - kGemmHalfHead : trow);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          second ? wr1 : wr0, (__attribute__((address_space(3))) void *)(dw + i * 512), 16,
+          ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb, 0, 0, 0);
+    }
+  };
+
+  // fragment reads: rows 16 q + lr (q: fragment), chunk 4 ks + g4 at
+  // physical chunk (4 ks + g4) ^ f(lr), f(lr) = (lr / RPB) % CH
+  const int fl = (lr / L::RPB) % L::CH;
+  const int rd_off0 = lr * L::ROWB + 16 * ((g4) ^ fl);
+  const int rd_off1 = lr * L::ROWB + 16 * ((4 + g4) ^ fl);
+  const int arow0 = (T::BM / T::WM) * wm;
 
   f32x4 acc[T::FM][T::FN];
 #pragma unroll
@@ -294,39 +344,20 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int lds_at = srow * kGemmRow + piece * 8;
-  auto load_slab = [&](int slab, u32x4 (&rx)[kXPass], u32x4 (&rw)[kWPass]) {
-    const int64_t k0 = static_cast<int64_t>(slab) * BK;
-#pragma unroll
-    for (int p = 0; p < kXPass; ++p)
-      rx[p] = *reinterpret_cast<const u32x4 *>(xrow[p] + k0);
-#pragma unroll
-    for (int p = 0; p < kWPass; ++p)
-      rw[p] = *reinterpret_cast<const u32x4 *>(wrow[p] + k0);
-  };
-  auto store_slab = [&](int buf, const u32x4 (&rx)[kXPass],
-                        const u32x4 (&rw)[kWPass]) {
-#pragma unroll
-    for (int p = 0; p < kXPass; ++p)
-      *reinterpret_cast<u32x4 *>(&lds_x[buf][lds_at + p * kGemmRowsPass * kGemmRow]) = rx[p];
-#pragma unroll
-    for (int p = 0; p < kWPass; ++p)
-      *reinterpret_cast<u32x4 *>(&lds_w[buf][lds_at + p * kGemmRowsPass * kGemmRow]) = rw[p];
-  };
-  auto compute = [&](int buf) {
-    const uint16_t *la = lds_x[buf] + (T::BM / T::WM) * wm * kGemmRow;
-    const uint16_t *lb = lds_w[buf];
+  auto compute = [&](const uint16_t *bx, const uint16_t *bw) {
+    const char *ax = reinterpret_cast<const char *>(bx) + arow0 * L::ROWB;
+    const char *aw = reinterpret_cast<const char *>(bw);
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
+      const int off = ks ? rd_off1 : rd_off0;
       u32x4 af[T::FM], bfr[T::FN];
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
-        af[i] = *reinterpret_cast<const u32x4 *>(
-            la + (16 * i + lr) * kGemmRow + 32 * ks + lk);
+        af[i] = *reinterpret_cast<const u32x4 *>(ax + off + 16 * i * L::ROWB);
 #pragma unroll
       for (int j = 0; j < T::FN; ++j)
         bfr[j] = *reinterpret_cast<const u32x4 *>(
-            lb + gemm_col<T>(wn, j, lr) * kGemmRow + 32 * ks + lk);
+            aw + off + (gemm_col<T>(wn, j, lr) - lr) * L::ROWB);
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
 #pragma unroll
@@ -336,40 +367,22 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   };
 
   const int slabs = static_cast<int>(a.k / BK);
-  if constexpr (DEPTH == 1) {
-    // The next slab's global loads are in flight during this slab's MFMAs;
-    // they land in the other LDS buffer, one barrier per slab.
-    u32x4 rx[kXPass], rw[kWPass];
-    load_slab(0, rx, rw);
-    store_slab(0, rx, rw);
-    __syncthreads();
-    for (int s = 0; s < slabs; ++s) {
-      const bool more = s + 1 < slabs;
-      if (more) load_slab(s + 1, rx, rw);
-      compute(s & 1);
-      if (more) store_slab((s + 1) & 1, rx, rw);
-      __syncthreads();
-    }
-  } else {
-    // Two register sets: slab s + 2 loads while slab s computes and slab
-    // s + 1 (loaded a slab earlier) goes to the other LDS buffer.
-    u32x4 r0x[kXPass], r0w[kWPass], r1x[kXPass], r1w[kWPass];
-    load_slab(0, r0x, r0w);
-    if (slabs > 1) load_slab(1, r1x, r1w);
-    store_slab(0, r0x, r0w);
-    __syncthreads();
-    for (int s = 0; s < slabs;) {
-      if (s + 2 < slabs) load_slab(s + 2, r0x, r0w);
-      compute(0);
-      if (s + 1 < slabs) store_slab(1, r1x, r1w);
-      __syncthreads();
-      if (++s >= slabs) break;
-      if (s + 2 < slabs) load_slab(s + 2, r1x, r1w);
-      compute(1);
-      if (s + 1 < slabs) store_slab(0, r0x, r0w);
-      __syncthreads();
-      ++s;
-    }
+  // s_waitcnt vmcnt(0), expcnt / lgkmcnt left alone
+  constexpr int kWaitLoads = (7 << 4) | (15 << 8);
+  // slab s: this wave's loads of s done; barrier (everyone's slab s has
+  // landed, slab s - 1 has been read); slab s + 1 into the other buffer;
+  // compute s.  The buffers are named directly at every call.
+  auto step = [&](int s, const uint16_t *cur, uint16_t *nxt) {
+    if (s >= slabs) return;
+    __builtin_amdgcn_s_waitcnt(kWaitLoads);
+    __builtin_amdgcn_s_barrier();
+    if (s + 1 < slabs) load_slab(s + 1, nxt, nxt + XB);
+    compute(cur, cur + XB);
+  };
+  load_slab(0, sb0, sb0 + XB);
+  for (int s0 = 0; s0 < slabs; s0 += 2) {
+    step(s0, sb0, sb1);
+    step(s0 + 1, sb1, sb0);
   }
   gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
 }
@@ -383,7 +396,7 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   a.tiles_n = static_cast<int32_t>(tiles_n);
   a.tiles = static_cast<int32_t>(tiles);
   const int64_t grid = (tiles + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(gemm_kernel<EPI, T, 1>, dim3(static_cast<unsigned>(grid)),
+  return launch_kernel(gemm_kernel<EPI, T>, dim3(static_cast<unsigned>(grid)),
                        dim3(kGemmThreads), 0, s, a);
 }
 
@@ -398,18 +411,23 @@ static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
 }
 
 // Shared argument checks: X [m, k], K a multiple of the 64-deep slab.
+// Byte offsets of the slab loads are 32-bit: X and every W stay below 2 GiB.
+constexpr int64_t kGemmMaxBytes = int64_t{1} << 31;
+
 static int gemm_check_x(const void *x, int64_t m, int64_t k) {
   if (x == nullptr || m <= 0 || k <= 0 || m > (int64_t{1} << 24))
     return CASCADE_EINVAL;
   if (!aligned16(x)) return CASCADE_EALIGN;
   if (k % kTileK) return CASCADE_ESHAPE;
+  if (m * k * 2 >= kGemmMaxBytes) return CASCADE_ESHAPE;
   return 0;
 }
 
-static int gemm_check_w(const void *w, int64_t n, int64_t granule) {
+static int gemm_check_w(const void *w, int64_t n, int64_t granule, int64_t k) {
   if (w == nullptr || n <= 0) return CASCADE_EINVAL;
   if (!aligned16(w)) return CASCADE_EALIGN;
   if (n % granule) return CASCADE_ESHAPE;
+  if (n * k * 2 >= kGemmMaxBytes) return CASCADE_ESHAPE;
   return 0;
 }
 
@@ -420,7 +438,7 @@ using namespace cascade;
 static int gemm_plain(int epi, const void *x, const void *w, const void *aux,
                       void *y, int64_t m, int64_t n, int64_t k, void *stream) {
   if (int e = gemm_check_x(x, m, k)) return e;
-  if (int e = gemm_check_w(w, n, 1)) return e;
+  if (int e = gemm_check_w(w, n, 1, k)) return e;
   if (y == nullptr) return CASCADE_EINVAL;
   if (!aligned16(y)) return CASCADE_EALIGN;
   if ((epi == kGemmResidual || epi == kGemmMul) && aux == nullptr)
@@ -483,8 +501,8 @@ extern "C" int cascade_gate_up_swiglu_gemm_bf16(const void *x,
                                                 int64_t m, int64_t n_half,
                                                 int64_t k, void *stream) {
   if (int e = gemm_check_x(x, m, k)) return e;
-  if (int e = gemm_check_w(w_gate, n_half, kGemmHalfHead)) return e;
-  if (int e = gemm_check_w(w_up, n_half, kGemmHalfHead)) return e;
+  if (int e = gemm_check_w(w_gate, n_half, kGemmHalfHead, k)) return e;
+  if (int e = gemm_check_w(w_up, n_half, kGemmHalfHead, k)) return e;
   if (y == nullptr) return CASCADE_EINVAL;
   if (!aligned16(y)) return CASCADE_EALIGN;
   GemmArgs a{};
@@ -508,6 +526,7 @@ extern "C" int cascade_qkv_rope_gemm_bf16(
     void *stream) {
   if (int e = gemm_check_x(x, m, k)) return e;
   if (nq < 0 || nk < 0 || nv < 0 || nq + nk + nv == 0) return CASCADE_EINVAL;
+  if (std::max(nq, std::max(nk, nv)) * k * 2 >= kGemmMaxBytes) return CASCADE_ESHAPE;
   if ((nq % kGemmHead) || (nk % kGemmHead) || (nv % kGemmHead))
     return CASCADE_ESHAPE;
   if (nq && (wq == nullptr || q_out == nullptr)) return CASCADE_EINVAL;
