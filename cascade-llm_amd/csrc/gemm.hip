@@ -101,6 +101,7 @@ struct GemmArgs {
   int64_t kv_head_stride;
   int64_t slot0;
   int32_t tiles_m, tiles_n, tiles;
+  int32_t vec_out;  // row pitches and widths allow 16-byte output accesses
 };
 
 __device__ __forceinline__ float gemm_silu(float g) {
@@ -233,6 +234,192 @@ __device__ __forceinline__ void gemm_epilogue(
   }
 }
 
+// Vectorised epilogue.  The waves first write their fragments to LDS in
+// column-major order (a lane's 4 rows of one column are 8 contiguous bytes:
+// one ds_write_b64 per fragment), then read them back row-major with
+// ds_read_b64_tr_b16, which hands lane i of a 16-lane group row i of the 4
+// columns the group addresses, so every lane ends up with 8 consecutive
+// columns of one row and loads aux / stores results 16 bytes at a time.
+// Column stride 272 bytes: the fragment writes of 32 lanes fall in distinct
+// banks.  The values staged are those of the direct epilogue's rounding
+// points (bf16(acc), or the final SwiGLU product), so results are the same
+// bit for bit.
+constexpr int kStageCol = 136;  // bf16 per staged column (128 rows + 8 pad)
+
+__device__ __forceinline__ uint2 stage_read_tr(const uint16_t *p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+__device__ __forceinline__ float lo_f(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+template <int EPI, class T>
+__device__ __forceinline__ void gemm_epilogue_staged(
+    const GemmArgs &a, int tm, int tn, int wm, int wn, int lane, int wave,
+    const f32x4 (&acc)[T::FM][T::FN], uint16_t *stage) {
+  const int lr = lane & 15;
+  const int lq = lane >> 4;
+  const int arow = (T::BM / T::WM) * wm;
+  // items: 16 rows x 32 columns of the output tile; lane (g, i) of a wave
+  // takes row i, columns 8 g .. 8 g + 7 of the item.  Wave w takes items
+  // w, w + 4, ...
+  constexpr int TW = EPI == kGemmSwiglu || EPI == kGemmQkvRope ? 64 : kTileN;
+  constexpr int kItems = (T::BM / 16) * (TW / 32);
+  constexpr int kPer = kItems / kGemmWaves;
+  static_assert(kItems % kGemmWaves == 0, "whole items per wave");
+  const int g = lq, li = lr;
+  auto item_r0 = [&](int n) { return 16 * ((wave + kGemmWaves * n) / (TW / 32)); };
+  auto item_c0 = [&](int n) { return 32 * ((wave + kGemmWaves * n) % (TW / 32)) + 8 * g; };
+  const int64_t ncols = a.n0;  // output width (SwiGLU: n_half)
+
+  // ---- inputs the epilogue reads from memory, issued first so their
+  // latency overlaps the staging below
+  u32x4 in0[kPer], in1[kPer];
+#pragma unroll
+  for (int n = 0; n < kPer; ++n) {
+    const int64_t row = static_cast<int64_t>(tm) * T::BM + item_r0(n) + li;
+    in0[n] = in1[n] = u32x4{0u, 0u, 0u, 0u};
+    if (row >= a.m) continue;
+    if constexpr (EPI == kGemmResidual || EPI == kGemmMul) {
+      const int64_t col = static_cast<int64_t>(tn) * TW + item_c0(n);
+      if (col + 8 <= ncols)
+        in0[n] = *reinterpret_cast<const u32x4 *>(a.aux + row * a.ldy + col);
+    } else if constexpr (EPI == kGemmQkvRope) {
+      if (tn < (a.n0 + a.n1) / kGemmHead) {
+        const int64_t pos = a.pos0 + row;
+        in0[n] = *reinterpret_cast<const u32x4 *>(a.rope_cos + pos * kGemmHalfHead + item_c0(n));
+        in1[n] = *reinterpret_cast<const u32x4 *>(a.rope_sin + pos * kGemmHalfHead + item_c0(n));
+      }
+    }
+  }
+
+  // ---- fragments -> LDS (column-major, 4 rows per 8-byte piece)
+  if constexpr (EPI == kGemmSwiglu) {
+    // column c (0..63) holds bf16(silu(bf16(gate c)) * bf16(up c))
+#pragma unroll
+    for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::H; ++j) {
+        const int col = gemm_col<T>(wn, j, lr);
+        uint2 v;
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gt = round_bf16(acc[i][j][r]);
+          const float u = round_bf16(acc[i][j + T::H][r]);
+          o[r] = round_bf16(gemm_silu(gt)) * u;
+        }
+        v.x = pack_bf16x2(o[0], o[1]);
+        v.y = pack_bf16x2(o[2], o[3]);
+        *reinterpret_cast<uint2 *>(stage + col * kStageCol + arow + 16 * i + 4 * lq) = v;
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::FN; ++j) {
+        const int col = gemm_col<T>(wn, j, lr);
+        uint2 v;
+        v.x = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+        v.y = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+        *reinterpret_cast<uint2 *>(stage + col * kStageCol + arow + 16 * i + 4 * lq) = v;
+      }
+  }
+  __syncthreads();
+
+  // ---- LDS -> rows
+  const int qk = li >> 2, qq = li & 3;  // addressing lane k = 4 j + q of the group
+  auto read8 = [&](int r0, int c0, uint32_t (&w)[4]) {
+    // two transposed reads: columns c0 .. c0 + 3 and c0 + 4 .. c0 + 7
+    const uint2 lo = stage_read_tr(stage + (c0 + qk) * kStageCol + r0 + 4 * qq);
+    const uint2 hi = stage_read_tr(stage + (c0 + 4 + qk) * kStageCol + r0 + 4 * qq);
+    w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
+  };
+#pragma unroll
+  for (int n = 0; n < kPer; ++n) {
+    const int r0 = item_r0(n), c0 = item_c0(n);
+    const int64_t row = static_cast<int64_t>(tm) * T::BM + r0 + li;
+    // the transposed reads need every addressing lane: read before any
+    // lane drops out
+    uint32_t w[4], w2[4];
+    read8(r0, c0, w);  // bf16 pairs: columns c0 + 2 p, c0 + 2 p + 1
+    if constexpr (EPI == kGemmQkvRope) read8(r0, c0 + kGemmHalfHead, w2);  // d + 64
+    if (row >= a.m) continue;
+    if constexpr (EPI == kGemmQkvRope) {
+      const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
+      u32x4 oa, ob;
+      if (tn < hq + hk) {
+        const u32x4 cs = in0[n], sn = in1[n];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          // x*cos + rotate_half(x)*sin, products and sum rounded to bf16
+          const float xa0 = lo_f(w[p]), xa1 = hi_f(w[p]);
+          const float xb0 = lo_f(w2[p]), xb1 = hi_f(w2[p]);
+          const float c0f = lo_f(cs[p]), c1f = hi_f(cs[p]);
+          const float s0f = lo_f(sn[p]), s1f = hi_f(sn[p]);
+          oa[p] = pack_bf16x2(round_bf16(xa0 * c0f) + round_bf16(-xb0 * s0f),
+                              round_bf16(xa1 * c1f) + round_bf16(-xb1 * s1f));
+          ob[p] = pack_bf16x2(round_bf16(xb0 * c0f) + round_bf16(xa0 * s0f),
+                              round_bf16(xb1 * c1f) + round_bf16(xa1 * s1f));
+        }
+      } else {
+        oa = u32x4{w[0], w[1], w[2], w[3]};
+        ob = u32x4{w2[0], w2[1], w2[2], w2[3]};
+      }
+      uint16_t *dst;
+      if (tn < hq) {
+        dst = a.y + row * a.ldy + static_cast<int64_t>(tn) * kGemmHead;
+      } else if (tn < hq + hk) {
+        dst = a.k_out + (tn - hq) * a.kv_head_stride + (a.slot0 + row) * kGemmHead;
+      } else {
+        dst = a.v_out + (tn - hq - hk) * a.kv_head_stride + (a.slot0 + row) * kGemmHead;
+      }
+      *reinterpret_cast<u32x4 *>(dst + c0) = oa;
+      *reinterpret_cast<u32x4 *>(dst + c0 + kGemmHalfHead) = ob;
+    } else {
+      const int64_t col = static_cast<int64_t>(tn) * TW + c0;
+      const int64_t at = row * a.ldy + col;
+      u32x4 out;
+      if constexpr (EPI == kGemmStore || EPI == kGemmSwiglu) {
+        out = u32x4{w[0], w[1], w[2], w[3]};
+      } else {
+        const u32x4 aux = in0[n];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float v0 = lo_f(w[p]), v1 = hi_f(w[p]);
+          float o0, o1;
+          if constexpr (EPI == kGemmResidual) {
+            o0 = lo_f(aux[p]) + v0; o1 = hi_f(aux[p]) + v1;
+          } else if constexpr (EPI == kGemmSilu) {
+            o0 = gemm_silu(v0); o1 = gemm_silu(v1);
+          } else {  // kGemmMul
+            o0 = lo_f(aux[p]) * v0; o1 = hi_f(aux[p]) * v1;
+          }
+          out[p] = pack_bf16x2(o0, o1);
+        }
+      }
+      if (col + 8 <= ncols) {
+        *reinterpret_cast<u32x4 *>(a.y + at) = out;
+      } else if (col < ncols) {  // N tail: element stores (aux read element-wise)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (col + e >= ncols) break;
+          const uint32_t pr = w[e >> 1];
+          const float v = (e & 1) ? hi_f(pr) : lo_f(pr);
+          float o = v;
+          if constexpr (EPI == kGemmResidual) o = bf16_to_f32(a.aux[at + e]) + v;
+          else if constexpr (EPI == kGemmSilu) o = gemm_silu(v);
+          else if constexpr (EPI == kGemmMul) o = bf16_to_f32(a.aux[at + e]) * v;
+          a.y[at + e] = f32_to_bf16(o);
+        }
+      }
+    }
+  }
+}
+
 // Slab geometry (see the staging and layout notes at the top).
 template <int BK>
 struct DmaSlab {
@@ -258,8 +445,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   constexpr int XW = XI / kGemmWaves, WW = WI / kGemmWaves;  // per wave
   static_assert(XI % kGemmWaves == 0 && WI % kGemmWaves == 0, "whole loads per wave");
   constexpr int XB = T::BM * BK, WB = kTileN * BK;  // bf16 per slab buffer
-  // one array per slab buffer (X slab, then W slab)
-  __shared__ __attribute__((aligned(16))) uint16_t sb0[XB + WB];
+  // one array per slab buffer (X slab, then W slab); sb0 also holds the
+  // staged output tile of the vectorised epilogue
+  constexpr int kStage = kTileN * kStageCol;
+  __shared__ __attribute__((aligned(16))) uint16_t sb0[XB + WB > kStage ? XB + WB : kStage];
   __shared__ __attribute__((aligned(16))) uint16_t sb1[XB + WB];
   int tm, tn;
   if (!gemm_tile(a, tm, tn)) return;  // whole workgroup: no barrier skipped
@@ -371,20 +560,42 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   constexpr int kWaitLoads = (7 << 4) | (15 << 8);
   // slab s: this wave's loads of s done; barrier (everyone's slab s has
   // landed, slab s - 1 has been read); slab s + 1 into the other buffer;
-  // compute s.  The buffers are named directly at every call.
-  auto step = [&](int s, const uint16_t *cur, uint16_t *nxt) {
-    if (s >= slabs) return;
+  // compute s.  The buffers are named directly at every call, and the
+  // MFMAs sit in straight-line code (a branch around them makes the compiler
+  // copy every accumulator between AGPRs and VGPRs each iteration).
+  auto publish = [&]() {
     __builtin_amdgcn_s_waitcnt(kWaitLoads);
     __builtin_amdgcn_s_barrier();
-    if (s + 1 < slabs) load_slab(s + 1, nxt, nxt + XB);
-    compute(cur, cur + XB);
   };
   load_slab(0, sb0, sb0 + XB);
-  for (int s0 = 0; s0 < slabs; s0 += 2) {
-    step(s0, sb0, sb1);
-    step(s0 + 1, sb1, sb0);
+  int s = 0;
+  // sched_barrier: the next slab's loads go out before any of this slab's
+  // reads or MFMAs (the scheduler would otherwise sink them)
+  for (; s + 2 <= slabs; s += 2) {
+    publish();
+    load_slab(s + 1, sb1, sb1 + XB);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sb0, sb0 + XB);
+    publish();
+    // the last pair reloads its final slab into sb0 (never read again):
+    // the load stays unconditional and in range
+    load_slab(min(s + 2, slabs - 1), sb0, sb0 + XB);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sb1, sb1 + XB);
   }
-  gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
+  if (s < slabs) {  // odd slab count: the last slab sits in sb0
+    publish();
+    compute(sb0, sb0 + XB);
+  }
+  // no load may land in LDS after the workgroup has left (or in sb0 while
+  // it holds the staged tile)
+  __builtin_amdgcn_s_waitcnt(kWaitLoads);
+  if (EPI != kGemmF32 && a.vec_out) {
+    __builtin_amdgcn_s_barrier();  // every wave's loads landed, slabs read
+    gemm_epilogue_staged<EPI, T>(a, tm, tn, wm, wn, lane, wave, acc, sb0);
+  } else {
+    gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
+  }
 }
 
 template <int EPI, class T>
@@ -395,6 +606,12 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   a.tiles_m = static_cast<int32_t>(tiles_m);
   a.tiles_n = static_cast<int32_t>(tiles_n);
   a.tiles = static_cast<int32_t>(tiles);
+  // 16-byte output accesses need 16-byte aligned rows in every buffer the
+  // epilogue touches; otherwise the element-wise epilogue runs
+  auto ok16 = [](const void *p) { return p == nullptr || aligned16(p); };
+  a.vec_out = (a.ldy % 8 == 0) && ok16(a.y) && ok16(a.aux) && ok16(a.rope_cos) &&
+              ok16(a.rope_sin) && ok16(a.k_out) && ok16(a.v_out) &&
+              (a.kv_head_stride % 8 == 0);
   const int64_t grid = (tiles + kXcds - 1) / kXcds * kXcds;
   return launch_kernel(gemm_kernel<EPI, T>, dim3(static_cast<unsigned>(grid)),
                        dim3(kGemmThreads), 0, s, a);
