@@ -59,6 +59,12 @@ def parse_args():
     p.add_argument("--steps", type=int, default=32)
     p.add_argument("--warmup", type=int, default=4)
     p.add_argument("--context", type=int, default=32768)
+    p.add_argument("--granularity", default="matrix_group",
+                   choices=("layer", "matrix_group"),
+                   help="config 4 plan granularity (all weights resident)")
+    p.add_argument("--one-launch-layers", action="store_true",
+                   help="config 4: run each decoder layer as one launch "
+                        "(cascade_decode_layer_bf16; implies layer units)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-streamed", action="store_true")
     p.add_argument("--streamed-steps", type=int, default=7)
@@ -80,6 +86,7 @@ def parse_args():
 
 PROBE_COPY_BYTES = 256 << 20
 TRAFFIC_FILE = ROOT / "profiles" / "gate_up_traffic.txt"
+LAYER_TRAFFIC_FILE = ROOT / "profiles" / "decode_layer_traffic.txt"
 
 
 def counter_probe():
@@ -108,11 +115,11 @@ def counter_probe():
     log("probe: 12 gate/up launches done")
 
 
-def measured_traffic():
-    """HBM bytes per gate/up launch from the committed counter summary."""
+def measured_traffic(path):
+    """HBM bytes per launch from a committed counter summary."""
 
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
+        for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch="):
                 return int(line.split("=", 1)[1])
     except OSError:
@@ -136,6 +143,17 @@ def gate_up_bytes():
     return 2 * INTER * HIDDEN * 2 + HIDDEN * 2 + HIDDEN * 2 + INTER * 2
 
 
+def layer_bytes(length):
+    """Algorithmic HBM bytes of one decoder layer at attended length L:
+    the seven weight matrices, two norm weights, K and V rows [0, L) read,
+    the new K / V row written, the hidden state read and written."""
+
+    weights = 436207616
+    norms = 2 * HIDDEN * 2
+    kv = length * KV_BYTES_PER_POS_LAYER + KV_BYTES_PER_POS_LAYER
+    return weights + norms + kv + 2 * HIDDEN * 2
+
+
 def resident_decode(args):
     import torch
     from layer_streaming import (
@@ -147,12 +165,14 @@ def resident_decode(args):
     )
 
     dev = torch.device("cuda:0")
-    plan = build_llama31_8b_plan("matrix_group", stream_vocab=False)
+    granularity = "layer" if args.one_launch_layers else args.granularity
+    plan = build_llama31_8b_plan(granularity, stream_vocab=False)
     log("config 4: drawing 16 GB of synthetic weights in HBM")
     resident = ResidentDeviceArena(plan, None, dev, fill=False).fill_random(args.seed)
     runtime = ResidentTransformerRuntime(plan, None, resident, dev,
                                          synchronize=False).fill_random(args.seed)
-    executor = Llama31DecodeExecutor(Llama31Config(), resident, top_k=10)
+    executor = Llama31DecodeExecutor(Llama31Config(), resident, top_k=10,
+                                     one_launch_layers=args.one_launch_layers)
     total = args.context + args.warmup + args.steps + 1
     executor.reserve(total)
     cache = executor.kv_cache
@@ -169,8 +189,12 @@ def resident_decode(args):
             state = executor.finish(runtime.run(executor, executor.begin(token)))
             token = state.topk_indices.reshape(1, -1)[:, :1]
         torch.cuda.synchronize(dev)
+        # the dominant launch: the whole layer where it runs as one launch,
+        # else the gate/up GEMV
+        group = "layer" if executor.fused_layer else "gate_up"
+        log("config 4: {} units, timing {} launches".format(granularity, group))
         stride = args.roofline_stride
-        executor.instrument("gate_up", (args.steps * LAYERS + stride - 1) // stride,
+        executor.instrument(group, (args.steps * LAYERS + stride - 1) // stride,
                             stride=stride, offset=(LAYERS // 2) % stride)
         log("config 4: timing {} decode steps".format(args.steps))
         start = time.perf_counter()
@@ -179,15 +203,17 @@ def resident_decode(args):
             token = state.topk_indices.reshape(1, -1)[:, :1]
         torch.cuda.synchronize(dev)
         elapsed = time.perf_counter() - start
-    gate_up_ms = executor.kernel_times_ms("gate_up")
+    timed_ms = executor.kernel_times_ms(group)
     ms_per_step = elapsed * 1000.0 / args.steps
     mean_context = args.context + args.warmup + (args.steps - 1) / 2.0
     result = {
         "ms_per_step": ms_per_step,
         "tokens": args.steps,
-        "gate_up_launches": len(gate_up_ms),
-        "gate_up_avg_us": 1000.0 * statistics.mean(gate_up_ms),
-        "gate_up_median_us": 1000.0 * statistics.median(gate_up_ms),
+        "timed_group": group,
+        "timed_launches": len(timed_ms),
+        "timed_avg_us": 1000.0 * statistics.mean(timed_ms),
+        "timed_median_us": 1000.0 * statistics.median(timed_ms),
+        "mean_attended": mean_context + 1,
         "token_hbm_bytes": token_bytes(int(mean_context)),
         "last_token": int(token.reshape(-1)[0]),
     }
@@ -451,8 +477,18 @@ def main():
         return
     resident = resident_decode(args)
     ms = resident["ms_per_step"]
-    gu_us = resident["gate_up_avg_us"]
-    achieved = gate_up_bytes() / (gu_us * 1e-6) / 1e9
+    t_us = resident["timed_avg_us"]
+    if resident["timed_group"] == "layer":
+        kernel = ("decode_layer_kernel: one decoder layer per launch (q|k|v, "
+                  "attention, merge, o, gate/up, down), attended length {:.1f}"
+                  .format(resident["mean_attended"]))
+        per_launch = layer_bytes(resident["mean_attended"])
+        traffic = measured_traffic(LAYER_TRAFFIC_FILE)
+    else:
+        kernel = "gate_up_swiglu GEMV (gemv_kernel<8,2,4,3,true>), 2x[14336,4096] bf16"
+        per_launch = gate_up_bytes()
+        traffic = measured_traffic(TRAFFIC_FILE)
+    achieved = per_launch / (t_us * 1e-6) / 1e9
     line = {
         "metric": "decode ms/token, 8B-shape bf16 b=1; achieved HBM & H2D GB/s vs peak",
         "value": round(ms, 4),
@@ -471,6 +507,8 @@ def main():
                         "all weights HBM-resident, batch 1 greedy decode at "
                         "context {}".format(args.context),
             "context": args.context,
+            "units": "layer (one launch each)" if args.one_launch_layers
+                     else args.granularity,
             "batch": 1,
             "layers": LAYERS,
             "vocab": VOCAB,
@@ -481,16 +519,17 @@ def main():
         "token_hbm_frac_of_peak": round(
             resident["token_hbm_bytes"] / 1e9 / (ms / 1e3) / HBM_PEAK_GBPS, 4),
         "roofline": {
-            "kernel": "gate_up_swiglu GEMV (gemv_kernel<8,2,4,3,true>), 2x[14336,4096] bf16",
+            "kernel": kernel,
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(),
-            "bytes_per_launch": gate_up_bytes(),
-            "avg_launch_us": round(gu_us, 3),
-            "launches_timed": resident["gate_up_launches"],
+            "traffic": traffic,
+            "bytes_per_launch": int(per_launch),
+            "avg_launch_us": round(t_us, 3),
+            "median_launch_us": round(resident["timed_median_us"], 3),
+            "launches_timed": resident["timed_launches"],
         },
     }
     if not args.no_streamed:

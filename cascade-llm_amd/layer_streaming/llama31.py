@@ -200,6 +200,9 @@ _EXPECTED = {
 # Kernel groups whose entry point launches exactly one kernel.
 _KERNEL_TIMED_GROUPS = frozenset((
     "gate_up", "qkv", "o_proj", "down_proj",
+    # one-launch decoder layer (cascade_decode_layer_bf16 records the events
+    # on its stream around the cooperative launch)
+    "layer",
     # prefill (S > 1 tokens): one MFMA GEMM / attention launch per unit
     "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_gate", "gemm_up", "gemm_down",
     "gemm_lm_head", "prefill_attention"))
@@ -210,7 +213,7 @@ class Llama31DecodeExecutor:
     multi-token prefill, then one-token decode calls)."""
 
     def __init__(self, config, resident, kv_cache=None, vocab_runtime=None,
-                 top_k=10, return_full_logits=False):
+                 top_k=10, return_full_logits=False, one_launch_layers=False):
         _hip.load()  # no kernels, no executor
         layers = getattr(resident, "plan", None)
         layers = layers.num_layers if layers is not None else 32
@@ -274,6 +277,7 @@ class Llama31DecodeExecutor:
         self._k_silu_gemm = lib.cascade_gate_silu_gemm_bf16
         self._k_mul_gemm = lib.cascade_up_mul_gemm_bf16
         self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
+        self._k_layer = lib.cascade_decode_layer_bf16
         self._batched = False
         self._first_slot = 0
         self._unit_cache = {}
@@ -286,6 +290,13 @@ class Llama31DecodeExecutor:
         self._attn_ws = None
         self._attn_ws_len = 0
         self._head_ws = None
+        # One-launch decoder layer (cascade_decode_layer_bf16) for
+        # single-token "layer" units, on request: None = try at the first
+        # such unit, True = running, False = the per-stage kernels (the
+        # default; also where the device cannot run the one-launch kernel).
+        self.fused_layer = None if one_launch_layers else False
+        self._layer_ws = None
+        self._layer_err = None
         self._ensure_buffers(1)
 
     # ------------------------------------------------------------ buffers
@@ -464,9 +475,68 @@ class Llama31DecodeExecutor:
             _hip.check("cascade_gemv_residual_bf16", rc)
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
 
+    def _layer_one_launch(self, layer, ptrs, state, stream):
+        """A whole single-token layer unit in one launch
+        (cascade_decode_layer_bf16); False when it does not apply here."""
+
+        if self.fused_layer is False or len(state.positions) != 1:
+            return False
+        names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                 "down_proj")
+        if any(n not in ptrs for n in names):
+            return False
+        if self._layer_ws is None:
+            self._layer_ws = torch.zeros(_hip.decode_layer_workspace_bytes(),
+                                         dtype=torch.uint8, device=self.device)
+        slot = self._first_slot
+        pos = state.positions[0]
+        half = self.head_dim // 2
+        norm_in, norm_post = self._norm_ptrs[layer]
+        ws = self._layer_ws
+        ev = self._mark_begin("layer")
+        rc = self._k_layer(
+            *(ptrs[n] for n in names), norm_in, norm_post, self.eps,
+            state.hidden_states.data_ptr(),
+            self.rope.cos.data_ptr() + 2 * half * pos,
+            self.rope.sin.data_ptr() + 2 * half * pos,
+            self._kv_pointer(layer, 0, 0), self._kv_pointer(layer, 1, 0),
+            self.kv_cache.head_stride, slot + 1, self.scale, ws.data_ptr(),
+            ws.numel(), stream)
+        self._mark_end("layer", ev, rc)
+        if rc == _hip.ESHAPE and self.fused_layer is None:
+            self.fused_layer = False
+            return False
+        _hip.check("cascade_decode_layer_bf16", rc)
+        self.fused_layer = True
+        self.kv_cache.set_length(layer, slot + 1)
+        if self.capture is not None:
+            self.capture.append((layer, state.hidden_states.detach().clone()))
+        return True
+
+    def _check_layer_errors(self):
+        """Surface a grid-barrier timeout of the one-launch layer.  Non-
+        blocking: the error word is copied to pinned memory behind each
+        token's work and read one token later, once its event completed."""
+
+        if self._layer_ws is None or self._layer_ws.device.type != "cuda":
+            return
+        if self._layer_err is None:
+            self._layer_err = (torch.zeros(1, dtype=torch.int32, pin_memory=True),
+                               torch.cuda.Event())
+        host, event = self._layer_err
+        if event.query() and int(host[0]) != 0:
+            self._layer_ws.zero_()
+            host.zero_()
+            raise RuntimeError(
+                "cascade_decode_layer_bf16: a grid barrier timed out (not all "
+                "workgroups resident); the results of the last tokens are invalid")
+        word = _hip.DECODE_LAYER_ERROR
+        host.copy_(self._layer_ws[word:word + 4].view(torch.int32), non_blocking=True)
+        event.record()
+
     def instrument(self, name, launches, stride=1, offset=0):
-        """Time ``launches`` launches of kernel group ``name`` ("gate_up",
-        "qkv", "attention", "o_proj", "down_proj", "lm_head"): of the group's
+        """Time ``launches`` launches of kernel group ``name`` ("layer",
+        "gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head"): of the group's
         coming launches, numbers offset, offset + stride, ...; read them back
         with :meth:`kernel_times_ms` after a synchronize.  The one-kernel
         groups (gate_up, qkv, o_proj, down_proj) bind the events to the
@@ -688,6 +758,8 @@ class Llama31DecodeExecutor:
         if self._batched:
             return self._call_batched(layer, op, ptrs, state, stream)
         if op == "layer":
+            if self._layer_one_launch(layer, ptrs, state, stream):
+                return state
             self._qkv(layer, ptrs, state, stream)
             self._attention_o(layer, ptrs, state, stream)
             self._gate_up(layer, ptrs, state, stream)
@@ -709,6 +781,7 @@ class Llama31DecodeExecutor:
         return state
 
     def finish(self, state):
+        self._check_layer_errors()
         rows = self._token_rows(state)
         count = rows.shape[0]
         stream = self._stream()

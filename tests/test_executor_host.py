@@ -146,6 +146,27 @@ class FakeKernels:
         return 0
 
 
+    def layer(self, wq, wk, wv, wo, wg, wu, wd, norm_in, norm_post, eps, x,
+              cos, sin, k0, v0, stride, length, scale, ws, ws_bytes, stream):
+        # the one-launch layer: the five per-stage doubles through the same
+        # pointers (new K / V at slot length - 1, x updated in place)
+        before = len(self.calls)
+        h, i, kv, dim = 4096, 14336, 1024, 128
+        slot = length - 1
+        q = torch.empty(h, dtype=BF16)
+        attn = torch.empty(h, dtype=BF16)
+        inter = torch.empty(i, dtype=BF16)
+        self.qkv(wq, wk, wv, h, kv, kv, h, x, norm_in, eps, cos, sin, q.data_ptr(),
+                 k0 + 2 * slot * dim, v0 + 2 * slot * dim, stride, stream)
+        self.attention(q.data_ptr(), k0, v0, stride, length, 32, 8, dim, scale,
+                       attn.data_ptr(), 0, 0, stream)
+        self.residual(wo, attn.data_ptr(), x, x, h, h, stream)
+        self.swiglu(wg, wu, i, h, x, norm_post, eps, inter.data_ptr(), stream)
+        self.residual(wd, inter.data_ptr(), x, x, h, i, stream)
+        del self.calls[before:]
+        self.calls.append("layer")
+        return 0
+
     # -------------------------------------- batched (S > 1) entry points
 
     def qkv_gemm(self, x, m, wq, wk, wv, nq, nk, nv, k, cos, sin, positions,
@@ -262,7 +283,7 @@ def exact_oracle(monkeypatch):
     monkeypatch.setattr(_hip, "require_device", lenient_require)
 
 
-def make_executor(monkeypatch, plan, store):
+def make_executor(monkeypatch, plan, store, one_launch_layers=False):
     fakes = FakeKernels()
 
     def gather(table, ids, out, error_flag=None, stream=None):
@@ -272,7 +293,8 @@ def make_executor(monkeypatch, plan, store):
     monkeypatch.setattr(_hip, "embedding_gather", gather)
     cache = SimpleKVCache(LAYERS, device="cpu")
     ex = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
-                               HostResident(plan, store), kv_cache=cache, top_k=5)
+                               HostResident(plan, store), kv_cache=cache, top_k=5,
+                               one_launch_layers=one_launch_layers)
     ex._stream = lambda: 0
     ex._k_qkv, ex._k_attn, ex._k_residual = fakes.qkv, fakes.attention, fakes.residual
     ex._k_swiglu, ex._k_silu, ex._k_mul = fakes.swiglu, fakes.silu, fakes.mul
@@ -281,6 +303,7 @@ def make_executor(monkeypatch, plan, store):
     ex._k_gemm_residual, ex._k_swiglu_gemm = fakes.gemm_residual, fakes.swiglu_gemm
     ex._k_silu_gemm, ex._k_mul_gemm = fakes.silu_gemm, fakes.mul_gemm
     ex._k_f32_gemm = fakes.f32_gemm
+    ex._k_layer = fakes.layer
     return ex, fakes
 
 
@@ -291,15 +314,20 @@ def run_units(plan, store, executor, state):
     return state
 
 
-@pytest.mark.parametrize("granularity", ["matrix_group", "matrix", "layer"])
+@pytest.mark.parametrize("granularity", ["matrix_group", "matrix", "layer",
+                                         "layer_one_launch"])
 def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
                                                         exact_oracle, granularity):
-    plan = build_llama31_8b_plan(granularity, num_layers=LAYERS)
+    # layer_one_launch: layer units, each decode step of a layer one launch
+    # of cascade_decode_layer_bf16 (its double below)
+    one_launch = granularity == "layer_one_launch"
+    plan = build_llama31_8b_plan("layer" if one_launch else granularity,
+                                 num_layers=LAYERS)
     # every granularity packs the arena identically, so one store serves all
     for key in plan.tensors:
         assert plan.tensor_host_offset(key) == weights.plan.tensor_host_offset(key)
     store = weights
-    executor, fakes = make_executor(monkeypatch, plan, store)
+    executor, fakes = make_executor(monkeypatch, plan, store, one_launch)
     oracle = ref.OracleLlama(store.tensor, LAYERS)
     prompt = [7, 99, 1234, 5, 128255, 0]
     expected_logits, ev, ei = oracle.step(prompt, 5)
@@ -323,10 +351,13 @@ def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
         k, v = executor.kv_cache.entries[layer]
         assert torch.equal(k[0], oracle.caches[layer]["k"])
         assert torch.equal(v[0], oracle.caches[layer]["v"])
-    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5}[granularity]
+    # (a layer unit of one token is one launch of the whole layer)
+    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5,
+                 "layer_one_launch": 1}[granularity]
     # prefill, per layer: input norm, q/k/v GEMM(s), causal attention,
     # o GEMM, post-attention norm, MLP GEMM(s), down GEMM
-    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7}[granularity]
+    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7,
+                   "layer_one_launch": 7}[granularity]
     # decode, per layer and token: qkv launch(es), attention, o residual,
     # MLP, down; finish: one rmsnorm, then (prefill) one logits GEMM over
     # every position and one LM-head launch for the last

@@ -99,6 +99,11 @@ def copy_weights(src, dst):
 
 
 def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
+    # "layer_one_launch": layer units, each run as one launch of the whole
+    # decoder layer (cascade_decode_layer_bf16) at decode
+    one_launch = granularity == "layer_one_launch"
+    if one_launch:
+        granularity = "layer"
     plan = build_llama31_8b_plan(granularity, stream_vocab=(vocab_mode == "streamed"),
                                  num_layers=LAYERS)
     store = create_weight_store(plan, store_mode)
@@ -113,7 +118,8 @@ def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
         vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
     executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
                                      resident, vocab_runtime=vocab, top_k=TOP_K,
-                                     return_full_logits=True)
+                                     return_full_logits=True,
+                                     one_launch_layers=one_launch)
     return store, runtime, executor
 
 
@@ -163,6 +169,7 @@ CONFIGS = [
     ("full_pinned", "layer", "resident", "double"),
     ("pinned_staging", "matrix_group", "resident", "double"),
     ("full_pinned", "matrix_group", "resident", "resident"),
+    ("full_pinned", "layer_one_launch", "resident", "resident"),
 ]
 
 
