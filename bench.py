@@ -59,12 +59,11 @@ def parse_args():
     p.add_argument("--steps", type=int, default=32)
     p.add_argument("--warmup", type=int, default=4)
     p.add_argument("--context", type=int, default=32768)
-    p.add_argument("--granularity", default="matrix_group",
-                   choices=("layer", "matrix_group"),
-                   help="config 4 plan granularity (all weights resident)")
-    p.add_argument("--one-launch-layers", action="store_true",
-                   help="config 4: run each decoder layer as one launch "
-                        "(cascade_decode_layer_bf16; implies layer units)")
+    p.add_argument("--layer-mode", default="stages", choices=("stages", "mlp", "one"),
+                   help="config 4 launches per decoder layer: stages = six "
+                        "per-stage kernels (matrix_group units); mlp = q|k|v and "
+                        "attention per stage, o_proj..down_proj as one launch "
+                        "(layer units); one = the whole layer as one launch")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-streamed", action="store_true")
     p.add_argument("--streamed-steps", type=int, default=7)
@@ -87,6 +86,7 @@ def parse_args():
 PROBE_COPY_BYTES = 256 << 20
 TRAFFIC_FILE = ROOT / "profiles" / "gate_up_traffic.txt"
 LAYER_TRAFFIC_FILE = ROOT / "profiles" / "decode_layer_traffic.txt"
+MLP_TRAFFIC_FILE = ROOT / "profiles" / "decode_mlp_traffic.txt"
 
 
 def counter_probe():
@@ -143,6 +143,15 @@ def gate_up_bytes():
     return 2 * INTER * HIDDEN * 2 + HIDDEN * 2 + HIDDEN * 2 + INTER * 2
 
 
+def mlp_bytes():
+    """Algorithmic HBM bytes of the one-launch MLP half of a layer: o_proj,
+    gate, up and down weights, the post-attention norm weight, the attention
+    output read, the hidden state read and written."""
+
+    weights = HIDDEN * HIDDEN * 2 + 3 * INTER * HIDDEN * 2
+    return weights + HIDDEN * 2 + HIDDEN * 2 + 2 * HIDDEN * 2
+
+
 def layer_bytes(length):
     """Algorithmic HBM bytes of one decoder layer at attended length L:
     the seven weight matrices, two norm weights, K and V rows [0, L) read,
@@ -165,14 +174,14 @@ def resident_decode(args):
     )
 
     dev = torch.device("cuda:0")
-    granularity = "layer" if args.one_launch_layers else args.granularity
+    granularity = "matrix_group" if args.layer_mode == "stages" else "layer"
     plan = build_llama31_8b_plan(granularity, stream_vocab=False)
     log("config 4: drawing 16 GB of synthetic weights in HBM")
     resident = ResidentDeviceArena(plan, None, dev, fill=False).fill_random(args.seed)
     runtime = ResidentTransformerRuntime(plan, None, resident, dev,
                                          synchronize=False).fill_random(args.seed)
     executor = Llama31DecodeExecutor(Llama31Config(), resident, top_k=10,
-                                     one_launch_layers=args.one_launch_layers)
+                                     layer_mode=args.layer_mode)
     total = args.context + args.warmup + args.steps + 1
     executor.reserve(total)
     cache = executor.kv_cache
@@ -191,7 +200,9 @@ def resident_decode(args):
         torch.cuda.synchronize(dev)
         # the dominant launch: the whole layer where it runs as one launch,
         # else the gate/up GEMV
-        group = "layer" if executor.fused_layer else "gate_up"
+        fused = executor._fused_ok is True
+        group = {"one": "layer", "mlp": "mlp"}.get(args.layer_mode, "gate_up")
+        group = group if fused else "gate_up"
         log("config 4: {} units, timing {} launches".format(granularity, group))
         stride = args.roofline_stride
         executor.instrument(group, (args.steps * LAYERS + stride - 1) // stride,
@@ -210,6 +221,7 @@ def resident_decode(args):
         "ms_per_step": ms_per_step,
         "tokens": args.steps,
         "timed_group": group,
+        "units": granularity,
         "timed_launches": len(timed_ms),
         "timed_avg_us": 1000.0 * statistics.mean(timed_ms),
         "timed_median_us": 1000.0 * statistics.median(timed_ms),
@@ -478,7 +490,12 @@ def main():
     resident = resident_decode(args)
     ms = resident["ms_per_step"]
     t_us = resident["timed_avg_us"]
-    if resident["timed_group"] == "layer":
+    if resident["timed_group"] == "mlp":
+        kernel = ("decode_layer_kernel<true>: o_proj + residual, RMSNorm + "
+                  "gate/up + SwiGLU, down_proj + residual of one layer in one launch")
+        per_launch = mlp_bytes()
+        traffic = measured_traffic(MLP_TRAFFIC_FILE)
+    elif resident["timed_group"] == "layer":
         kernel = ("decode_layer_kernel: one decoder layer per launch (q|k|v, "
                   "attention, merge, o, gate/up, down), attended length {:.1f}"
                   .format(resident["mean_attended"]))
@@ -507,8 +524,10 @@ def main():
                         "all weights HBM-resident, batch 1 greedy decode at "
                         "context {}".format(args.context),
             "context": args.context,
-            "units": "layer (one launch each)" if args.one_launch_layers
-                     else args.granularity,
+            "units": resident["units"],
+            "layer_launches": {"stages": "6 per-stage kernels",
+                               "mlp": "q|k|v, attention (+ split merge), one MLP launch",
+                               "one": "one launch per layer"}[args.layer_mode],
             "batch": 1,
             "layers": LAYERS,
             "vocab": VOCAB,

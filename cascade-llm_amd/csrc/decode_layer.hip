@@ -354,10 +354,12 @@ __device__ __forceinline__ void attn_wg_merge(LayerShared &sh, int t) {
 }
 
 // ------------------------------------------------------------------ workers
+template <bool MLP>
 __device__ __forceinline__ void layer_worker(const LayerArgs &a, LayerShared &sh,
                                              int blk, int wave, int lane) {
   const int wi = wave - 1;
 
+  if constexpr (!MLP) {
   // ------------------------------------------------------------ A: q|k|v
   {
     // pair p = b + 256 k (k < 12): rows (d, d + 64) of head p / 64,
@@ -538,6 +540,7 @@ __device__ __forceinline__ void layer_worker(const LayerArgs &a, LayerShared &sh
     if (sp.nb > 0) attn_wg_merge(sh, wave * kWave + lane);
     __syncthreads();  // S5: split partials to the control wave
   }
+  }  // !MLP
 
   // D rows r(m) = b + 256 m (m < 16), F rows the same: worker w takes
   // m = w, w + 7 and, for w < 2, w + 14.  Their weights and gate/up pair 0
@@ -555,10 +558,12 @@ __device__ __forceinline__ void layer_worker(const LayerArgs &a, LayerShared &sh
     load_row<kKcH>(a.wu + i * kLH, lane, w[1]);
   };
   u32x4 pa[2][kKcH], pb[2][kKcH];
-  __syncthreads();  // S6: grid barrier 2 passed (the control wave merges)
-  __syncthreads();  // S7: the control wave's merge loads are out
-  load_pair(0, pa);
-  __syncthreads();  // S8: grid barrier 3 passed
+  if constexpr (!MLP) {
+    __syncthreads();  // S6: grid barrier 2 passed (the control wave merges)
+    __syncthreads();  // S7: the control wave's merge loads are out
+    load_pair(0, pa);
+    __syncthreads();  // S8: grid barrier 3 passed
+  }
 
   // ------------------------------------------------------------ D: o_proj
   __syncthreads();  // S9: attn staged
@@ -571,8 +576,14 @@ __device__ __forceinline__ void layer_worker(const LayerArgs &a, LayerShared &sh
     }
   }
   __syncthreads();  // S10: results to the control wave
-  load_pair(1, pb);
-  __syncthreads();  // S11: grid barrier 4 passed
+  if constexpr (MLP) {
+    load_pair(0, pa);
+    __syncthreads();  // S11: grid barrier 4 passed
+    load_pair(1, pb);
+  } else {
+    load_pair(1, pb);
+    __syncthreads();  // S11: grid barrier 4 passed
+  }
 
   // ------------------------------------------------------------ E: gate/up
   __syncthreads();  // S12: normalised x staged
@@ -621,6 +632,7 @@ __device__ __forceinline__ void layer_worker(const LayerArgs &a, LayerShared &sh
 }
 
 // ------------------------------------------------------------ control wave
+template <bool MLP>
 __device__ __forceinline__ void layer_control(const LayerArgs &a, LayerShared &sh,
                                               int blk, int lane) {
   // generation of the last barrier passed (lane 0): the value found at
@@ -641,6 +653,7 @@ __device__ __forceinline__ void layer_control(const LayerArgs &a, LayerShared &s
     __syncthreads();
   };
 
+  if constexpr (!MLP) {
   // ------------------------------------------------------------ A
   ctl_stage<kLH, kLThreads>(a.x, a.norm_in, a.eps, sh.xs, lane);
   __syncthreads();  // S1
@@ -721,6 +734,7 @@ __device__ __forceinline__ void layer_control(const LayerArgs &a, LayerShared &s
   }
   arrive();
   wait();  // S8
+  }  // !MLP
 
   // ------------------------------------------------------------ D
   ctl_stage<kLH, kLThreads>(a.attn, nullptr, 0.0f, sh.xs, lane);
@@ -751,15 +765,19 @@ __device__ __forceinline__ void layer_control(const LayerArgs &a, LayerShared &s
     st_agent16(a.x + blk + kLGrid * lane, f32_to_bf16(round_bf16(xr + round_bf16(sh.out[lane]))));
 }
 
+// MLP = false: the whole layer (stages A..F).  MLP = true: stages D..F
+// only, from an attention output the caller computed (a.attn): o_proj +
+// residual, RMSNorm + gate/up + SwiGLU, down_proj + residual.
+template <bool MLP>
 __global__ __launch_bounds__(kLThreads) void decode_layer_kernel(LayerArgs a) {
   __shared__ LayerShared sh;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const int blk = static_cast<int>(blockIdx.x);
   if (wave == 0)
-    layer_control(a, sh, blk, lane);
+    layer_control<MLP>(a, sh, blk, lane);
   else
-    layer_worker(a, sh, blk, wave, lane);
+    layer_worker<MLP>(a, sh, blk, wave, lane);
 }
 
 struct DeviceInfo {
@@ -782,7 +800,7 @@ bool layer_device_ok() {
     int cus = 0, blocks = 0;
     const bool ok =
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_layer_kernel,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_layer_kernel<false>,
                                                      kLThreads, 0) == hipSuccess &&
         blocks >= 1 && cus == kLGrid;
     info.checked = ok ? 1 : -1;
@@ -845,6 +863,34 @@ extern "C" int cascade_decode_layer_bf16(
   a.part_ml = reinterpret_cast<float *>(ws + kWsMl);
   a.part_acc = reinterpret_cast<float *>(ws + kWsAcc);
   a.sync = reinterpret_cast<uint32_t *>(ws);
-  return launch_kernel(decode_layer_kernel, dim3(kLGrid), dim3(kLThreads), 0,
+  return launch_kernel(decode_layer_kernel<false>, dim3(kLGrid), dim3(kLThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
+}
+
+extern "C" int cascade_decode_mlp_bf16(const void *wo, const void *w_gate,
+                                       const void *w_up, const void *w_down,
+                                       const void *norm_post, float eps,
+                                       const void *attn, void *x, void *workspace,
+                                       size_t workspace_bytes, void *stream) {
+  const void *in[] = {wo, w_gate, w_up, w_down, norm_post, attn, x, workspace};
+  for (const void *p : in)
+    if (p == nullptr) return CASCADE_EINVAL;
+  for (const void *p : in)
+    if (!aligned16(p)) return CASCADE_EALIGN;
+  if (workspace_bytes < kWsBytes) return CASCADE_EWORKSPACE;
+  if (!layer_device_ok()) return CASCADE_ESHAPE;
+  char *ws = static_cast<char *>(workspace);
+  LayerArgs a{};
+  a.wo = static_cast<const uint16_t *>(wo);
+  a.wg = static_cast<const uint16_t *>(w_gate);
+  a.wu = static_cast<const uint16_t *>(w_up);
+  a.wd = static_cast<const uint16_t *>(w_down);
+  a.norm_post = static_cast<const uint16_t *>(norm_post);
+  a.eps = eps;
+  a.x = static_cast<uint16_t *>(x);
+  a.attn = const_cast<uint16_t *>(static_cast<const uint16_t *>(attn));
+  a.inter = reinterpret_cast<uint16_t *>(ws + kWsInter);
+  a.sync = reinterpret_cast<uint32_t *>(ws);
+  return launch_kernel(decode_layer_kernel<true>, dim3(kLGrid), dim3(kLThreads), 0,
                        static_cast<hipStream_t>(stream), a);
 }

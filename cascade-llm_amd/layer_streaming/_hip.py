@@ -64,6 +64,8 @@ _SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _I64,
          _I64, _F, _P, _SZ, _P],
     ),
+    "cascade_decode_mlp_bf16": (
+        _INT, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
     "cascade_gemm_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "cascade_gemm_residual_bf16": (
         _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
@@ -634,6 +636,32 @@ def decode_layer(w, x, rope_cos, rope_sin, k_cache, v_cache, kv_head_stride,
         stream_handle(stream))
     if code not in (0, ESHAPE):
         _check("cascade_decode_layer_bf16", code)
+    return code
+
+
+def decode_mlp(w, attn, x, workspace, eps, stream=None):
+    """o_proj + residual, RMSNorm + gate/up + SwiGLU, down_proj + residual
+    of one token in one launch; x [4096] bf16 updated in place.  ``w`` maps
+    o, gate, up, down and ln2.  Returns the library status (0, or
+    CASCADE_ESHAPE where the device cannot run the kernel)."""
+
+    shape = DECODE_LAYER_SHAPE
+    h, i = shape["hidden"], shape["intermediate"]
+    for name, rows, k in (("o", h, h), ("gate", i, h), ("up", i, h), ("down", h, i)):
+        _bf16(w[name], name, rows * k)
+        if tuple(w[name].shape) != (rows, k):
+            raise ValueError("{} must be [{}, {}]".format(name, rows, k))
+    _bf16(w["ln2"], "ln2", h)
+    _bf16(attn, "attn", h)
+    _bf16(x, "x", h)
+    require_device(workspace, "workspace", torch.uint8)
+    code = load().cascade_decode_mlp_bf16(
+        w["o"].data_ptr(), w["gate"].data_ptr(), w["up"].data_ptr(),
+        w["down"].data_ptr(), w["ln2"].data_ptr(), float(eps), attn.data_ptr(),
+        x.data_ptr(), workspace.data_ptr(), workspace.numel(),
+        stream_handle(stream))
+    if code not in (0, ESHAPE):
+        _check("cascade_decode_mlp_bf16", code)
     return code
 
 

@@ -200,9 +200,8 @@ _EXPECTED = {
 # Kernel groups whose entry point launches exactly one kernel.
 _KERNEL_TIMED_GROUPS = frozenset((
     "gate_up", "qkv", "o_proj", "down_proj",
-    # one-launch decoder layer (cascade_decode_layer_bf16 records the events
-    # on its stream around the cooperative launch)
-    "layer",
+    # one-launch decoder layer and its MLP half
+    "layer", "mlp",
     # prefill (S > 1 tokens): one MFMA GEMM / attention launch per unit
     "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_gate", "gemm_up", "gemm_down",
     "gemm_lm_head", "prefill_attention"))
@@ -213,7 +212,7 @@ class Llama31DecodeExecutor:
     multi-token prefill, then one-token decode calls)."""
 
     def __init__(self, config, resident, kv_cache=None, vocab_runtime=None,
-                 top_k=10, return_full_logits=False, one_launch_layers=False):
+                 top_k=10, return_full_logits=False, layer_mode="stages"):
         _hip.load()  # no kernels, no executor
         layers = getattr(resident, "plan", None)
         layers = layers.num_layers if layers is not None else 32
@@ -278,6 +277,7 @@ class Llama31DecodeExecutor:
         self._k_mul_gemm = lib.cascade_up_mul_gemm_bf16
         self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
         self._k_layer = lib.cascade_decode_layer_bf16
+        self._k_mlp = lib.cascade_decode_mlp_bf16
         self._batched = False
         self._first_slot = 0
         self._unit_cache = {}
@@ -290,11 +290,16 @@ class Llama31DecodeExecutor:
         self._attn_ws = None
         self._attn_ws_len = 0
         self._head_ws = None
-        # One-launch decoder layer (cascade_decode_layer_bf16) for
-        # single-token "layer" units, on request: None = try at the first
-        # such unit, True = running, False = the per-stage kernels (the
-        # default; also where the device cannot run the one-launch kernel).
-        self.fused_layer = None if one_launch_layers else False
+        # Launches of a single-token "layer" unit (decode): "stages" = the
+        # per-stage kernels (six launches); "mlp" = q|k|v and attention per
+        # stage, o_proj .. down_proj in one launch (four); "one" = the whole
+        # layer in one launch.  _fused_ok: None until the first fused launch,
+        # then True, or False where the device cannot run those kernels
+        # (the per-stage kernels run from then on).
+        if layer_mode not in ("stages", "mlp", "one"):
+            raise ValueError("layer_mode must be stages, mlp or one")
+        self.layer_mode = layer_mode
+        self._fused_ok = None
         self._layer_ws = None
         self._layer_err = None
         self._ensure_buffers(1)
@@ -451,9 +456,7 @@ class Llama31DecodeExecutor:
             self._mark_end("qkv", ev, rc)
             _hip.check("cascade_qkv_rope_bf16", rc)
 
-    def _attention_o(self, layer, ptrs, state, stream):
-        wo = ptrs["o_proj"]
-        x = state.hidden_states.data_ptr()
+    def _attention_o(self, layer, ptrs, state, stream, with_o=True):
         row = 2 * self.hidden
         k0 = self._kv_pointer(layer, 0, 0)
         v0 = self._kv_pointer(layer, 1, 0)
@@ -467,19 +470,28 @@ class Llama31DecodeExecutor:
                               stream)
             self._mark_end("attention", ev, rc)
             _hip.check("cascade_decode_attention_bf16", rc)
-            ev = self._mark_begin("o_proj")
-            xt = x + t * row
-            rc = self._k_residual(wo, self._attn_ptr + t * row, xt, xt,
-                                  self.hidden, self.hidden, stream)
-            self._mark_end("o_proj", ev, rc)
-            _hip.check("cascade_gemv_residual_bf16", rc)
+            if with_o:
+                self._o_residual(ptrs, state, t, stream)
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
 
-    def _layer_one_launch(self, layer, ptrs, state, stream):
-        """A whole single-token layer unit in one launch
-        (cascade_decode_layer_bf16); False when it does not apply here."""
+    def _o_residual(self, ptrs, state, t, stream):
+        row = 2 * self.hidden
+        xt = state.hidden_states.data_ptr() + t * row
+        ev = self._mark_begin("o_proj")
+        rc = self._k_residual(ptrs["o_proj"], self._attn_ptr + t * row, xt, xt,
+                              self.hidden, self.hidden, stream)
+        self._mark_end("o_proj", ev, rc)
+        _hip.check("cascade_gemv_residual_bf16", rc)
 
-        if self.fused_layer is False or len(state.positions) != 1:
+    def _layer_fused(self, layer, ptrs, state, stream):
+        """A single-token layer unit through the one-launch kernels --
+        layer_mode "one": the whole layer in one launch
+        (cascade_decode_layer_bf16); "mlp": q|k|v and attention per stage,
+        then o_proj .. down_proj in one launch (cascade_decode_mlp_bf16).
+        False when they do not apply; the per-stage kernels run instead."""
+
+        if (self.layer_mode == "stages" or self._fused_ok is False
+                or len(state.positions) != 1):
             return False
         names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
                  "down_proj")
@@ -488,27 +500,44 @@ class Llama31DecodeExecutor:
         if self._layer_ws is None:
             self._layer_ws = torch.zeros(_hip.decode_layer_workspace_bytes(),
                                          dtype=torch.uint8, device=self.device)
-        slot = self._first_slot
-        pos = state.positions[0]
-        half = self.head_dim // 2
-        norm_in, norm_post = self._norm_ptrs[layer]
         ws = self._layer_ws
-        ev = self._mark_begin("layer")
-        rc = self._k_layer(
-            *(ptrs[n] for n in names), norm_in, norm_post, self.eps,
-            state.hidden_states.data_ptr(),
-            self.rope.cos.data_ptr() + 2 * half * pos,
-            self.rope.sin.data_ptr() + 2 * half * pos,
-            self._kv_pointer(layer, 0, 0), self._kv_pointer(layer, 1, 0),
-            self.kv_cache.head_stride, slot + 1, self.scale, ws.data_ptr(),
-            ws.numel(), stream)
-        self._mark_end("layer", ev, rc)
-        if rc == _hip.ESHAPE and self.fused_layer is None:
-            self.fused_layer = False
-            return False
-        _hip.check("cascade_decode_layer_bf16", rc)
-        self.fused_layer = True
-        self.kv_cache.set_length(layer, slot + 1)
+        x = state.hidden_states.data_ptr()
+        norm_in, norm_post = self._norm_ptrs[layer]
+        if self.layer_mode == "one":
+            slot = self._first_slot
+            pos = state.positions[0]
+            half = self.head_dim // 2
+            ev = self._mark_begin("layer")
+            rc = self._k_layer(
+                *(ptrs[n] for n in names), norm_in, norm_post, self.eps, x,
+                self.rope.cos.data_ptr() + 2 * half * pos,
+                self.rope.sin.data_ptr() + 2 * half * pos,
+                self._kv_pointer(layer, 0, 0), self._kv_pointer(layer, 1, 0),
+                self.kv_cache.head_stride, slot + 1, self.scale, ws.data_ptr(),
+                ws.numel(), stream)
+            self._mark_end("layer", ev, rc)
+            if rc == _hip.ESHAPE and self._fused_ok is None:
+                self._fused_ok = False
+                return False
+            _hip.check("cascade_decode_layer_bf16", rc)
+            self.kv_cache.set_length(layer, slot + 1)
+        else:
+            self._qkv(layer, ptrs, state, stream)
+            self._attention_o(layer, ptrs, state, stream, with_o=False)
+            ev = self._mark_begin("mlp")
+            rc = self._k_mlp(ptrs["o_proj"], ptrs["gate_proj"], ptrs["up_proj"],
+                             ptrs["down_proj"], norm_post, self.eps, self._attn_ptr,
+                             x, ws.data_ptr(), ws.numel(), stream)
+            self._mark_end("mlp", ev, rc)
+            if rc == _hip.ESHAPE and self._fused_ok is None:
+                # the device cannot run it: finish this layer per stage
+                self._fused_ok = False
+                self._o_residual(ptrs, state, 0, stream)
+                self._gate_up(layer, ptrs, state, stream)
+                self._down(layer, ptrs, state, stream)
+                return True
+            _hip.check("cascade_decode_mlp_bf16", rc)
+        self._fused_ok = True
         if self.capture is not None:
             self.capture.append((layer, state.hidden_states.detach().clone()))
         return True
@@ -528,14 +557,15 @@ class Llama31DecodeExecutor:
             self._layer_ws.zero_()
             host.zero_()
             raise RuntimeError(
-                "cascade_decode_layer_bf16: a grid barrier timed out (not all "
-                "workgroups resident); the results of the last tokens are invalid")
+                "cascade_decode_layer_bf16 / cascade_decode_mlp_bf16: a grid "
+                "barrier timed out (not all workgroups resident); the results "
+                "of the last tokens are invalid")
         word = _hip.DECODE_LAYER_ERROR
         host.copy_(self._layer_ws[word:word + 4].view(torch.int32), non_blocking=True)
         event.record()
 
     def instrument(self, name, launches, stride=1, offset=0):
-        """Time ``launches`` launches of kernel group ``name`` ("layer",
+        """Time ``launches`` launches of kernel group ``name`` ("layer", "mlp",
         "gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head"): of the group's
         coming launches, numbers offset, offset + stride, ...; read them back
         with :meth:`kernel_times_ms` after a synchronize.  The one-kernel
@@ -758,7 +788,7 @@ class Llama31DecodeExecutor:
         if self._batched:
             return self._call_batched(layer, op, ptrs, state, stream)
         if op == "layer":
-            if self._layer_one_launch(layer, ptrs, state, stream):
+            if self._layer_fused(layer, ptrs, state, stream):
                 return state
             self._qkv(layer, ptrs, state, stream)
             self._attention_o(layer, ptrs, state, stream)

@@ -171,6 +171,22 @@ int cascade_decode_layer_bf16(const void *wq, const void *wk, const void *wv,
                               int64_t len, float scale, void *workspace,
                               size_t workspace_bytes, void *stream);
 
+/* The MLP half of the same layer in one launch (stages o_proj .. down of
+ * cascade_decode_layer_bf16), after the caller ran q|k|v and attention with
+ * the per-stage calls:
+ *   x += bf16(Wo . attn); n2 = RMSNorm(x, norm_post);
+ *   inter = SwiGLU(Wg . n2, Wu . n2); x += bf16(Wd . inter)
+ * attn [4096] bf16 (the attention output), x [4096] bf16 updated in place.
+ * Same shape, device, workspace and error-word rules as
+ * cascade_decode_layer_bf16 (one workspace may serve both); rounds as the
+ * per-stage calls do, bit for bit.
+ * Replaces llama31.py:246-279 (o_proj .. down_proj) for a layer unit.      */
+int cascade_decode_mlp_bf16(const void *wo, const void *w_gate,
+                            const void *w_up, const void *w_down,
+                            const void *norm_post, float eps, const void *attn,
+                            void *x, void *workspace, size_t workspace_bytes,
+                            void *stream);
+
 /* ------------------------------------------------------ prefill (M > 1)
  * MFMA GEMMs over the token rows of a prefill call: Y[M, N] =
  * epilogue(X[M, K] . W[N, K]^T), X row-major [M, K] (already normalised:

@@ -167,6 +167,19 @@ class FakeKernels:
         self.calls.append("layer")
         return 0
 
+    def mlp(self, wo, wg, wu, wd, norm_post, eps, attn, x, ws, ws_bytes, stream):
+        # the one-launch MLP half: o_proj + residual, gate/up + SwiGLU, down
+        # + residual through the same pointers
+        before = len(self.calls)
+        h, i = 4096, 14336
+        inter = torch.empty(i, dtype=BF16)
+        self.residual(wo, attn, x, x, h, h, stream)
+        self.swiglu(wg, wu, i, h, x, norm_post, eps, inter.data_ptr(), stream)
+        self.residual(wd, inter.data_ptr(), x, x, h, i, stream)
+        del self.calls[before:]
+        self.calls.append("mlp")
+        return 0
+
     # -------------------------------------- batched (S > 1) entry points
 
     def qkv_gemm(self, x, m, wq, wk, wv, nq, nk, nv, k, cos, sin, positions,
@@ -283,7 +296,7 @@ def exact_oracle(monkeypatch):
     monkeypatch.setattr(_hip, "require_device", lenient_require)
 
 
-def make_executor(monkeypatch, plan, store, one_launch_layers=False):
+def make_executor(monkeypatch, plan, store, layer_mode="stages"):
     fakes = FakeKernels()
 
     def gather(table, ids, out, error_flag=None, stream=None):
@@ -294,7 +307,7 @@ def make_executor(monkeypatch, plan, store, one_launch_layers=False):
     cache = SimpleKVCache(LAYERS, device="cpu")
     ex = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
                                HostResident(plan, store), kv_cache=cache, top_k=5,
-                               one_launch_layers=one_launch_layers)
+                               layer_mode=layer_mode)
     ex._stream = lambda: 0
     ex._k_qkv, ex._k_attn, ex._k_residual = fakes.qkv, fakes.attention, fakes.residual
     ex._k_swiglu, ex._k_silu, ex._k_mul = fakes.swiglu, fakes.silu, fakes.mul
@@ -304,6 +317,7 @@ def make_executor(monkeypatch, plan, store, one_launch_layers=False):
     ex._k_silu_gemm, ex._k_mul_gemm = fakes.silu_gemm, fakes.mul_gemm
     ex._k_f32_gemm = fakes.f32_gemm
     ex._k_layer = fakes.layer
+    ex._k_mlp = fakes.mlp
     return ex, fakes
 
 
@@ -315,19 +329,18 @@ def run_units(plan, store, executor, state):
 
 
 @pytest.mark.parametrize("granularity", ["matrix_group", "matrix", "layer",
-                                         "layer_one_launch"])
+                                         "layer/mlp", "layer/one"])
 def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
                                                         exact_oracle, granularity):
-    # layer_one_launch: layer units, each decode step of a layer one launch
-    # of cascade_decode_layer_bf16 (its double below)
-    one_launch = granularity == "layer_one_launch"
-    plan = build_llama31_8b_plan("layer" if one_launch else granularity,
-                                 num_layers=LAYERS)
+    # layer/mlp, layer/one: layer units whose decode steps run through
+    # cascade_decode_mlp_bf16 / cascade_decode_layer_bf16 (doubles above)
+    base, _, layer_mode = granularity.partition("/")
+    plan = build_llama31_8b_plan(base, num_layers=LAYERS)
     # every granularity packs the arena identically, so one store serves all
     for key in plan.tensors:
         assert plan.tensor_host_offset(key) == weights.plan.tensor_host_offset(key)
     store = weights
-    executor, fakes = make_executor(monkeypatch, plan, store, one_launch)
+    executor, fakes = make_executor(monkeypatch, plan, store, layer_mode or "stages")
     oracle = ref.OracleLlama(store.tensor, LAYERS)
     prompt = [7, 99, 1234, 5, 128255, 0]
     expected_logits, ev, ei = oracle.step(prompt, 5)
@@ -352,12 +365,12 @@ def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
         assert torch.equal(k[0], oracle.caches[layer]["k"])
         assert torch.equal(v[0], oracle.caches[layer]["v"])
     # (a layer unit of one token is one launch of the whole layer)
-    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5,
-                 "layer_one_launch": 1}[granularity]
+    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5, "layer/mlp": 3,
+                 "layer/one": 1}[granularity]
     # prefill, per layer: input norm, q/k/v GEMM(s), causal attention,
     # o GEMM, post-attention norm, MLP GEMM(s), down GEMM
-    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7,
-                   "layer_one_launch": 7}[granularity]
+    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7, "layer/mlp": 7,
+                   "layer/one": 7}[granularity]
     # decode, per layer and token: qkv launch(es), attention, o residual,
     # MLP, down; finish: one rmsnorm, then (prefill) one logits GEMM over
     # every position and one LM-head launch for the last

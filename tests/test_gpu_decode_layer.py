@@ -64,3 +64,31 @@ def test_decode_layer_repeated_launches_are_identical(gpu_device):
     print("24 launches done, error word", _hip.decode_layer_error(ws), flush=True)
     assert _hip.decode_layer_error(ws) == 0
     assert torch.equal(outs.cpu(), first["out"].expand(24, -1).contiguous())
+
+
+@pytest.mark.parametrize("past", [0, 2048])
+def test_decode_mlp_equals_per_stage_kernels(gpu_device, past):
+    # q|k|v and attention per stage, then the one-launch MLP half: the hidden
+    # state must equal the per-stage o_proj / gate_up / down path bit for bit
+    # (same GEMV rows, same RMSNorm order), and match the oracle
+    case = cases.layer_case(23 + past, past)
+    staged = gpu_cases.run_layer_gpu(case, gpu_device)
+    dev = torch.device(gpu_device)
+    w = {k: case[k].to(dev) for k in ("o", "gate", "up", "down", "ln2")}
+    ws = torch.zeros(_hip.decode_layer_workspace_bytes(), dtype=torch.uint8,
+                     device=dev)
+    x = case["x"].to(dev).clone()
+    attn = staged["attn"].to(dev)
+    print("decode_mlp past={}".format(past), flush=True)
+    code = _hip.decode_mlp(w, attn, x, ws, case["eps"])
+    if code != 0:
+        pytest.skip("device cannot run the one-launch MLP (needs 256 CUs)")
+    torch.cuda.synchronize(dev)
+    inter = ws[_hip.DECODE_LAYER_INTER:_hip.DECODE_LAYER_INTER + 2 * 14336]
+    assert _hip.decode_layer_error(ws) == 0
+    assert torch.equal(inter.view(torch.bfloat16).cpu(), staged["inter"])
+    assert torch.equal(x.cpu(), staged["out"])
+    expected = cases.layer_expected(case)
+    alternative = cases.layer_expected(case, cases.sgemm_linear)
+    r = cases.within_noise_floor(x.cpu(), expected["out"], alternative["out"])
+    assert r["ok"], r

@@ -99,11 +99,10 @@ def copy_weights(src, dst):
 
 
 def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
-    # "layer_one_launch": layer units, each run as one launch of the whole
-    # decoder layer (cascade_decode_layer_bf16) at decode
-    one_launch = granularity == "layer_one_launch"
-    if one_launch:
-        granularity = "layer"
+    # "layer/mlp", "layer/one": layer units whose decode steps run the MLP
+    # half (cascade_decode_mlp_bf16) or the whole layer
+    # (cascade_decode_layer_bf16) as one launch
+    granularity, _, layer_mode = granularity.partition("/")
     plan = build_llama31_8b_plan(granularity, stream_vocab=(vocab_mode == "streamed"),
                                  num_layers=LAYERS)
     store = create_weight_store(plan, store_mode)
@@ -119,7 +118,7 @@ def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
     executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
                                      resident, vocab_runtime=vocab, top_k=TOP_K,
                                      return_full_logits=True,
-                                     one_launch_layers=one_launch)
+                                     layer_mode=layer_mode or "stages")
     return store, runtime, executor
 
 
@@ -169,7 +168,8 @@ CONFIGS = [
     ("full_pinned", "layer", "resident", "double"),
     ("pinned_staging", "matrix_group", "resident", "double"),
     ("full_pinned", "matrix_group", "resident", "resident"),
-    ("full_pinned", "layer_one_launch", "resident", "resident"),
+    ("full_pinned", "layer/mlp", "resident", "resident"),
+    ("full_pinned", "layer/one", "resident", "resident"),
 ]
 
 
