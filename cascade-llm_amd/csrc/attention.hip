@@ -72,18 +72,6 @@ __device__ __forceinline__ u32x4 kv_load(const uint16_t *p) {
     return *reinterpret_cast<const u32x4 *>(p);
 }
 
-// Operand e of the transposed V block: dword p = (row 2p, row 2p + 1) of
-// dim 8 c + e, from the lane's 8 loaded rows.
-__device__ __forceinline__ u32x4 v_operand(const u32x4 (&vt)[8], int e) {
-  // v_perm_b32 selectors: low halves / high halves of (src1, src0)
-  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-    r[p] = __builtin_amdgcn_perm(vt[2 * p + 1][e >> 1], vt[2 * p][e >> 1], sel);
-  return r;
-}
-
 template <int WAVES, bool NT>
 __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
     AttnArgs a) {

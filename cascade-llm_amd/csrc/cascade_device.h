@@ -72,6 +72,19 @@ __device__ __forceinline__ f32x4 mfma_16x16x32_bf16(u32x4 a, u32x4 b,
       0, 0);
 }
 
+// Operand e of a V block transposed in registers for the P.V MFMA (decode
+// attention): lane (c, g4) holds dims 8 c .. 8 c + 7 of rows 8 g4 + j in
+// vt[j]; dword p of the result = (row 2p, row 2p + 1) of dim 8 c + e.
+__device__ __forceinline__ u32x4 v_operand(const u32x4 (&vt)[8], int e) {
+  // v_perm_b32 selectors: low halves / high halves of (src1, src0)
+  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+    r[p] = __builtin_amdgcn_perm(vt[2 * p + 1][e >> 1], vt[2 * p][e >> 1], sel);
+  return r;
+}
+
 // Two floats rounded to bf16 (round to nearest even), lo in bits 0..15.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));

@@ -1,31 +1,35 @@
-// One Llama-3.1-8B-shaped decoder layer of batch-1 decode in one persistent
-// launch on gfx950 (MI355X).
+// One Llama-3.1-8B-shaped decoder layer of batch-1 decode as one persistent
+// launch on gfx950 (MI355X), or its MLP half (o_proj .. down_proj).
 //
 // The per-stage path (gemv.hip, attention.hip) runs a layer as six kernels:
-// q|k|v, attention, split merge, o_proj, gate/up, down_proj.  Each launch
-// boundary costs a few microseconds of dispatch, ramp-up and drain in which
-// HBM idles -- a fifth of the time of a resident decode token.  This kernel
-// runs the same six stages as one launch of 256 workgroups (one per CU, all
-// resident at once) with a grid barrier between stages, and issues every stage's first
-// weight (or K / V) loads BEFORE the barrier that opens the stage: the
-// barrier's latency then overlaps HBM traffic the stage needs anyway.
+// q|k|v, attention, split merge, o_proj, gate/up, down_proj, each paying a
+// few microseconds of dispatch, ramp-up and drain.  This kernel runs the
+// same stages in one launch of 256 workgroups (one per CU, all resident at
+// once) with a grid barrier between stages, and issues each stage's first
+// weight (or K / V) loads before the barrier that opens it, so the barrier
+// overlaps HBM traffic the stage needs anyway.  Measured on config 4 it is
+// on par with the per-stage kernels, not faster (the stage tails of uneven
+// per-CU bandwidth and the hand-off latencies eat the launch savings), so
+// callers select it explicitly.
 //
-// Stages (reference: layer_streaming/llama31.py; 2048 waves in the grid):
+// Stages (reference: layer_streaming/llama31.py).  Wave 0 of a workgroup is
+// the control wave; waves 1..7 (workers) carry the rows:
 //   A  RMSNorm + q|k|v rows + RoPE; q -> scratch, k / v -> cache slot
 //      len - 1 (:169-180, :206-218, :241-245)    12 (d, d + 64) pairs / WG
-//   B  attention over positions [0, len) (:219-229): kv head g = wg % 8,
-//      split wg / 8 of 32; each wave walks 32-row blocks wave, wave + 8, ...
-//   C  split merge -> attn (bf16)                          1 (head, 16 dims)
-//   D  o_proj + residual -> x (:246-251)                   2 rows per wave
-//   E  RMSNorm + gate/up + SwiGLU -> inter (:252-275)      7 row pairs / wave
-//   F  down_proj + residual -> x (:276-279)                2 rows per wave
+//   B  attention over positions [0, len) (:219-229): KV head g = wg % 8,
+//      split wg / 8 of 32; worker w walks 32-row blocks w, w + 7, ...
+//   C  split merge -> attn (bf16), control wave       1 (head, 16 dims) / WG
+//   D  o_proj + residual -> x (:246-251)              16 rows / WG
+//   E  RMSNorm + gate/up + SwiGLU -> inter (:252-275) 56 row pairs / WG
+//   F  down_proj + residual -> x (:276-279)           16 rows / WG
 // Workgroup b takes rows b, b + 256, b + 512, ... of every matrix, so each
 // XCD (b % 8) reads rows spread over the whole matrix: with contiguous
 // blocks per workgroup, some XCDs were measured ~30% slower than others on
 // the same stage, depending on where the matrix sits in memory.
 // Each GEMV row is computed exactly as gemv.hip computes it (same loads,
-// same dot8 order, same wave reduction and rounding points), so stages A, D,
-// E and F give the per-stage path's results bit for bit on the same input.
+// same dot8 order, same wave reduction and rounding points, same RMSNorm
+// reduction order), so stages A, D, E and F give the per-stage path's
+// results bit for bit on the same input.
 //
 // Coherence.  The 8 XCDs' L2 caches are not coherent with each other.
 // Everything one stage hands to the next (q, the new K / V row, split
@@ -56,17 +60,12 @@ constexpr int kLG = kLQ / kLKV;   // query heads per KV head
 constexpr int kLWaves = 8;
 constexpr int kLThreads = kLWaves * kWave;
 constexpr int kLGrid = 256;       // one workgroup per CU
-constexpr int kLGridWaves = kLGrid * kLWaves;
 constexpr int kLSplits = kLGrid / kLKV;  // attention splits per KV head
 constexpr int kLBlock = 32;       // attention rows per wave step
 constexpr int kKcH = kLH / 512;   // 16-byte loads per lane, 4096-long row
 constexpr int kKcI = kLI / 512;   // 16-byte loads per lane, 14336-long row
 constexpr int kQkvPairs = (kLQ + 2 * kLKV) * kLD / 2;  // (d, d + 64) pairs
-constexpr int kGatePairs = kLI / kLGridWaves;          // per wave
 constexpr float kLLog2e = 1.4426950408889634f;
-static_assert(kLH % kLGridWaves == 0 && kLH / kLGridWaves == 2, "2 rows / wave");
-static_assert(kLI % kLGridWaves == 0, "whole gate/up pairs per wave");
-static_assert(kQkvPairs <= 2 * kLGridWaves, "at most 2 q|k|v pairs per wave");
 static_assert(kLGrid == kLQ * 8, "merge: one (head, 16 dims) per workgroup");
 
 // Sync words (uint32), one 64-byte line each: 8 arrival counters (one per
@@ -275,16 +274,6 @@ __device__ __forceinline__ void ctl_stage(const uint16_t *src, const uint16_t *n
 }
 
 __device__ __forceinline__ float layer_silu(float g) { return g / (1.0f + expf(-g)); }
-
-// Operand e of a transposed V block (as attention.hip's v_operand).
-__device__ __forceinline__ u32x4 layer_v_operand(const u32x4 (&vt)[8], int e) {
-  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-    r[p] = __builtin_amdgcn_perm(vt[2 * p + 1][e >> 1], vt[2 * p][e >> 1], sel);
-  return r;
-}
 
 // Roles inside a workgroup.  vmcnt, the counter a wave waits on for its
 // vector loads and stores, completes in issue order on gfx950: a wave that
@@ -515,7 +504,7 @@ __device__ __forceinline__ void layer_worker(const LayerArgs &a, LayerShared &sh
         for (int e = 0; e < 8; ++e) o[e] *= alpha;
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = mfma_16x16x32_bf16(layer_v_operand(vt, e), pop, o[e]);
+      for (int e = 0; e < 8; ++e) o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
     };
     for (int i = 0; i < nbw; i += 2) {
       step(i, ktA, vtA);
