@@ -27,7 +27,12 @@ Also reported (extra keys, not ``value``):
   * cpu_baseline: the CPU oracle on this host's cores on a bounded sample
     (skip: --no-cpu-baseline).
 
-Run: python bench.py [--steps K] [--warmup W] [--context L]
+Config 4 runs the six per-stage kernels per layer by default; --layer-mode
+mlp / one switch to the one-launch MLP half / whole layer
+(cascade_decode_mlp_bf16 / cascade_decode_layer_bf16, on par with the
+default), and the roofline then describes that launch.
+
+Run: python bench.py [--steps K] [--warmup W] [--context L] [--layer-mode M]
 """
 
 import argparse
