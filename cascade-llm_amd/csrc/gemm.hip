@@ -75,8 +75,6 @@ enum GemmEpilogue : int {
 
 constexpr int kTileN = 128;
 constexpr int kTileK = 64;
-constexpr int kGemmWaves = 4;
-constexpr int kGemmThreads = kGemmWaves * kWave;
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 constexpr int kGemmHead = 128;
@@ -125,20 +123,26 @@ __device__ __forceinline__ bool gemm_tile(const GemmArgs &a, int &tm, int &tn) {
 }
 
 // Tile shapes.  Every tile is 128 columns wide (one head of q|k|v, or 64
-// gate + 64 up rows); BM rows of X are split over WM x WN = 4 waves, each
+// gate + 64 up rows); BM rows of X are split over WM x WN waves, each
 // owning FM x FN fragments of 16 x 16.
 template <int BM_, int WM_, int WN_>
 struct GemmTile {
   static constexpr int BM = BM_;
   static constexpr int WM = WM_;
   static constexpr int WN = WN_;
+  static constexpr int WAVES = WM * WN;
   static constexpr int FM = BM / WM / 16;
   static constexpr int FN = kTileN / WN / 16;
   static constexpr int H = FN / 2;  // fragments per half tile
-  static_assert(WM * WN == kGemmWaves, "four waves");
+  // staged epilogue: bf16 per staged column (BM rows + 8 pad; the column
+  // stride is 4 banks mod 64, so 16 lanes writing 16 columns hit 16
+  // distinct 4-bank groups)
+  static constexpr int STAGE_COL = BM + 8;
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
 };
-using GemmTile128 = GemmTile<128, 2, 2>;  // waves of 64 x 64
-using GemmTile64 = GemmTile<64, 1, 4>;    // waves of 64 x 32
+using GemmTile256 = GemmTile<256, 4, 2>;  // 8 waves of 64 x 64
+using GemmTile128 = GemmTile<128, 2, 2>;  // 4 waves of 64 x 64
+using GemmTile64 = GemmTile<64, 1, 4>;    // 4 waves of 64 x 32
 
 // Tile column of fragment j of wave column wn for lane row lr.  A wave's
 // first-half fragments (j < H) and second-half fragments (j >= H) sit 64
@@ -240,11 +244,10 @@ __device__ __forceinline__ void gemm_epilogue(
 // ds_read_b64_tr_b16, which hands lane i of a 16-lane group row i of the 4
 // columns the group addresses, so every lane ends up with 8 consecutive
 // columns of one row and loads aux / stores results 16 bytes at a time.
-// Column stride 272 bytes: the fragment writes of 32 lanes fall in distinct
-// banks.  The values staged are those of the direct epilogue's rounding
-// points (bf16(acc), or the final SwiGLU product), so results are the same
-// bit for bit.
-constexpr int kStageCol = 136;  // bf16 per staged column (128 rows + 8 pad)
+// Column stride (BM + 8) bf16 (GemmTile::STAGE_COL): the fragment writes
+// of a lane group fall in distinct banks.  The values staged are those of
+// the direct epilogue's rounding points (bf16(acc), or the final SwiGLU
+// product), so results are the same bit for bit.
 
 __device__ __forceinline__ uint2 stage_read_tr(const uint16_t *p) {
   typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -268,11 +271,11 @@ __device__ __forceinline__ void gemm_epilogue_staged(
   // w, w + 4, ...
   constexpr int TW = EPI == kGemmSwiglu || EPI == kGemmQkvRope ? 64 : kTileN;
   constexpr int kItems = (T::BM / 16) * (TW / 32);
-  constexpr int kPer = kItems / kGemmWaves;
-  static_assert(kItems % kGemmWaves == 0, "whole items per wave");
+  constexpr int kPer = kItems / T::WAVES;
+  static_assert(kItems % T::WAVES == 0, "whole items per wave");
   const int g = lq, li = lr;
-  auto item_r0 = [&](int n) { return 16 * ((wave + kGemmWaves * n) / (TW / 32)); };
-  auto item_c0 = [&](int n) { return 32 * ((wave + kGemmWaves * n) % (TW / 32)) + 8 * g; };
+  auto item_r0 = [&](int n) { return 16 * ((wave + T::WAVES * n) / (TW / 32)); };
+  auto item_c0 = [&](int n) { return 32 * ((wave + T::WAVES * n) % (TW / 32)) + 8 * g; };
   const int64_t ncols = a.n0;  // output width (SwiGLU: n_half)
 
   // ---- inputs the epilogue reads from memory, issued first so their
@@ -314,7 +317,7 @@ __device__ __forceinline__ void gemm_epilogue_staged(
         }
         v.x = pack_bf16x2(o[0], o[1]);
         v.y = pack_bf16x2(o[2], o[3]);
-        *reinterpret_cast<uint2 *>(stage + col * kStageCol + arow + 16 * i + 4 * lq) = v;
+        *reinterpret_cast<uint2 *>(stage + col * T::STAGE_COL + arow + 16 * i + 4 * lq) = v;
       }
   } else {
 #pragma unroll
@@ -325,7 +328,7 @@ __device__ __forceinline__ void gemm_epilogue_staged(
         uint2 v;
         v.x = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
         v.y = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
-        *reinterpret_cast<uint2 *>(stage + col * kStageCol + arow + 16 * i + 4 * lq) = v;
+        *reinterpret_cast<uint2 *>(stage + col * T::STAGE_COL + arow + 16 * i + 4 * lq) = v;
       }
   }
   __syncthreads();
@@ -334,8 +337,8 @@ __device__ __forceinline__ void gemm_epilogue_staged(
   const int qk = li >> 2, qq = li & 3;  // addressing lane k = 4 j + q of the group
   auto read8 = [&](int r0, int c0, uint32_t (&w)[4]) {
     // two transposed reads: columns c0 .. c0 + 3 and c0 + 4 .. c0 + 7
-    const uint2 lo = stage_read_tr(stage + (c0 + qk) * kStageCol + r0 + 4 * qq);
-    const uint2 hi = stage_read_tr(stage + (c0 + 4 + qk) * kStageCol + r0 + 4 * qq);
+    const uint2 lo = stage_read_tr(stage + (c0 + qk) * T::STAGE_COL + r0 + 4 * qq);
+    const uint2 hi = stage_read_tr(stage + (c0 + 4 + qk) * T::STAGE_COL + r0 + 4 * qq);
     w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
   };
 #pragma unroll
@@ -437,19 +440,54 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const uint16_t *base
                                            static_cast<int>(bytes), 0x00020000);
 }
 
-template <int EPI, class T, int BK = kTileK>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
+// The same resource as four words (for inline asm): base, stride 0,
+// num_records, the flags above.
+__device__ __forceinline__ u32x4 gemm_rsrc_words(const uint16_t *base, int64_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
+  r.z = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bytes));
+  r.w = 0x00020000u;
+  return r;
+}
+
+// buffer_load_dwordx4 ... lds issued from inline asm: lane l's 16 bytes at
+// voffset land at LDS byte (lds + 16 l).  The compiler does not see these
+// loads, so it adds no vmcnt waits of its own for them (the caller waits);
+// the memory clobber keeps LDS accesses from moving across the issue.
+__device__ __forceinline__ void dma_lds16(const u32x4 &rsrc, int voff, const uint16_t *lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)lds)));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(m0), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+
+// STAGES = 2: two slab buffers, the slab loads through the LDS-DMA builtin
+// (the compiler waits for them exactly).  STAGES = 3: a ring of three slab
+// buffers with two slabs in flight; the loads go through dma_lds16 and each
+// slab step waits for exactly its own slab (vmcnt = the next slab's loads),
+// since with more than two buffers the compiler would wait for every load
+// in flight at each barrier.
+template <int EPI, class T, int STAGES = 2, int BK = kTileK>
+__global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
+  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 slab buffers");
   using L = DmaSlab<BK>;
   constexpr int XI = T::BM * L::ROWB / 1024;  // load instructions per X slab
   constexpr int WI = kTileN * L::ROWB / 1024;
-  constexpr int XW = XI / kGemmWaves, WW = WI / kGemmWaves;  // per wave
-  static_assert(XI % kGemmWaves == 0 && WI % kGemmWaves == 0, "whole loads per wave");
+  constexpr int XW = XI / T::WAVES, WW = WI / T::WAVES;  // per wave
+  static_assert(XI % T::WAVES == 0 && WI % T::WAVES == 0, "whole loads per wave");
   constexpr int XB = T::BM * BK, WB = kTileN * BK;  // bf16 per slab buffer
-  // one array per slab buffer (X slab, then W slab); sb0 also holds the
-  // staged output tile of the vectorised epilogue
-  constexpr int kStage = kTileN * kStageCol;
-  __shared__ __attribute__((aligned(16))) uint16_t sb0[XB + WB > kStage ? XB + WB : kStage];
-  __shared__ __attribute__((aligned(16))) uint16_t sb1[XB + WB];
+  // STAGES = 2: one array per slab buffer (X slab, then W slab); sb0 also
+  // holds the staged output tile of the vectorised epilogue.  STAGES = 3:
+  // sb0 holds the ring (slab buffer k at sb0 + k (XB + WB)) and, after the
+  // loop, the staged tile.
+  constexpr int kStage = kTileN * T::STAGE_COL;
+  constexpr int kSlab = XB + WB;
+  constexpr int kSb0 = (STAGES == 2 ? kSlab : 3 * kSlab) > kStage
+                           ? (STAGES == 2 ? kSlab : 3 * kSlab) : kStage;
+  __shared__ __attribute__((aligned(16))) uint16_t sb0[kSb0];
+  __shared__ __attribute__((aligned(16))) uint16_t sb1[STAGES == 2 ? kSlab : 8];
   int tm, tn;
   if (!gemm_tile(a, tm, tn)) return;  // whole workgroup: no barrier skipped
   const int tid = threadIdx.x;
@@ -558,13 +596,91 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   const int slabs = static_cast<int>(a.k / BK);
   // s_waitcnt vmcnt(0), expcnt / lgkmcnt left alone
   constexpr int kWaitLoads = (7 << 4) | (15 << 8);
+  if constexpr (STAGES == 3) {
+    const u32x4 xw = gemm_rsrc_words(a.x, a.m * k_bytes);
+    const u32x4 ww0 = gemm_rsrc_words(wbase0, wrows0 * k_bytes);
+    const u32x4 ww1 = gemm_rsrc_words(wbase1, wrows1 * k_bytes);
+    auto ring_load = [&](int slab, uint16_t *dx) {
+      uint16_t *dw = dx + XB;
+      const int kb = slab * BK * 2;
+#pragma unroll
+      for (int h = 0; h < XW; ++h) {
+        const int i = wave * XW + h;
+        const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
+        dma_lds16(xw, ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
+                  dx + i * 512);
+      }
+#pragma unroll
+      for (int h = 0; h < WW; ++h) {
+        const int i = wave * WW + h;
+        const int trow = L::RPI * i;
+        const bool second = EPI == kGemmSwiglu && trow >= kGemmHalfHead;
+        const int64_t row = (second ? wrow1 : wrow0) + (second ? trow - kGemmHalfHead : trow);
+        dma_lds16(second ? ww1 : ww0,
+                  ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
+                  dw + i * 512);
+      }
+    };
+    // wait for this wave's loads of the slab about to be computed (the next
+    // slab's D loads may stay in flight), then the barrier publishes it to
+    // the workgroup and frees the buffer read one step earlier
+    // (lgkmcnt(0) too: this wave's LDS reads of the buffer about to be
+    // refilled have completed before the barrier lets a refill start)
+    constexpr int D = XW + WW;
+    constexpr int kWaitOne = (D & 15) | ((D >> 4) << 14) | (7 << 4);
+    auto publish1 = [&]() {
+      __builtin_amdgcn_s_waitcnt(kWaitOne);
+      __builtin_amdgcn_s_barrier();
+    };
+    uint16_t *b0 = sb0, *b1 = sb0 + kSlab, *b2 = sb0 + 2 * kSlab;
+    // loads past the last slab reload it into the free buffer (never read):
+    // every step then has the same loads in flight
+    ring_load(0, b0);
+    ring_load(min(1, slabs - 1), b1);
+    int s = 0;
+    for (; s + 3 <= slabs; s += 3) {
+      publish1();
+      ring_load(min(s + 2, slabs - 1), b2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b0, b0 + XB);
+      publish1();
+      ring_load(min(s + 3, slabs - 1), b0);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b1, b1 + XB);
+      publish1();
+      ring_load(min(s + 4, slabs - 1), b1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b2, b2 + XB);
+    }
+    if (s < slabs) {
+      publish1();
+      ring_load(min(s + 2, slabs - 1), b2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b0, b0 + XB);
+      ++s;
+    }
+    if (s < slabs) {
+      publish1();
+      compute(b1, b1 + XB);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLoads);
+    if (EPI != kGemmF32 && a.vec_out) {
+      __builtin_amdgcn_s_barrier();  // every wave's loads landed, ring read
+      gemm_epilogue_staged<EPI, T>(a, tm, tn, wm, wn, lane, wave, acc, sb0);
+    } else {
+      gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
+    }
+    return;
+  }
   // slab s: this wave's loads of s done; barrier (everyone's slab s has
   // landed, slab s - 1 has been read); slab s + 1 into the other buffer;
   // compute s.  The buffers are named directly at every call, and the
   // MFMAs sit in straight-line code (a branch around them makes the compiler
   // copy every accumulator between AGPRs and VGPRs each iteration).
+  // (lgkmcnt(0) too: this wave's LDS reads of the buffer about to be
+  // refilled have completed before the barrier lets a refill start)
   auto publish = [&]() {
-    __builtin_amdgcn_s_waitcnt(kWaitLoads);
+    __builtin_amdgcn_s_waitcnt(kWaitLoads & ~(15 << 8));
     __builtin_amdgcn_s_barrier();
   };
   load_slab(0, sb0, sb0 + XB);
@@ -598,7 +714,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   }
 }
 
-template <int EPI, class T>
+template <int EPI, class T, int STAGES = 2>
 static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   const int64_t tiles_m = (a.m + T::BM - 1) / T::BM;
   const int64_t tiles = tiles_m * tiles_n;
@@ -613,8 +729,8 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
               ok16(a.rope_sin) && ok16(a.k_out) && ok16(a.v_out) &&
               (a.kv_head_stride % 8 == 0);
   const int64_t grid = (tiles + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(gemm_kernel<EPI, T>, dim3(static_cast<unsigned>(grid)),
-                       dim3(kGemmThreads), 0, s, a);
+  return launch_kernel(gemm_kernel<EPI, T, STAGES>, dim3(static_cast<unsigned>(grid)),
+                       dim3(T::WAVES * kWave), 0, s, a);
 }
 
 // 128-row tiles unless they would leave CUs idle: at most 64 rows of X
@@ -622,6 +738,8 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
 // projections, N = 1024, at M = 2048) take 64-row tiles.
 template <int EPI>
 static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+  const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
+  if (a.m > 128 && tiles256 >= 256) return launch_tiles<EPI, GemmTile256, 3>(a, tiles_n, s);
   const int64_t tiles128 = (a.m + 127) / 128 * tiles_n;
   if (a.m <= 64 || tiles128 < 256) return launch_tiles<EPI, GemmTile64>(a, tiles_n, s);
   return launch_tiles<EPI, GemmTile128>(a, tiles_n, s);
