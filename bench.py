@@ -15,6 +15,9 @@ Also reported (extra keys, not ``value``):
     events: kernel execution only; one launch per token, layer 16, by
     default, since a timed launch adds a few microseconds of queue time), HBM traffic per launch from the
     committed FETCH_SIZE / WRITE_SIZE counter summary;
+  * decode_graph: config 4 again, the same number of steps continuing the
+    same sequence, replayed as one HIP graph per token (the position held
+    on the device; layer_streaming.DecodeGraph; skip: --no-decode-graph);
   * streamed: BASELINE config 3 -- full_pinned 16 GB host arena,
     matrix_group units through two 224 MiB slots, streamed vocabulary;
     decode ms/token and the PCIe-inclusive H2D GB/s (skip: --no-streamed);
@@ -69,6 +72,11 @@ def parse_args():
                         "per-stage kernels (matrix_group units); mlp = q|k|v and "
                         "attention per stage, o_proj..down_proj as one launch "
                         "(layer units); one = the whole layer as one launch")
+    p.add_argument("--no-decode-graph", action="store_true",
+                   help="config 4: skip the second timed run, which replays "
+                        "the same number of decode steps as one HIP graph per "
+                        "token (layer_streaming.DecodeGraph, per-stage "
+                        "launches) after the eager timed steps")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-streamed", action="store_true")
     p.add_argument("--streamed-steps", type=int, default=7)
@@ -188,6 +196,9 @@ def resident_decode(args):
     executor = Llama31DecodeExecutor(Llama31Config(), resident, top_k=10,
                                      layer_mode=args.layer_mode)
     total = args.context + args.warmup + args.steps + 1
+    graphed = not args.no_decode_graph and args.layer_mode == "stages"
+    if graphed:
+        total += args.warmup + args.steps + 1
     executor.reserve(total)
     cache = executor.kv_cache
     log("config 4: KV cache {} positions x 32 layers ~ N(0,1)".format(args.context))
@@ -221,6 +232,28 @@ def resident_decode(args):
         elapsed = time.perf_counter() - start
     timed_ms = executor.kernel_times_ms(group)
     ms_per_step = elapsed * 1000.0 / args.steps
+    graph = None
+    if graphed:
+        from layer_streaming import DecodeGraph
+
+        with torch.inference_mode():
+            decoder = DecodeGraph(executor, runtime, token,
+                                  args.warmup + args.steps + 1)
+            decoder.step(args.warmup)
+            torch.cuda.synchronize(dev)
+            log("config 4: timing {} graph-replayed decode steps".format(args.steps))
+            start = time.perf_counter()
+            decoder.step(args.steps)
+            torch.cuda.synchronize(dev)
+            g_elapsed = time.perf_counter() - start
+            decoder.check()
+            graph = {
+                "ms_per_step": round(g_elapsed * 1000.0 / args.steps, 4),
+                "tokens": args.steps,
+                "launches_per_step": "one graph replay (197 kernel nodes)",
+                "last_token": int(decoder.tokens()[0, -1]),
+            }
+            decoder.close()
     mean_context = args.context + args.warmup + (args.steps - 1) / 2.0
     result = {
         "ms_per_step": ms_per_step,
@@ -234,6 +267,8 @@ def resident_decode(args):
         "token_hbm_bytes": token_bytes(int(mean_context)),
         "last_token": int(token.reshape(-1)[0]),
     }
+    if graph is not None:
+        result["decode_graph"] = graph
     del executor, runtime, resident, cache
     torch.cuda.empty_cache()
     return result
@@ -556,6 +591,8 @@ def main():
             "launches_timed": resident["timed_launches"],
         },
     }
+    if "decode_graph" in resident:
+        line["decode_graph"] = resident["decode_graph"]
     if not args.no_streamed:
         s = streamed_decode(args)
         line["streamed"] = {

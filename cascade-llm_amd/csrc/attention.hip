@@ -62,6 +62,9 @@ struct AttnArgs {
   uint16_t *out;
   float *part_ml;      // [kv_heads][nsplits][G][2]  (max in log2 units, sum)
   float *part_acc;     // [kv_heads][nsplits][G][D]
+  // AT kernels: the length is this device word, clamped to [1, len] (len
+  // then holds the cache capacity, which sets span and nsplits)
+  const int64_t *len_word;
 };
 
 template <bool NT>
@@ -72,7 +75,7 @@ __device__ __forceinline__ u32x4 kv_load(const uint16_t *p) {
     return *reinterpret_cast<const u32x4 *>(p);
 }
 
-template <int WAVES, bool NT>
+template <int WAVES, bool NT, bool AT = false>
 __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
     AttnArgs a) {
   constexpr int G = kAttnG, D = kAttnD;
@@ -84,19 +87,39 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
   const int wave = tid / kWave;
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
-  const int begin = split * a.span;
-  const int end = min(begin + a.span, a.len);
-
-  __shared__ float s_ml[WAVES][G][2];
-  __shared__ float s_acc[WAVES][G][D];
-
   // q operand of dim chunk c: B[8 g4 + j][c16] = q[head c16][32 c + 8 g4 + j]
+  // (loaded first: under AT its latency overlaps the length's)
   u32x4 qop[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     qop[c] = c16 < G ? *reinterpret_cast<const u32x4 *>(
                            a.q + (g * G + c16) * D + 32 * c + 8 * g4)
                      : u32x4{0u, 0u, 0u, 0u};
+  int len = a.len;
+  if constexpr (AT)
+    len = static_cast<int>(
+        min(max(*a.len_word, int64_t{1}), static_cast<int64_t>(a.len)));
+  const int begin = split * a.span;
+  const int end = min(begin + a.span, len);
+  if constexpr (AT) {
+    if (begin >= len) {
+      // A split past the current length (the grid is sized for the
+      // capacity): an empty partial, m = -inf and l = 0, which the merge
+      // weighs 0.  Split 0 always holds position 0, so nsplits > 1 here.
+      const int64_t slot0 = (static_cast<int64_t>(g) * a.nsplits + split) * G;
+      for (int i = tid; i < G * D; i += WAVES * kWave)
+        a.part_acc[slot0 * D + i] = 0.0f;
+      if (tid < G) {
+        a.part_ml[(slot0 + tid) * 2] = -INFINITY;
+        a.part_ml[(slot0 + tid) * 2 + 1] = 0.0f;
+      }
+      return;
+    }
+  }
+
+  __shared__ float s_ml[WAVES][G][2];
+  __shared__ float s_acc[WAVES][G][D];
+
   const uint16_t *kb = a.k + g * a.head_stride;
   const uint16_t *vb = a.v + g * a.head_stride;
   const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
@@ -630,11 +653,14 @@ extern "C" size_t cascade_decode_attention_workspace_bytes(
   return attention_workspace(kAttnMaxSplits, n_kv_heads);
 }
 
-extern "C" int cascade_decode_attention_bf16(
-    const void *q, const void *k_cache, const void *v_cache,
-    int64_t kv_head_stride, int64_t len, int64_t n_q_heads, int64_t n_kv_heads,
-    int64_t head_dim, float scale, void *out, void *workspace,
-    size_t workspace_bytes, void *stream) {
+// Argument checks and packing shared by the two decode entry points; len
+// is the attended length (the capacity for the AT form).
+static int decode_attention_args(const void *q, const void *k_cache,
+                                 const void *v_cache, int64_t kv_head_stride,
+                                 int64_t len, int64_t n_q_heads,
+                                 int64_t n_kv_heads, int64_t head_dim,
+                                 float scale, void *out, void *workspace,
+                                 size_t workspace_bytes, AttnArgs &a) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       out == nullptr || workspace == nullptr)
     return CASCADE_EINVAL;
@@ -650,7 +676,6 @@ extern "C" int cascade_decode_attention_bf16(
   const AttnShape shape = attention_shape(len);
   if (workspace_bytes < attention_workspace(shape.nsplits, n_kv_heads))
     return CASCADE_EWORKSPACE;
-  AttnArgs a{};
   a.q = static_cast<const uint16_t *>(q);
   a.k = static_cast<const uint16_t *>(k_cache);
   a.v = static_cast<const uint16_t *>(v_cache);
@@ -665,16 +690,52 @@ extern "C" int cascade_decode_attention_bf16(
   a.part_ml = reinterpret_cast<float *>(ws + kAttnHeaderBytes);
   a.part_acc = reinterpret_cast<float *>(ws + kAttnHeaderBytes +
                                          per * 2 * sizeof(float));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(shape.nsplits),
+  return 0;
+}
+
+template <bool AT>
+static int launch_decode_attention(const AttnArgs &a, int64_t n_kv_heads,
+                                   hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.nsplits),
                   static_cast<unsigned>(n_kv_heads));
   const hipError_t e =
-      launch_kernel(decode_attention_kernel<kAttnWaves, true>, grid,
+      launch_kernel(decode_attention_kernel<kAttnWaves, true, AT>, grid,
                     dim3(kAttnWaves * kWave), 0, s, a);
-  if (e != hipSuccess || shape.nsplits == 1) return e;
+  if (e != hipSuccess || a.nsplits == 1) return e;
   return launch_kernel(decode_attention_merge_kernel,
                        dim3(static_cast<unsigned>(n_kv_heads * kAttnG)),
                        dim3(kMergeThreads), 0, s, a);
+}
+
+extern "C" int cascade_decode_attention_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, int64_t len, int64_t n_q_heads, int64_t n_kv_heads,
+    int64_t head_dim, float scale, void *out, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  AttnArgs a{};
+  if (int e = decode_attention_args(q, k_cache, v_cache, kv_head_stride, len,
+                                    n_q_heads, n_kv_heads, head_dim, scale,
+                                    out, workspace, workspace_bytes, a))
+    return e;
+  return launch_decode_attention<false>(a, n_kv_heads,
+                                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_decode_attention_at_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, const int64_t *length, int64_t capacity,
+    int64_t n_q_heads, int64_t n_kv_heads, int64_t head_dim, float scale,
+    void *out, void *workspace, size_t workspace_bytes, void *stream) {
+  if (length == nullptr) return CASCADE_EINVAL;
+  if (reinterpret_cast<uintptr_t>(length) & 7) return CASCADE_EALIGN;
+  AttnArgs a{};
+  if (int e = decode_attention_args(q, k_cache, v_cache, kv_head_stride,
+                                    capacity, n_q_heads, n_kv_heads, head_dim,
+                                    scale, out, workspace, workspace_bytes, a))
+    return e;
+  a.len_word = length;
+  return launch_decode_attention<true>(a, n_kv_heads,
+                                       static_cast<hipStream_t>(stream));
 }
 
 extern "C" int cascade_prefill_attention_bf16(

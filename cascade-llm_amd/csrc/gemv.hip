@@ -49,6 +49,11 @@ struct GemvArgs {
   uint16_t *v_out;
   int64_t kv_head_stride;
   int64_t n_tiles;
+  // qkv at a device-held position (nullable): the token's position is
+  // *length - 1, clamped to [0, capacity); rope_cos / rope_sin then point at
+  // row 0 of the tables and k_out / v_out at position 0 of the cache
+  const int64_t *length;
+  int64_t capacity;
 };
 
 constexpr int kHeadDim = 128;
@@ -168,13 +173,24 @@ __device__ __forceinline__ void tile_rows(const GemvArgs &a, int64_t tile,
 template <int EPI, int R>
 __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
                                          const float (&acc)[R],
-                                         const bool (&ok)[R]) {
+                                         const bool (&ok)[R],
+                                         int64_t length_word) {
   if constexpr (EPI == kQkvRope) {
     constexpr int P = R / 2;
     constexpr int kTilesPerHead = kHalfHead / P;
     const int64_t head = tile / kTilesPerHead;
     const int d0 = static_cast<int>(tile % kTilesPerHead) * P;
     const int64_t hq = a.n0 / kHeadDim, hk = a.n1 / kHeadDim;
+    const uint16_t *rope_cos = a.rope_cos, *rope_sin = a.rope_sin;
+    uint16_t *k_out = a.k_out, *v_out = a.v_out;
+    if (a.length != nullptr) {
+      const int64_t pos =
+          min(max(length_word - 1, int64_t{0}), a.capacity - 1);
+      rope_cos += pos * kHalfHead;
+      rope_sin += pos * kHalfHead;
+      k_out += pos * kHeadDim;
+      v_out += pos * kHeadDim;
+    }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int d = d0 + p;
@@ -185,8 +201,8 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
         // apply_rotary_pos_emb: x*cos + rotate_half(x)*sin, every product
         // and the sum rounded to bf16; cos/sin are bf16 and identical for
         // d and d + 64 (emb = cat(freqs, freqs)).
-        const float c = bf16_to_f32(a.rope_cos[d]);
-        const float s = bf16_to_f32(a.rope_sin[d]);
+        const float c = bf16_to_f32(rope_cos[d]);
+        const float s = bf16_to_f32(rope_sin[d]);
         oa = f32_to_bf16(round_bf16(xa * c) + round_bf16(-xb * s));
         ob = f32_to_bf16(round_bf16(xb * c) + round_bf16(xa * s));
       } else {
@@ -197,11 +213,11 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
         a.y[head * kHeadDim + d] = oa;
         a.y[head * kHeadDim + d + kHalfHead] = ob;
       } else if (head < hq + hk) {
-        uint16_t *dst = a.k_out + (head - hq) * a.kv_head_stride;
+        uint16_t *dst = k_out + (head - hq) * a.kv_head_stride;
         dst[d] = oa;
         dst[d + kHalfHead] = ob;
       } else {
-        uint16_t *dst = a.v_out + (head - hq - hk) * a.kv_head_stride;
+        uint16_t *dst = v_out + (head - hq - hk) * a.kv_head_stride;
         dst[d] = oa;
         dst[d + kHalfHead] = ob;
       }
@@ -250,6 +266,16 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
   const int wave = threadIdx.x / kWave;
   const int64_t tile = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
   const bool tile_ok = tile < a.n_tiles;
+
+  // A device-held position is loaded up front and unconditionally (x, 16
+  // readable bytes, stands in when the position came from the host), so the
+  // load is in flight with the weight loads instead of waited for on the
+  // spot at the end of a branch.
+  int64_t length_word = 0;
+  if constexpr (EPI == kQkvRope)
+    length_word = *(a.length != nullptr
+                        ? a.length
+                        : reinterpret_cast<const int64_t *>(a.x));
 
   const uint16_t *wrow[R];
   bool ok[R];
@@ -303,7 +329,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-  if (lane == 0 && tile_ok) epilogue<EPI, R>(a, tile, acc, ok);
+  if (lane == 0 && tile_ok) epilogue<EPI, R>(a, tile, acc, ok, length_word);
 }
 
 template <int KC, int R, int WAVES, int EPI, bool NT>
@@ -416,14 +442,13 @@ extern "C" int cascade_gemv_residual_bf16(const void *w, const void *x,
   return dispatch_gemv<1, kResidual>(a, s);
 }
 
-extern "C" int cascade_qkv_rope_bf16(const void *wq, const void *wk,
-                                     const void *wv, int64_t nq, int64_t nk,
-                                     int64_t nv, int64_t k, const void *x,
-                                     const void *norm_weight, float eps,
-                                     const void *rope_cos,
-                                     const void *rope_sin, void *q_out,
-                                     void *k_out, void *v_out,
-                                     int64_t kv_head_stride, void *stream) {
+// Argument checks and packing shared by the two q|k|v entry points.
+static int qkv_rope_args(const void *wq, const void *wk, const void *wv,
+                         int64_t nq, int64_t nk, int64_t nv, int64_t k,
+                         const void *x, const void *norm_weight, float eps,
+                         const void *rope_cos, const void *rope_sin,
+                         void *q_out, void *k_out, void *v_out,
+                         int64_t kv_head_stride, GemvArgs &a) {
   if (nq < 0 || nk < 0 || nv < 0) return CASCADE_EINVAL;
   if ((nq % kHeadDim) || (nk % kHeadDim) || (nv % kHeadDim))
     return CASCADE_ESHAPE;
@@ -441,7 +466,6 @@ extern "C" int cascade_qkv_rope_bf16(const void *wq, const void *wk,
   if ((nq || nk) && (rope_cos == nullptr || rope_sin == nullptr))
     return CASCADE_EINVAL;
   if ((nk || nv) && kv_head_stride < kHeadDim) return CASCADE_EINVAL;
-  GemvArgs a{};
   a.w0 = static_cast<const uint16_t *>(wq);
   a.w1 = static_cast<const uint16_t *>(wk);
   a.w2 = static_cast<const uint16_t *>(wv);
@@ -459,6 +483,42 @@ extern "C" int cascade_qkv_rope_bf16(const void *wq, const void *wk,
   a.v_out = static_cast<uint16_t *>(v_out);
   a.kv_head_stride = kv_head_stride;
   a.n_tiles = total / 2;  // two rows (d, d + 64) per tile
+  return 0;
+}
+
+extern "C" int cascade_qkv_rope_bf16(const void *wq, const void *wk,
+                                     const void *wv, int64_t nq, int64_t nk,
+                                     int64_t nv, int64_t k, const void *x,
+                                     const void *norm_weight, float eps,
+                                     const void *rope_cos,
+                                     const void *rope_sin, void *q_out,
+                                     void *k_out, void *v_out,
+                                     int64_t kv_head_stride, void *stream) {
+  GemvArgs a{};
+  if (int e = qkv_rope_args(wq, wk, wv, nq, nk, nv, k, x, norm_weight, eps,
+                            rope_cos, rope_sin, q_out, k_out, v_out,
+                            kv_head_stride, a))
+    return e;
+  return dispatch_gemv<2, kQkvRope>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_qkv_rope_at_bf16(
+    const void *wq, const void *wk, const void *wv, int64_t nq, int64_t nk,
+    int64_t nv, int64_t k, const void *x, const void *norm_weight, float eps,
+    const void *rope_cos_table, const void *rope_sin_table, void *q_out,
+    void *k_cache, void *v_cache, int64_t kv_head_stride,
+    const int64_t *length, int64_t capacity, void *stream) {
+  if (length == nullptr || capacity <= 0 || capacity > (int64_t{1} << 30))
+    return CASCADE_EINVAL;
+  if (reinterpret_cast<uintptr_t>(length) & 7) return CASCADE_EALIGN;
+  if ((nk || nv) && kv_head_stride < capacity * kHeadDim) return CASCADE_EINVAL;
+  GemvArgs a{};
+  if (int e = qkv_rope_args(wq, wk, wv, nq, nk, nv, k, x, norm_weight, eps,
+                            rope_cos_table, rope_sin_table, q_out, k_cache,
+                            v_cache, kv_head_stride, a))
+    return e;
+  a.length = length;
+  a.capacity = capacity;
   return dispatch_gemv<2, kQkvRope>(a, static_cast<hipStream_t>(stream));
 }
 

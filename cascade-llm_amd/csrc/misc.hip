@@ -24,6 +24,40 @@ __global__ __launch_bounds__(kGatherThreads) void embedding_gather_kernel(
   for (int64_t j = threadIdx.x; j < nvec; j += kGatherThreads) dst[j] = src[j];
 }
 
+// First kernel of a decode step whose position lives on the device: the
+// gather of ids[0] as above, and the step's bookkeeping by thread 0 --
+// history[L] = ids[0] (the token that sits at position L) and *length =
+// L + 1, L being the cached length before the step.  A length outside
+// [0, capacity) is left as it is and sets *error_flag.  Nothing else in
+// the kernel reads *length, and later kernels of the stream see the new
+// value.
+__global__ __launch_bounds__(kGatherThreads) void decode_step_begin_kernel(
+    const uint16_t *table, int64_t vocab, int64_t hidden, const int64_t *ids,
+    uint16_t *out, int64_t *length, int64_t *history, int64_t capacity,
+    int32_t *error_flag) {
+  const int64_t id = ids[0];
+  const int64_t nvec = hidden >> 3;
+  u32x4 *dst = reinterpret_cast<u32x4 *>(out);
+  const bool id_ok = id >= 0 && id < vocab;
+  if (threadIdx.x == 0) {
+    const int64_t len = *length;
+    if (len >= 0 && len < capacity) {
+      history[len] = id;
+      *length = len + 1;
+    } else if (error_flag != nullptr) {
+      *error_flag = 1;
+    }
+    if (!id_ok && error_flag != nullptr) *error_flag = 1;
+  }
+  if (!id_ok) {
+    for (int64_t j = threadIdx.x; j < nvec; j += kGatherThreads)
+      dst[j] = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const u32x4 *src = reinterpret_cast<const u32x4 *>(table + id * hidden);
+  for (int64_t j = threadIdx.x; j < nvec; j += kGatherThreads) dst[j] = src[j];
+}
+
 constexpr int kStreamThreads = 256;
 
 __global__ __launch_bounds__(kStreamThreads) void hbm_read_kernel(
@@ -98,6 +132,26 @@ extern "C" int cascade_embedding_gather_bf16(const void *table, int64_t vocab,
                        0, static_cast<hipStream_t>(stream),
                        static_cast<const uint16_t *>(table), vocab, hidden, ids,
                        static_cast<uint16_t *>(out), error_flag);
+}
+
+extern "C" int cascade_decode_step_begin_bf16(
+    const void *table, int64_t vocab, int64_t hidden, const int64_t *ids,
+    void *out, int64_t *length, int64_t *history, int64_t capacity,
+    int32_t *error_flag, void *stream) {
+  if (table == nullptr || ids == nullptr || out == nullptr ||
+      length == nullptr || history == nullptr)
+    return CASCADE_EINVAL;
+  if (vocab <= 0 || hidden <= 0 || capacity <= 0) return CASCADE_EINVAL;
+  if ((hidden & 7) || !aligned16(table) || !aligned16(out) ||
+      (reinterpret_cast<uintptr_t>(ids) & 7) ||
+      (reinterpret_cast<uintptr_t>(length) & 7) ||
+      (reinterpret_cast<uintptr_t>(history) & 7))
+    return CASCADE_EALIGN;
+  return launch_kernel(decode_step_begin_kernel, dim3(1), dim3(kGatherThreads),
+                       0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t *>(table), vocab, hidden, ids,
+                       static_cast<uint16_t *>(out), length, history, capacity,
+                       error_flag);
 }
 
 extern "C" int cascade_memcpy_h2d_async(void *dst, const void *src,

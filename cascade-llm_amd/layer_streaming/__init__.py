@@ -6,6 +6,7 @@ libcascade_hip.so (see ``layer_streaming._hip``), which must be built --
 nothing here falls back to other device code.
 """
 
+from .graph import DecodeGraph
 from .llama31 import (
     LLAMA31_8B_MODEL_ID,
     Llama31Config,
@@ -31,6 +32,7 @@ from .weight_store import (
 )
 
 __all__ = [
+    "DecodeGraph",
     "DoubleBufferRuntime",
     "FullPinnedWeightStore",
     "Granularity",

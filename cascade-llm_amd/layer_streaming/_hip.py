@@ -49,6 +49,11 @@ _SIGNATURES = {
         [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P,
          _I64, _P],
     ),
+    "cascade_qkv_rope_at_bf16": (
+        _INT,
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P,
+         _I64, _P, _I64, _P],
+    ),
     "cascade_gate_up_swiglu_bf16": (
         _INT, [_P, _P, _I64, _I64, _P, _P, _F, _P, _P]),
     "cascade_gate_silu_bf16": (_INT, [_P, _I64, _I64, _P, _P, _F, _P, _P]),
@@ -57,6 +62,10 @@ _SIGNATURES = {
     "cascade_decode_attention_bf16": (
         _INT,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P],
+    ),
+    "cascade_decode_attention_at_bf16": (
+        _INT,
+        [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P],
     ),
     "cascade_decode_layer_workspace_bytes": (_SZ, []),
     "cascade_decode_layer_bf16": (
@@ -89,6 +98,8 @@ _SIGNATURES = {
     ),
     "cascade_embedding_gather_bf16": (
         _INT, [_P, _I64, _I64, _P, _I64, _P, _P, _P]),
+    "cascade_decode_step_begin_bf16": (
+        _INT, [_P, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P]),
     "cascade_memcpy_h2d_async": (_INT, [_P, _P, _SZ, _P]),
     "cascade_memcpy_d2d_async": (_INT, [_P, _P, _SZ, _P]),
     "cascade_event_create": (_INT, [ctypes.POINTER(_U64), _INT]),
@@ -580,6 +591,99 @@ def decode_attention(q, k_cache, v_cache, kv_head_stride, length, out,
          v_cache.data_ptr(), int(kv_head_stride), int(length), n_q_heads,
          n_kv_heads, head_dim, float(scale), out.data_ptr(),
          workspace.data_ptr(), workspace.numel(), stream_handle(stream))
+    return out
+
+
+def _length_word(length, capacity):
+    require_device(length, "length", torch.int64, 1)
+    if int(capacity) <= 0:
+        raise ValueError("capacity must be positive")
+
+
+def qkv_rope_at(wq, wk, wv, x, norm_weight, eps, rope_cos, rope_sin, q_out,
+                k_cache, v_cache, kv_head_stride, length, capacity,
+                stream=None):
+    """q|k|v + RoPE + KV write at the position *length - 1 held on the device.
+
+    rope_cos / rope_sin are the [capacity, 64] tables; k_cache / v_cache are
+    views at position 0 of KV head 0 of the layer cache.
+    """
+
+    _length_word(length, capacity)
+    nq = 0 if wq is None else _matrix(wq, "wq")[0]
+    nk = 0 if wk is None else _matrix(wk, "wk")[0]
+    nv = 0 if wv is None else _matrix(wv, "wv")[0]
+    k = _matrix(next(w for w in (wq, wk, wv) if w is not None), "w")[1]
+    _bf16(x, "x", k)
+    if norm_weight is not None:
+        _bf16(norm_weight, "norm_weight", k)
+    if nq or nk:
+        _bf16(rope_cos, "rope_cos", capacity * 64)
+        _bf16(rope_sin, "rope_sin", capacity * 64)
+    if nq:
+        _bf16(q_out, "q_out", nq)
+    for name, buf, heads in (("k_cache", k_cache, nk // 128),
+                             ("v_cache", v_cache, nv // 128)):
+        if heads:
+            require_device(buf, name, torch.bfloat16, contiguous=False)
+            if buf.storage_offset() + (heads - 1) * kv_head_stride + (
+                capacity * 128
+            ) > buf.untyped_storage().nbytes() // 2:
+                raise ValueError("{} cannot hold {} positions".format(name, capacity))
+
+    def ptr(t):
+        return 0 if t is None else t.data_ptr()
+
+    call("cascade_qkv_rope_at_bf16", ptr(wq), ptr(wk), ptr(wv), nq, nk, nv, k,
+         x.data_ptr(), ptr(norm_weight), float(eps),
+         ptr(rope_cos) if (nq or nk) else 0,
+         ptr(rope_sin) if (nq or nk) else 0,
+         ptr(q_out) if nq else 0, ptr(k_cache) if nk else 0,
+         ptr(v_cache) if nv else 0, int(kv_head_stride), length.data_ptr(),
+         int(capacity), stream_handle(stream))
+
+
+def decode_attention_at(q, k_cache, v_cache, kv_head_stride, length, capacity,
+                        out, workspace, scale, n_q_heads=32, n_kv_heads=8,
+                        head_dim=128, stream=None):
+    """decode_attention over positions [0, *length) held on the device; the
+    split plan follows ``capacity``."""
+
+    _length_word(length, capacity)
+    _bf16(q, "q", n_q_heads * head_dim)
+    _bf16(out, "out", n_q_heads * head_dim)
+    for name, buf in (("k_cache", k_cache), ("v_cache", v_cache)):
+        require_device(buf, name, torch.bfloat16, contiguous=False)
+        end = buf.storage_offset() + (n_kv_heads - 1) * kv_head_stride + (
+            capacity * head_dim
+        )
+        if end > buf.untyped_storage().nbytes() // 2:
+            raise ValueError("{} is too small for capacity {}".format(name, capacity))
+    require_device(workspace, "workspace", torch.uint8)
+    call("cascade_decode_attention_at_bf16", q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), int(kv_head_stride), length.data_ptr(),
+         int(capacity), n_q_heads, n_kv_heads, head_dim, float(scale),
+         out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+         stream_handle(stream))
+    return out
+
+
+def decode_step_begin(table, ids, out, length, history, error_flag=None,
+                      stream=None):
+    """Gather table[ids[0]] into out, then history[L] = ids[0] and
+    *length = L + 1 (L = *length on entry, 0 <= L < history.numel())."""
+
+    vocab, hidden = _matrix(table, "table")
+    require_device(ids, "ids", torch.int64, contiguous=False)
+    _bf16(out, "out", hidden)
+    require_device(history, "history", torch.int64)
+    _length_word(length, history.numel())
+    if error_flag is not None:
+        require_device(error_flag, "error_flag", torch.int32, 1)
+    call("cascade_decode_step_begin_bf16", table.data_ptr(), vocab, hidden,
+         ids.data_ptr(), out.data_ptr(), length.data_ptr(), history.data_ptr(),
+         history.numel(), 0 if error_flag is None else error_flag.data_ptr(),
+         stream_handle(stream))
     return out
 
 

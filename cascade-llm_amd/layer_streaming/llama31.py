@@ -278,6 +278,12 @@ class Llama31DecodeExecutor:
         self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
         self._k_layer = lib.cascade_decode_layer_bf16
         self._k_mlp = lib.cascade_decode_mlp_bf16
+        self._k_qkv_at = lib.cascade_qkv_rope_at_bf16
+        self._k_attn_at = lib.cascade_decode_attention_at_bf16
+        self._k_step_begin = lib.cascade_decode_step_begin_bf16
+        # Set by DecodeGraph (layer_streaming/graph.py): decode steps take
+        # their position from a device word instead of host values.
+        self._device_step = None
         self._batched = False
         self._first_slot = 0
         self._unit_cache = {}
@@ -374,8 +380,18 @@ class Llama31DecodeExecutor:
             ids = input_ids.reshape(-1)
             if ids.device != self.device or ids.dtype != torch.long:
                 ids = ids.to(device=self.device, dtype=torch.long)
-            _hip.embedding_gather(self.resident["model.embed_tokens.weight"],
-                                  ids, hidden)
+            table = self.resident["model.embed_tokens.weight"]
+            step = self._device_step
+            if step is None:
+                _hip.embedding_gather(table, ids, hidden)
+            else:
+                if sequence != 1:
+                    raise ValueError("a device-position step decodes one token")
+                _hip.check("cascade_decode_step_begin_bf16", self._k_step_begin(
+                    table.data_ptr(), table.shape[0], self.hidden,
+                    ids.data_ptr(), hidden.data_ptr(), step.length.data_ptr(),
+                    step.history.data_ptr(), step.capacity,
+                    step.error.data_ptr(), self._stream()))
         else:
             hidden = self.vocab_runtime.embedding(input_ids)
         _hip.require_device(hidden, "hidden_states", torch.bfloat16,
@@ -443,6 +459,19 @@ class Llama31DecodeExecutor:
         cos = self.rope.cos.data_ptr()
         sin = self.rope.sin.data_ptr()
         half = self.head_dim // 2
+        step = self._device_step
+        if step is not None:
+            # position = *length - 1 on the device; tables and cache from row 0
+            ev = self._mark_begin("qkv")
+            rc = self._k_qkv_at(
+                wq, wk, wv, nq, nk, nv, self.hidden, x, norm, self.eps, cos, sin,
+                self._q_ptr if wq else 0,
+                self._kv_pointer(layer, 0, 0) if wk else 0,
+                self._kv_pointer(layer, 1, 0) if wv else 0,
+                stride, step.length.data_ptr(), step.capacity, stream)
+            self._mark_end("qkv", ev, rc)
+            _hip.check("cascade_qkv_rope_at_bf16", rc)
+            return
         for t, slot in enumerate(self._slots(state)):
             pos = state.positions[t]
             ev = self._mark_begin("qkv")
@@ -462,8 +491,19 @@ class Llama31DecodeExecutor:
         v0 = self._kv_pointer(layer, 1, 0)
         stride = self.kv_cache.head_stride
         ws, ws_bytes = self._attn_ws.data_ptr(), self._attn_ws.numel()
+        step = self._device_step
         for t, slot in enumerate(self._slots(state)):
             ev = self._mark_begin("attention")
+            if step is not None:
+                rc = self._k_attn_at(
+                    self._q_ptr, k0, v0, stride, step.length.data_ptr(),
+                    step.capacity, self.n_heads, self.n_kv_heads, self.head_dim,
+                    self.scale, self._attn_ptr, ws, ws_bytes, stream)
+                self._mark_end("attention", ev, rc)
+                _hip.check("cascade_decode_attention_at_bf16", rc)
+                if with_o:
+                    self._o_residual(ptrs, state, t, stream)
+                continue
             rc = self._k_attn(self._q_ptr + t * row, k0, v0, stride, slot + 1,
                               self.n_heads, self.n_kv_heads, self.head_dim,
                               self.scale, self._attn_ptr + t * row, ws, ws_bytes,
@@ -839,9 +879,17 @@ class Llama31DecodeExecutor:
             self._head_ws = torch.zeros(size, dtype=torch.uint8, device=self.device)
             self._head = (head.data_ptr(), vocab)
         head_ptr, vocab = self._head
-        logits = torch.empty((1, count, vocab), dtype=torch.float32, device=self.device)
-        values = torch.empty((1, 1, self.top_k), dtype=torch.float32, device=self.device)
-        indices = torch.empty((1, 1, self.top_k), dtype=torch.int64, device=self.device)
+        step = self._device_step
+        if step is not None and count == 1:
+            # fixed buffers: the next step's input is indices[0, 0, 0]
+            logits, values, indices = step.logits, step.values, step.indices
+        else:
+            logits = torch.empty((1, count, vocab), dtype=torch.float32,
+                                 device=self.device)
+            values = torch.empty((1, 1, self.top_k), dtype=torch.float32,
+                                 device=self.device)
+            indices = torch.empty((1, 1, self.top_k), dtype=torch.int64,
+                                  device=self.device)
         ws, ws_bytes = self._head_ws.data_ptr(), self._head_ws.numel()
         first = 0
         if count > 1:

@@ -85,6 +85,24 @@ int cascade_qkv_rope_bf16(const void *wq, const void *wk, const void *wv,
                           const void *rope_cos, const void *rope_sin,
                           void *q_out, void *k_out, void *v_out,
                           int64_t kv_head_stride, void *stream);
+/* The same for a decode step whose position is held on the device (so that
+ * one captured HIP graph of the step serves every token): the position is
+ * p = *length - 1, clamped to [0, capacity).  rope_cos_table /
+ * rope_sin_table are the [capacity, 64] bf16 tables (row p is used);
+ * k_cache / v_cache point at position 0 of KV head 0 of this layer's cache,
+ * kv_head_stride >= capacity * 128; K / V land at position p.  length is an
+ * 8-byte aligned device int64 (cascade_decode_step_begin_bf16 advances it).
+ * Same computation and replaced code as cascade_qkv_rope_bf16, with the
+ * position the reference derives on the host per token (position_ids from
+ * the cache length, llama31.py:131-143).                                   */
+int cascade_qkv_rope_at_bf16(const void *wq, const void *wk, const void *wv,
+                             int64_t nq, int64_t nk, int64_t nv, int64_t k,
+                             const void *x, const void *norm_weight, float eps,
+                             const void *rope_cos_table,
+                             const void *rope_sin_table, void *q_out,
+                             void *k_cache, void *v_cache,
+                             int64_t kv_head_stride, const int64_t *length,
+                             int64_t capacity, void *stream);
 
 /* Fused post-attention RMSNorm + gate/up projections + SwiGLU:
  *   y[i] = bf16(bf16(silu(bf16(Wg[i] . n))) * bf16(Wu[i] . n)), i < n_half
@@ -128,6 +146,19 @@ int cascade_decode_attention_bf16(const void *q, const void *k_cache,
                                   int64_t n_kv_heads, int64_t head_dim,
                                   float scale, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream);
+/* The same over positions [0, L) with L = *length (device int64, clamped to
+ * [1, capacity]).  The split plan, and with it the launch shape, follows
+ * capacity, so one captured launch serves every L <= capacity; splits past
+ * L contribute nothing.  kv_head_stride >= capacity * head_dim; workspace as
+ * above (cascade_decode_attention_workspace_bytes(capacity, ...)).         */
+int cascade_decode_attention_at_bf16(const void *q, const void *k_cache,
+                                     const void *v_cache,
+                                     int64_t kv_head_stride,
+                                     const int64_t *length, int64_t capacity,
+                                     int64_t n_q_heads, int64_t n_kv_heads,
+                                     int64_t head_dim, float scale, void *out,
+                                     void *workspace, size_t workspace_bytes,
+                                     void *stream);
 
 /* One whole decoder layer of batch-1 decode in one launch (Llama-3.1-8B
  * shape only: hidden 4096, 32 query / 8 KV heads of 128, intermediate
@@ -280,6 +311,21 @@ int cascade_embedding_gather_bf16(const void *table, int64_t vocab,
                                   int64_t hidden, const int64_t *ids,
                                   int64_t n_ids, void *out, int32_t *error_flag,
                                   void *stream);
+/* First launch of a decode step with a device-held position: out[:] =
+ * table[ids[0], :] as above, then, with L = *length on entry (the cached
+ * length), history[L] = ids[0] and *length = L + 1.  L outside
+ * [0, capacity) leaves *length and history unchanged and sets *error_flag.
+ * ids, length and history (int64 [capacity]) are 8-byte aligned device
+ * pointers; error_flag is nullable.  With ids pointing at the previous
+ * step's top-1 output, a captured step feeds itself, and history collects
+ * the greedy token sequence by position.  Replaces the per-token embedding
+ * and the host's token / position bookkeeping of the decode loop,
+ * tools/run_llama31.py:105-121 and llama31.py:128-150.                     */
+int cascade_decode_step_begin_bf16(const void *table, int64_t vocab,
+                                   int64_t hidden, const int64_t *ids,
+                                   void *out, int64_t *length,
+                                   int64_t *history, int64_t capacity,
+                                   int32_t *error_flag, void *stream);
 
 /* ------------------------------------------------------- copy pipeline
  * Thin wrappers so the two-slot pipeline runs on hipMemcpyAsync + hipEvent:

@@ -82,6 +82,39 @@ def test_argument_checks_reject_without_launching():
     assert layer(length=(1 << 23) + 1, stride=128 << 24) == 1001
     assert layer(stride=128 * 4) == 1001   # stride < len * head_dim
     assert layer(ws_bytes=ws - 1) == 1004
+    # device-position forms: the length word must be given and 8-byte
+    # aligned, the capacity positive, the cache stride >= capacity * 128
+    def qkv_at(length=16, capacity=10, stride=128 * 10):
+        return lib.cascade_qkv_rope_at_bf16(16, 16, 16, 4096, 1024, 1024, 4096, 16,
+                                            16, 1e-5, 16, 16, 16, 16, 16, stride,
+                                            length, capacity, None)
+
+    assert qkv_at(length=None) == 1001
+    assert qkv_at(length=20) == 1002
+    assert qkv_at(capacity=0) == 1001
+    assert qkv_at(stride=128 * 9) == 1001
+    attn_ws = _hip.attention_workspace_bytes(10)
+
+    def attn_at(length=16, capacity=10, stride=128 * 10, ws_bytes=attn_ws):
+        return lib.cascade_decode_attention_at_bf16(16, 16, 16, stride, length,
+                                                    capacity, 32, 8, 128, 0.1, 16,
+                                                    16, ws_bytes, None)
+
+    assert attn_at(length=None) == 1001
+    assert attn_at(length=12) == 1002
+    assert attn_at(capacity=0) == 1001
+    assert attn_at(stride=128 * 9) == 1001
+    assert attn_at(ws_bytes=16) == 1004
+
+    def begin(ids=16, length=16, history=16, capacity=8):
+        return lib.cascade_decode_step_begin_bf16(16, 100, 64, ids, 16, length,
+                                                  history, capacity, None, None)
+
+    assert begin(ids=None) == 1001
+    assert begin(history=None) == 1001
+    assert begin(capacity=0) == 1001
+    assert begin(length=12) == 1002
+    assert begin(ids=20) == 1002
 
 
 def test_workspace_sizes():

@@ -97,6 +97,39 @@ class FakeKernels:
         at(out, hq * dim).copy_(ref.attention(qq, keys, vals, length - 1).reshape(-1))
         return 0
 
+    # device-position forms: the C ABI's position / length rules, then the
+    # host-position doubles at those pointers
+    def qkv_at(self, wq, wk, wv, nq, nk, nv, k, x, norm, eps, cos_t, sin_t,
+               q_out, k_cache, v_cache, stride, length, capacity, stream):
+        p = min(max(int(at(length, 1, torch.int64)[0]) - 1, 0), capacity - 1)
+        self.qkv(wq, wk, wv, nq, nk, nv, k, x, norm, eps, cos_t + 128 * p,
+                 sin_t + 128 * p, q_out, k_cache + 256 * p if k_cache else 0,
+                 v_cache + 256 * p if v_cache else 0, stride, stream)
+        self.calls[-1] = "qkv_at"
+        return 0
+
+    def attention_at(self, q, k0, v0, stride, length, capacity, hq, hkv, dim,
+                     scale, out, ws, ws_bytes, stream):
+        n = min(max(int(at(length, 1, torch.int64)[0]), 1), capacity)
+        self.attention(q, k0, v0, stride, n, hq, hkv, dim, scale, out, ws,
+                       ws_bytes, stream)
+        self.calls[-1] = "attention_at"
+        return 0
+
+    def step_begin(self, table, vocab, hidden, ids, out, length, history,
+                   capacity, error, stream):
+        self.calls.append("step_begin")
+        token = int(at(ids, 1, torch.int64)[0])
+        word = at(length, 1, torch.int64)
+        n = int(word[0])
+        at(out, hidden).copy_(at(table + 2 * token * hidden, hidden))
+        if 0 <= n < capacity:
+            at(history, capacity, torch.int64)[n] = token
+            word[0] = n + 1
+        else:
+            at(error, 1, torch.int32)[0] = 1
+        return 0
+
     def residual(self, w, x, res, y, n, k, stream):
         self.calls.append("residual")
         out = at(res, n).reshape(1, n) + ref.linear(at(x, k).reshape(1, k),
@@ -318,6 +351,8 @@ def make_executor(monkeypatch, plan, store, layer_mode="stages"):
     ex._k_f32_gemm = fakes.f32_gemm
     ex._k_layer = fakes.layer
     ex._k_mlp = fakes.mlp
+    ex._k_qkv_at, ex._k_attn_at = fakes.qkv_at, fakes.attention_at
+    ex._k_step_begin = fakes.step_begin
     return ex, fakes
 
 
@@ -378,6 +413,54 @@ def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
     assert fakes.calls.count("f32_gemm") == 1
     expected = (LAYERS * per_prefill + 3) + 3 * (LAYERS * per_token + 2)
     assert len(fakes.calls) == expected
+
+
+def test_device_step_decode_matches_oracle(monkeypatch, weights, exact_oracle):
+    # The executor in DecodeGraph's mode (position and length read from a
+    # device word, top-k into fixed buffers whose first id feeds the next
+    # step): same logits, top-k and cache as the oracle, and the length word
+    # and token history advance by one per step.
+    from layer_streaming.graph import DeviceStep
+
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    executor, fakes = make_executor(monkeypatch, plan, weights)
+    oracle = ref.OracleLlama(weights.tensor, LAYERS)
+    prompt = [7, 99, 1234, 5, 128255, 0]
+    _, _, ei = oracle.step(prompt, 5)
+    executor.finish(run_units(plan, weights, executor,
+                              executor.begin(torch.tensor([prompt]))))
+    past = len(prompt)
+    step = DeviceStep("cpu", past + 4, 128256, 5)
+    executor.reserve(past + 4)
+    step.length.fill_(past)
+    token = int(ei[0])
+    step.indices.view(-1)[0] = token
+    executor._device_step = step
+    fakes.calls.clear()
+    for i in range(3):
+        expected_logits, _, ei = oracle.step([token], 5)
+        state = run_units(plan, weights, executor, executor.begin(step.ids))
+        state = executor.finish(state)
+        assert state.logits is step.logits
+        assert torch.equal(step.logits[0, -1], expected_logits)
+        assert step.indices.reshape(-1).tolist() == ei.tolist()
+        assert int(step.length[0]) == past + i + 1
+        assert int(step.history[past + i]) == token
+        token = int(ei[0])
+    assert int(step.error[0]) == 0
+    # every position-dependent launch took the device-word form
+    assert fakes.calls.count("step_begin") == 3
+    assert fakes.calls.count("qkv_at") == 3 * LAYERS
+    assert fakes.calls.count("attention_at") == 3 * LAYERS
+    assert "qkv" not in fakes.calls and "attention" not in fakes.calls
+    for layer in range(LAYERS):
+        k, v = executor.kv_cache.entries[layer]
+        assert torch.equal(k[0], oracle.caches[layer]["k"])
+        assert torch.equal(v[0], oracle.caches[layer]["v"])
+    # a step past the capacity is refused by the first launch
+    step.length.fill_(past + 4)
+    run_units(plan, weights, executor, executor.begin(step.ids))
+    assert int(step.error[0]) == 1 and int(step.length[0]) == past + 4
 
 
 def test_rope_table_equals_oracle_cos_sin():
