@@ -95,11 +95,51 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
     qop[c] = c16 < G ? *reinterpret_cast<const u32x4 *>(
                            a.q + (g * G + c16) * D + 32 * c + 8 * g4)
                      : u32x4{0u, 0u, 0u, 0u};
-  int len = a.len;
-  if constexpr (AT)
-    len = static_cast<int>(
-        min(max(*a.len_word, int64_t{1}), static_cast<int64_t>(a.len)));
   const int begin = split * a.span;
+  const uint16_t *kb = a.k + g * a.head_stride;
+  const uint16_t *vb = a.v + g * a.head_stride;
+  const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
+
+  // K rows of the block as two MFMA halves, V rows as 8 whole rows per lane;
+  // rows past last repeat row last
+  auto load_block = [&](int r0, int last, u32x4 (&kt)[2][4], u32x4 (&vt)[8]) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = min(r0 + krow + 4 * hf, last);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kt[hf][c] = kv_load<NT>(kb + static_cast<int64_t>(row) * D + 32 * c +
+                                8 * g4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = min(r0 + 8 * g4 + j, last);
+      vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
+    }
+  };
+
+  // AT: the wave's first block is loaded before the length is known, its
+  // rows clamped to the capacity (allocated rows, whatever they hold); rows
+  // at or past the length are masked once it is known -- scores -inf as in
+  // any block, and V zeroed, since an unwritten row may hold NaN and 0 NaN
+  // is NaN in the P V product.
+  // The empty asm consumes the block so the compiler cannot sink its loads
+  // below the length test; the length's scalar load is issued first, and
+  // both latencies overlap.
+  int64_t len_word = a.len;
+  if constexpr (AT) len_word = *a.len_word;
+  u32x4 kt0[2][4], vt0[8];
+  if constexpr (AT) {
+    load_block(begin + wave * kAttnBlock, min(begin + a.span, a.len) - 1, kt0,
+               vt0);
+    asm volatile("" ::"v"(kt0[0][0]), "v"(kt0[0][1]), "v"(kt0[0][2]),
+                 "v"(kt0[0][3]), "v"(kt0[1][0]), "v"(kt0[1][1]),
+                 "v"(kt0[1][2]), "v"(kt0[1][3]));
+    asm volatile("" ::"v"(vt0[0]), "v"(vt0[1]), "v"(vt0[2]), "v"(vt0[3]),
+                 "v"(vt0[4]), "v"(vt0[5]), "v"(vt0[6]), "v"(vt0[7]));
+  }
+  const int len = static_cast<int>(
+      min(max(len_word, int64_t{1}), static_cast<int64_t>(a.len)));
   const int end = min(begin + a.span, len);
   if constexpr (AT) {
     if (begin >= len) {
@@ -120,9 +160,6 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
   __shared__ float s_ml[WAVES][G][2];
   __shared__ float s_acc[WAVES][G][D];
 
-  const uint16_t *kb = a.k + g * a.head_stride;
-  const uint16_t *vb = a.v + g * a.head_stride;
-  const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
   const int last = end - 1;
   const uint32_t head_mask = c16 < G ? 0xffffffffu : 0u;  // zero P columns
 
@@ -130,23 +167,6 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
   f32x4 o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // K rows of the block as two MFMA halves, V rows as 8 whole rows per lane
-  auto load_block = [&](int r0, u32x4 (&kt)[2][4], u32x4 (&vt)[8]) {
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int row = min(r0 + krow + 4 * hf, last);
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        kt[hf][c] = kv_load<NT>(kb + static_cast<int64_t>(row) * D + 32 * c +
-                                8 * g4);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = min(r0 + 8 * g4 + j, last);
-      vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
-    }
-  };
 
   auto block_step = [&](int r0, const u32x4 (&kt)[2][4], const u32x4 (&vt)[8]) {
     f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
@@ -188,10 +208,20 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
       o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
   };
 
-  for (int r0 = begin + wave * kAttnBlock; r0 < end; r0 += kPassRows) {
+  int r0 = begin + wave * kAttnBlock;
+  if constexpr (AT) {
+    if (r0 < end) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (r0 + 8 * g4 + j >= end) vt0[j] = u32x4{0u, 0u, 0u, 0u};
+      block_step(r0, kt0, vt0);
+    }
+    r0 += kPassRows;
+  }
+  for (; r0 < end; r0 += kPassRows) {
     u32x4 kt[2][4];
     u32x4 vt[8];
-    load_block(r0, kt, vt);
+    load_block(r0, last, kt, vt);
     block_step(r0, kt, vt);
   }
 
