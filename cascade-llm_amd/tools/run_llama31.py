@@ -7,6 +7,12 @@ Same flags and JSON result as the reference CLI (tools/run_llama31.py:27-154):
 (there is none on the GPU hosts) use --random-init: seeded synthetic weights
 (--seed), prompt ids from --prompt-ids, optionally fewer decoder layers
 (--layers) for quick runs.
+
+--decode-graph (not in the reference) keeps every weight resident in HBM
+and, after the prefill, decodes by replaying one captured HIP graph per
+token (layer_streaming.DecodeGraph; needs --vocab-mode resident).  Its
+decode_token_latencies_ms lists the replays; the first decode step runs
+eagerly while the graph is captured (decode_graph_setup_ms).
 """
 
 import argparse
@@ -22,10 +28,12 @@ if str(PACKAGE_ROOT) not in sys.path:
     sys.path.insert(0, str(PACKAGE_ROOT))
 
 from layer_streaming import (  # noqa: E402
+    DecodeGraph,
     DoubleBufferRuntime,
     Llama31Config,
     Llama31DecodeExecutor,
     ResidentDeviceArena,
+    ResidentTransformerRuntime,
     VocabStreamingRuntime,
     build_llama31_8b_plan,
     create_weight_store,
@@ -52,9 +60,15 @@ def parse_args(argv=None):
     parser.add_argument("--layers", type=int, default=32)
     parser.add_argument("--prompt-ids", default="128000,791,7438,315,2324,374",
                         help="comma-separated prompt ids for --random-init")
+    parser.add_argument("--decode-graph", action="store_true",
+                        help="weights resident in HBM; decode by replaying one "
+                             "captured HIP graph per token (needs --vocab-mode "
+                             "resident)")
     args = parser.parse_args(argv)
     if args.checkpoint is None and not args.random_init:
         parser.error("either --checkpoint or --random-init is required")
+    if args.decode_graph and args.vocab_mode != "resident":
+        parser.error("--decode-graph needs --vocab-mode resident")
     return args
 
 
@@ -90,7 +104,11 @@ def main(argv=None):
     device = torch.device(args.device)
     torch.cuda.set_device(device)
     resident = ResidentDeviceArena(plan, store, device)
-    runtime = DoubleBufferRuntime(plan, store, resident, device)
+    if args.decode_graph:
+        runtime = ResidentTransformerRuntime(plan, store, resident, device,
+                                             synchronize=False)
+    else:
+        runtime = DoubleBufferRuntime(plan, store, resident, device)
     vocab_runtime = None
     if plan.vocab is not None:
         vocab_runtime = VocabStreamingRuntime(plan, store, runtime)
@@ -105,13 +123,29 @@ def main(argv=None):
 
     generated = []
     token_latencies = []
+    graph_setup_ms = None
     with torch.inference_mode():
         state = executor.begin(input_ids)
         state = runtime.run(executor, state)
         state = executor.finish(state)
         next_token = state.topk_indices[..., 0]
         generated.append(next_token)
-        for _ in range(args.max_new_tokens - 1):
+        eager_steps = args.max_new_tokens - 1
+        if args.decode_graph and args.max_new_tokens >= 3:
+            started = time.perf_counter()
+            graph = DecodeGraph(executor, runtime, next_token, args.max_new_tokens - 1)
+            torch.cuda.synchronize(device)
+            graph_setup_ms = (time.perf_counter() - started) * 1000.0
+            for _ in range(args.max_new_tokens - 2):
+                started = time.perf_counter()
+                graph.step()
+                torch.cuda.synchronize(device)
+                token_latencies.append((time.perf_counter() - started) * 1000.0)
+            graph.check()
+            generated.append(graph.tokens())
+            graph.close()
+            eager_steps = 0
+        for _ in range(eager_steps):
             started = time.perf_counter()
             state = executor.begin(next_token)
             state = runtime.run(executor, state)
@@ -138,6 +172,7 @@ def main(argv=None):
         "generated_text": text,
         "checkpoint_load_seconds": load_seconds,
         "decode_token_latencies_ms": token_latencies,
+        "decode_graph_setup_ms": graph_setup_ms,
         "runtime": runtime.stats.as_dict(),
         "cpu_pinned_bytes": store.pinned_cpu_bytes,
         "vocab_extra_pinned_cpu_bytes": (

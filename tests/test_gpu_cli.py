@@ -50,3 +50,18 @@ def test_cli_tokens_agree_across_modes(gpu_device, tmp_path):
           flush=True)
     assert a["generated_ids"] == b["generated_ids"] == c["generated_ids"]
     assert b["cpu_pinned_bytes"] < a["cpu_pinned_bytes"]  # staging pins 2 slots only
+
+
+def test_cli_decode_graph_equals_eager(gpu_device, tmp_path):
+    # weights resident, decode as graph replays: the same kernels at the same
+    # split plan as the eager resident-vocabulary run, so the same tokens
+    eager = run_cli(tmp_path, "--granularity", "matrix_group", "--vocab-mode",
+                    "resident", "--max-new-tokens", "5")
+    graph = run_cli(tmp_path, "--granularity", "matrix_group", "--vocab-mode",
+                    "resident", "--max-new-tokens", "5", "--decode-graph")
+    print("eager", eager["generated_ids"], "graph", graph["generated_ids"],
+          flush=True)
+    assert graph["generated_ids"] == eager["generated_ids"]
+    assert len(graph["generated_ids"]) == 5
+    assert len(graph["decode_token_latencies_ms"]) == 3
+    assert graph["decode_graph_setup_ms"] > 0
