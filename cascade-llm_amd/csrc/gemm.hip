@@ -456,22 +456,30 @@ __device__ __forceinline__ u32x4 gemm_rsrc_words(const uint16_t *base, int64_t b
 // voffset land at LDS byte (lds + 16 l).  The compiler does not see these
 // loads, so it adds no vmcnt waits of its own for them (the caller waits);
 // the memory clobber keeps LDS accesses from moving across the issue.
+// The descriptor words pass through readfirstlane (a no-op on values the
+// compiler already keeps in SGPRs): where it cannot prove a selected
+// descriptor uniform it would otherwise hand the asm VGPRs.
 __device__ __forceinline__ void dma_lds16(const u32x4 &rsrc, int voff, const uint16_t *lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)lds)));
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(rsrc.x);
+  r.y = __builtin_amdgcn_readfirstlane(rsrc.y);
+  r.z = __builtin_amdgcn_readfirstlane(rsrc.z);
+  r.w = __builtin_amdgcn_readfirstlane(rsrc.w);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(m0), "v"(voff), "s"(rsrc) : "memory", "m0");
+               :: "s"(m0), "v"(voff), "s"(r) : "memory", "m0");
 }
 
 // STAGES = 2: two slab buffers, the slab loads through the LDS-DMA builtin
-// (the compiler waits for them exactly).  STAGES = 3: a ring of three slab
-// buffers with two slabs in flight; the loads go through dma_lds16 and each
-// slab step waits for exactly its own slab (vmcnt = the next slab's loads),
-// since with more than two buffers the compiler would wait for every load
-// in flight at each barrier.
+// (the compiler waits for them exactly).  STAGES = 3 or 4: a ring of slab
+// buffers with STAGES - 1 slabs in flight; the loads go through dma_lds16
+// and each slab step waits for exactly its own slab (vmcnt = the later
+// slabs' loads), since with more than two buffers the compiler would wait
+// for every load in flight at each barrier.
 template <int EPI, class T, int STAGES = 2, int BK = kTileK>
 __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
-  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 slab buffers");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 slab buffers");
   using L = DmaSlab<BK>;
   constexpr int XI = T::BM * L::ROWB / 1024;  // load instructions per X slab
   constexpr int WI = kTileN * L::ROWB / 1024;
@@ -479,13 +487,13 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
   static_assert(XI % T::WAVES == 0 && WI % T::WAVES == 0, "whole loads per wave");
   constexpr int XB = T::BM * BK, WB = kTileN * BK;  // bf16 per slab buffer
   // STAGES = 2: one array per slab buffer (X slab, then W slab); sb0 also
-  // holds the staged output tile of the vectorised epilogue.  STAGES = 3:
+  // holds the staged output tile of the vectorised epilogue.  STAGES >= 3:
   // sb0 holds the ring (slab buffer k at sb0 + k (XB + WB)) and, after the
   // loop, the staged tile.
   constexpr int kStage = kTileN * T::STAGE_COL;
   constexpr int kSlab = XB + WB;
-  constexpr int kSb0 = (STAGES == 2 ? kSlab : 3 * kSlab) > kStage
-                           ? (STAGES == 2 ? kSlab : 3 * kSlab) : kStage;
+  constexpr int kRing = (STAGES == 2 ? 1 : STAGES) * kSlab;
+  constexpr int kSb0 = kRing > kStage ? kRing : kStage;
   __shared__ __attribute__((aligned(16))) uint16_t sb0[kSb0];
   __shared__ __attribute__((aligned(16))) uint16_t sb1[STAGES == 2 ? kSlab : 8];
   int tm, tn;
@@ -596,7 +604,7 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
   const int slabs = static_cast<int>(a.k / BK);
   // s_waitcnt vmcnt(0), expcnt / lgkmcnt left alone
   constexpr int kWaitLoads = (7 << 4) | (15 << 8);
-  if constexpr (STAGES == 3) {
+  if constexpr (STAGES >= 3) {
     const u32x4 xw = gemm_rsrc_words(a.x, a.m * k_bytes);
     const u32x4 ww0 = gemm_rsrc_words(wbase0, wrows0 * k_bytes);
     const u32x4 ww1 = gemm_rsrc_words(wbase1, wrows1 * k_bytes);
@@ -621,47 +629,50 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
                   dw + i * 512);
       }
     };
-    // wait for this wave's loads of the slab about to be computed (the next
-    // slab's D loads may stay in flight), then the barrier publishes it to
-    // the workgroup and frees the buffer read one step earlier
+    // wait for this wave's loads of the slab about to be computed (the
+    // STAGES - 2 later slabs, D loads each, may stay in flight), then the
+    // barrier publishes it to the workgroup and frees the buffer read one
+    // step earlier
     // (lgkmcnt(0) too: this wave's LDS reads of the buffer about to be
     // refilled have completed before the barrier lets a refill start)
     constexpr int D = XW + WW;
-    constexpr int kWaitOne = (D & 15) | ((D >> 4) << 14) | (7 << 4);
+    constexpr int kAhead = (STAGES - 2) * D;
+    static_assert(kAhead < 64, "vmcnt holds 6 bits");
+    constexpr int kWaitOne = (kAhead & 15) | ((kAhead >> 4) << 14) | (7 << 4);
     auto publish1 = [&]() {
       __builtin_amdgcn_s_waitcnt(kWaitOne);
       __builtin_amdgcn_s_barrier();
     };
-    uint16_t *b0 = sb0, *b1 = sb0 + kSlab, *b2 = sb0 + 2 * kSlab;
-    // loads past the last slab reload it into the free buffer (never read):
-    // every step then has the same loads in flight
-    ring_load(0, b0);
-    ring_load(min(1, slabs - 1), b1);
+    // slab j lives in buffer j % STAGES; the loops are unrolled by STAGES so
+    // that every buffer is a constant offset.  Loads past the last slab
+    // reload it into the free buffer (never read), so every step that a
+    // later step's wait counts on has the same loads in flight.  Only a
+    // remainder step that is the last one skips its loads (the main loop
+    // stays free of branches).
+#pragma unroll
+    for (int p = 0; p < STAGES - 1; ++p)
+      ring_load(min(p, slabs - 1), sb0 + p * kSlab);
     int s = 0;
-    for (; s + 3 <= slabs; s += 3) {
-      publish1();
-      ring_load(min(s + 2, slabs - 1), b2);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(b0, b0 + XB);
-      publish1();
-      ring_load(min(s + 3, slabs - 1), b0);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(b1, b1 + XB);
-      publish1();
-      ring_load(min(s + 4, slabs - 1), b1);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(b2, b2 + XB);
+    for (; s + STAGES <= slabs; s += STAGES) {
+#pragma unroll
+      for (int i = 0; i < STAGES; ++i) {
+        publish1();
+        ring_load(min(s + i + STAGES - 1, slabs - 1),
+                  sb0 + ((i + STAGES - 1) % STAGES) * kSlab);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(sb0 + i * kSlab, sb0 + i * kSlab + XB);
+      }
     }
-    if (s < slabs) {
-      publish1();
-      ring_load(min(s + 2, slabs - 1), b2);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(b0, b0 + XB);
-      ++s;
-    }
-    if (s < slabs) {
-      publish1();
-      compute(b1, b1 + XB);
+#pragma unroll
+    for (int i = 0; i < STAGES - 1; ++i) {
+      if (s + i < slabs) {
+        publish1();
+        if (s + i + 1 < slabs)
+          ring_load(min(s + i + STAGES - 1, slabs - 1),
+                    sb0 + ((i + STAGES - 1) % STAGES) * kSlab);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(sb0 + i * kSlab, sb0 + i * kSlab + XB);
+      }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLoads);
     if (EPI != kGemmF32 && a.vec_out) {
@@ -741,7 +752,7 @@ static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
   if (a.m > 128 && tiles256 >= 256) return launch_tiles<EPI, GemmTile256, 3>(a, tiles_n, s);
   const int64_t tiles128 = (a.m + 127) / 128 * tiles_n;
-  if (a.m <= 64 || tiles128 < 256) return launch_tiles<EPI, GemmTile64>(a, tiles_n, s);
+  if (a.m <= 64 || tiles128 < 256) return launch_tiles<EPI, GemmTile64, 4>(a, tiles_n, s);
   return launch_tiles<EPI, GemmTile128>(a, tiles_n, s);
 }
 
