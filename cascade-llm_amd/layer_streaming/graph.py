@@ -52,6 +52,10 @@ class DeviceStep:
         self.indices = torch.zeros((1, 1, top_k), dtype=torch.int64,
                                    device=device)
         self.ids = self.indices.view(1, -1)[:, :1]
+        # True only while the owning DecodeGraph runs or captures a step:
+        # the executor refuses other calls meanwhile (they would advance
+        # the device length behind the graph's back)
+        self.active = False
 
 
 class DecodeGraph:
@@ -125,9 +129,13 @@ class DecodeGraph:
 
     def _run_step(self):
         ex = self.executor
-        state = ex.begin(self.step_buffers.ids)
-        state = self.runtime.run(ex, state)
-        ex.finish(state)
+        self.step_buffers.active = True
+        try:
+            state = ex.begin(self.step_buffers.ids)
+            state = self.runtime.run(ex, state)
+            ex.finish(state)
+        finally:
+            self.step_buffers.active = False
 
     def _set_host_length(self):
         cache = self.executor.kv_cache

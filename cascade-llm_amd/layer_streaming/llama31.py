@@ -353,6 +353,9 @@ class Llama31DecodeExecutor:
     # --------------------------------------------------------------- API
 
     def begin(self, input_ids, position_ids=None):
+        if self._device_step is not None and not self._device_step.active:
+            raise RuntimeError("the executor belongs to an open DecodeGraph "
+                               "(decode with DecodeGraph.step, or close it)")
         if input_ids.ndim != 2 or input_ids.shape[0] != 1:
             raise ValueError("first runtime supports one unpadded request")
         past = self.kv_cache.sequence_length()

@@ -436,6 +436,9 @@ def test_device_step_decode_matches_oracle(monkeypatch, weights, exact_oracle):
     token = int(ei[0])
     step.indices.view(-1)[0] = token
     executor._device_step = step
+    with pytest.raises(RuntimeError):  # only the owning DecodeGraph may step
+        executor.begin(step.ids)
+    step.active = True
     fakes.calls.clear()
     for i in range(3):
         expected_logits, _, ei = oracle.step([token], 5)

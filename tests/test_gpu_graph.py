@@ -233,6 +233,8 @@ def test_decode_graph_replays_equal_eager_steps(gpu_device, model, past, max_new
         assert hist[past] == 4242
         assert hist[past + 1:past + steps].tolist() == tokens[:-1]
         assert ex.kv_cache.sequence_length() == past + steps
+        with pytest.raises(RuntimeError):  # the executor belongs to the graph
+            ex.begin(first)
         if max_new == steps:
             with pytest.raises(RuntimeError):
                 graph.step()
