@@ -43,9 +43,14 @@ def linear_bound_report(actual, x, w):
 @pytest.mark.parametrize("m,n,k", [
     (2048, 4096, 4096), (6, 6144, 4096), (130, 1024, 4096), (2, 128, 64),
     (257, 4096, 14336), (1, 256, 4096), (300, 28672, 4096),
-    (5, 1000, 4096), (129, 200, 128), (7, 1001, 128)])
+    (5, 1000, 4096), (129, 200, 128), (7, 1001, 128),
+    (2048, 4096, 192), (2048, 4096, 320), (2048, 1024, 384),
+    (2048, 1024, 448), (40, 512, 1088)])
 def test_gemm_matches_oracle(gpu_device, m, n, k):
-    # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs
+    # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs.
+    # Slab rings (K / 64 slabs): 256-row tiles (3 slabs) at 3 and 5 slabs
+    # (no remainder, remainder 2); 64-row tiles (4 slabs) at 6, 7 and 17
+    # slabs (main loop plus a remainder of 2, 3 and 1), besides 1, 2, 64, 224
     print("gemm m={} n={} k={}".format(m, n, k), flush=True)
     dev = gpu_device
     x = cases.normal_bf16((m, k), 101)
