@@ -7,6 +7,8 @@
 //     async (hipMemcpyAsync on a stream) vs sync (hipMemcpy);
 //   * sizes from 4 KiB to --max-mib, plus the transfer units of the 8B plan
 //     (48 / 32 / 224 / 112 MiB matrix groups, 128 MiB vocab chunk);
+//   * pinned async copies also split over 2 and 4 streams (several DMA
+//     engines at once);
 //   * per size: --repeats event-timed copies after one warm-up,
 //     p10 / median / p90 GB/s (1 GB = 1e9 bytes);
 //   * host enqueue cost: least-squares slope of host time over batches of
@@ -76,6 +78,45 @@ std::vector<double> time_copies(void *dst, void *src, size_t bytes, bool async,
     }
     if (r >= 0) out.push_back(bytes / 1e9 / (ms / 1e3));
   }
+  CHECK(hipEventDestroy(a));
+  CHECK(hipEventDestroy(b));
+  return out;
+}
+
+// GB/s samples of `repeats` copies of `bytes`, each split into equal
+// pieces on the `streams` given (one piece per stream; pieces 4 KiB
+// aligned): stream 0 records the start, the others wait for it, and stream
+// 0 waits for every piece before recording the end.
+std::vector<double> time_split_copies(char *dst, const char *src, size_t bytes,
+                                      int repeats,
+                                      const std::vector<hipStream_t> &streams) {
+  const size_t n = streams.size();
+  hipEvent_t a, b;
+  CHECK(hipEventCreate(&a));
+  CHECK(hipEventCreate(&b));
+  std::vector<hipEvent_t> done(n);
+  for (auto &e : done) CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  const size_t piece = (bytes / n + 4095) / 4096 * 4096;
+  std::vector<double> out;
+  for (int r = -1; r < repeats; ++r) {
+    CHECK(hipEventRecord(a, streams[0]));
+    for (size_t i = 0; i < n; ++i) {
+      const size_t off = std::min(bytes, i * piece);
+      const size_t len = std::min(bytes - off, piece);
+      if (i) CHECK(hipStreamWaitEvent(streams[i], a, 0));
+      if (len)
+        CHECK(hipMemcpyAsync(dst + off, src + off, len, hipMemcpyHostToDevice,
+                             streams[i]));
+      CHECK(hipEventRecord(done[i], streams[i]));
+    }
+    for (size_t i = 1; i < n; ++i) CHECK(hipStreamWaitEvent(streams[0], done[i], 0));
+    CHECK(hipEventRecord(b, streams[0]));
+    CHECK(hipEventSynchronize(b));
+    float ms = 0.0f;
+    CHECK(hipEventElapsedTime(&ms, a, b));
+    if (r >= 0) out.push_back(bytes / 1e9 / (ms / 1e3));
+  }
+  for (auto &e : done) CHECK(hipEventDestroy(e));
   CHECK(hipEventDestroy(a));
   CHECK(hipEventDestroy(b));
   return out;
@@ -167,6 +208,29 @@ int main(int argc, char **argv) {
                    bytes, s.median);
     }
   }
+  // The same pinned copies split over 2 and 4 streams (several DMA engines
+  // at once), sizes of 1 MiB and up.
+  std::vector<hipStream_t> extra(4);
+  extra[0] = stream;
+  for (int i = 1; i < 4; ++i) CHECK(hipStreamCreate(&extra[i]));
+  for (int n : {2, 4}) {
+    std::vector<hipStream_t> use(extra.begin(), extra.begin() + n);
+    for (size_t bytes : sizes) {
+      if (bytes < mib) continue;
+      const Stats s = percentiles(time_split_copies(
+          static_cast<char *>(dev), static_cast<const char *>(pinned), bytes,
+          repeats, use));
+      char buf[256];
+      std::snprintf(buf, sizeof buf,
+                    ", {\"mode\": \"pinned_async_%d_streams\", \"bytes\": %zu, "
+                    "\"gbps_p10\": %.3f, \"gbps_median\": %.3f, \"gbps_p90\": %.3f}",
+                    n, bytes, s.p10, s.median, s.p90);
+      json += buf;
+      std::fprintf(stderr, "h2d_bench: pinned_async_%d_streams %zu B median %.2f GB/s\n",
+                   n, bytes, s.median);
+    }
+  }
+  for (int i = 1; i < 4; ++i) CHECK(hipStreamDestroy(extra[i]));
   json += "]";
 
   // Host enqueue cost of async copies (4 KiB each).
