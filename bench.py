@@ -20,13 +20,16 @@ Also reported (extra keys, not ``value``):
     on the device; layer_streaming.DecodeGraph; skip: --no-decode-graph);
   * streamed: BASELINE config 3 -- full_pinned 16 GB host arena,
     matrix_group units through two 224 MiB slots, streamed vocabulary;
-    decode ms/token and the PCIe-inclusive H2D GB/s (skip: --no-streamed);
+    decode ms/token and the PCIe-inclusive H2D GB/s, timed without copy /
+    unit events, which two further decodes carry for the per-copy rates
+    (skip: --no-streamed);
   * prefill: BASELINE config 5 -- a 2048-token random-ID prompt through the
     pinned_staging store with matrix granularity and the streamed
     vocabulary (pageable arena -> pinned staging slots -> two 128 MiB device
-    slots), prefill ms and H2D GB/s, and every prefill GEMM / attention
-    launch of the timed run bound to HIP events: per-matrix TFLOP/s and the
-    fraction of the bf16 dense MFMA peak (skip: --no-prefill);
+    slots), prefill ms and H2D GB/s timed without events, then one
+    profiled prefill whose every GEMM / attention launch is bound to HIP
+    events: per-matrix TFLOP/s and the fraction of the bf16 dense MFMA
+    peak (skip: --no-prefill);
   * cpu_baseline: the CPU oracle on this host's cores on a bounded sample
     (skip: --no-cpu-baseline).
 
@@ -294,18 +297,23 @@ def streamed_decode(args):
     store.fill_random(seed=args.seed, device=dev)
     setup_s = time.perf_counter() - t0
     resident = ResidentDeviceArena(plan, store, dev)
-    runtime = DoubleBufferRuntime(plan, store, resident, dev, profile=True)
-    vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
+    runtime = DoubleBufferRuntime(plan, store, resident, dev)
+    vocab = VocabStreamingRuntime(plan, store, runtime)
     executor = Llama31DecodeExecutor(Llama31Config(), resident, vocab_runtime=vocab,
                                      top_k=10)
     prompt = torch.tensor([[128000, 791, 7438, 315, 2324, 374]], device=dev)
-    walls, h2d, lm = [], [], []
+    walls, h2d, lm, profiled = [], [], [], []
     with torch.inference_mode():
         t0 = time.perf_counter()
         state = executor.finish(runtime.run(executor, executor.begin(prompt)))
         prefill_ms = (time.perf_counter() - t0) * 1000.0
         token = state.topk_indices[..., 0]
-        for step in range(1 + args.streamed_steps):
+        # warm-up, timed decodes without timing events, then two decodes
+        # with per-copy / per-unit events for the H2D and compute figures
+        # (the events cost about 1% of the token)
+        timed = args.streamed_steps
+        for step in range(1 + timed + 2):
+            runtime.profile = vocab.profile = step > timed
             t0 = time.perf_counter()
             state = executor.begin(token)
             state = runtime.run(executor, state)
@@ -315,15 +323,20 @@ def streamed_decode(args):
             wall = (time.perf_counter() - t0) * 1000.0
             if step == 0:
                 continue  # warm-up decode, as the reference's protocol
-            walls.append(wall)
-            h2d.append(runtime.last_profile)
-            lm.append(vocab.last_profile)
-            log("config 3: decode {} {:.1f} ms".format(step, wall))
+            log("config 3: decode {} {:.1f} ms{}".format(
+                step, wall, " (profiled)" if step > timed else ""))
+            if step > timed:
+                profiled.append(wall)
+                h2d.append(runtime.last_profile)
+                lm.append(vocab.last_profile)
+            else:
+                walls.append(wall)
     bytes_token = plan.stream_bytes_per_token + VOCAB * HIDDEN * 2 + HIDDEN * 2
     result = {
         "ms_per_token_median": statistics.median(walls),
         "ms_per_token_p10": sorted(walls)[max(0, int(0.1 * (len(walls) - 1)))],
         "ms_per_token_p90": sorted(walls)[int(0.9 * (len(walls) - 1))],
+        "profiled_ms_per_token": statistics.median(profiled),
         "prefill_6_tokens_ms": prefill_ms,
         "h2d_bytes_per_token": bytes_token,
         "pcie_inclusive_gbps": bytes_token / 1e9 / (statistics.median(walls) / 1e3),
@@ -379,8 +392,8 @@ def prefill_streamed(args):
     store = create_weight_store(plan, "pinned_staging")
     store.fill_random(seed=args.seed, device=dev)
     resident = ResidentDeviceArena(plan, store, dev)
-    runtime = DoubleBufferRuntime(plan, store, resident, dev, profile=True)
-    vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
+    runtime = DoubleBufferRuntime(plan, store, resident, dev)
+    vocab = VocabStreamingRuntime(plan, store, runtime)
     executor = Llama31DecodeExecutor(Llama31Config(), resident, vocab_runtime=vocab,
                                      top_k=10)
     executor.reserve(tokens + 1)
@@ -391,10 +404,15 @@ def prefill_streamed(args):
               "gemm_up": LAYERS, "gemm_down": LAYERS,
               "prefill_attention": LAYERS}
     repeats = args.prefill_repeats
+    profiled = None
     with torch.inference_mode():
-        for rep in range(1 + repeats):
+        # warm-up, timed prefills without timing events, then one prefill
+        # with copy / unit events and every GEMM and attention launch timed
+        for rep in range(1 + repeats + 1):
             executor.kv_cache.clear()
-            if rep == repeats:
+            last = rep == repeats + 1
+            runtime.profile = vocab.profile = last
+            if last:
                 for name, count in groups.items():
                     executor.instrument(name, count)
             torch.cuda.synchronize(dev)
@@ -402,11 +420,15 @@ def prefill_streamed(args):
             state = executor.finish(runtime.run(executor, executor.begin(prompt)))
             torch.cuda.synchronize(dev)
             wall = (time.perf_counter() - t0) * 1000.0
-            log("config 5: prefill {} {:.1f} ms".format(rep, wall))
+            log("config 5: prefill {} {:.1f} ms{}".format(
+                rep, wall, " (profiled)" if last else ""))
             if rep == 0:
                 continue  # warm-up
-            walls.append(wall)
-            profiles.append(runtime.last_profile)
+            if last:
+                profiled = wall
+                profiles.append(runtime.last_profile)
+            else:
+                walls.append(wall)
     times = {name: executor.kernel_times_ms(name) for name in groups}
     gemms = {}
     total_ms = 0.0
@@ -429,8 +451,10 @@ def prefill_streamed(args):
         "workload": "BASELINE config 5: {}-token random-ID prompt, pinned_staging "
                     "(pageable arena + pinned staging slots), matrix granularity, "
                     "2 x {} MiB device slots, streamed vocab; 1 warm-up + {} "
-                    "prefills".format(tokens, plan.slot_bytes >> 20, repeats),
+                    "timed prefills + 1 profiled prefill (copy / kernel "
+                    "events)".format(tokens, plan.slot_bytes >> 20, repeats),
         "prefill_ms_median": round(median, 2),
+        "profiled_prefill_ms": round(profiled, 2),
         "prefill_ms_min": round(min(walls), 2),
         "prompt_tokens_per_s": round(tokens / (median / 1e3), 1),
         "h2d_bytes": bytes_prefill,
@@ -598,7 +622,8 @@ def main():
         line["streamed"] = {
             "workload": "BASELINE config 3: full_pinned, matrix_group, 2 x 224 MiB "
                         "slots, streamed vocab, 6-token prompt, 1 warm-up + {} "
-                        "decodes".format(args.streamed_steps),
+                        "timed decodes + 2 profiled decodes (copy / unit "
+                        "events)".format(args.streamed_steps),
             **{k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()},
             "pcie_peak_gbps": PCIE_PEAK_GBPS,
         }
