@@ -163,6 +163,9 @@ class DoubleBufferRuntime:
         ]
         self.copy_stream = torch.cuda.Stream(device=self.device)
         self.compute_stream = torch.cuda.Stream(device=self.device)
+        # pinned_staging: units staged ahead of the one being copied (ring
+        # room permitting)
+        self.stage_lookahead = 8
         self.coordinator = torch.cuda.current_stream(self.device)
         count = len(plan.units)
         # Events are created once and re-recorded every token (each run()
@@ -221,8 +224,32 @@ class DoubleBufferRuntime:
             timing["pipeline"][0].record(self.coordinator)
 
         self.store.reset_profile()
-        staged = {i: self.store.prepare_unit(units[i], i) for i in range(min(slots, len(units)))}
         staging = self.store.mode.value == "pinned_staging"
+        ring = getattr(self.store, "staging_ring", None) if staging else None
+        staged = {}
+        next_stage = 0
+        if ring is None:
+            staged = {i: self.store.prepare_unit(units[i], i)
+                      for i in range(min(slots, len(units)))}
+        else:
+            # The previous run ended with every copy done; the ring starts
+            # empty.  (The copy stream is idle then, so this costs nothing.)
+            copy_stream.synchronize()
+            ring.reset()
+
+        def stage_ahead(done):
+            # ring staging: units after ``done`` (whose copy is enqueued)
+            # go to the staging workers while the ring has room for them
+            nonlocal next_stage
+            while next_stage < len(units) and next_stage - done <= self.stage_lookahead:
+                placed = ring.place(units[next_stage].nbytes, next_stage)
+                if placed is None:
+                    break
+                staged[next_stage] = self.store.stage_in_ring(units[next_stage], *placed)
+                next_stage += 1
+
+        if ring is not None:
+            stage_ahead(-1)
 
         source_wait_ms = 0.0
         submit_started = time.perf_counter()
@@ -243,7 +270,10 @@ class DoubleBufferRuntime:
             self._ready[index].record(copy_stream)
 
             ahead = index + slots
-            if ahead < len(units):
+            if ring is not None:
+                ring.copied(index, self._ready[index])
+                stage_ahead(index)
+            elif ahead < len(units):
                 # The staging worker may overwrite host slot `slot_index` as
                 # soon as this H2D copy has completed; it need not wait for
                 # the compute, which reads the device slot.

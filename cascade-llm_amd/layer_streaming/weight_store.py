@@ -10,6 +10,10 @@ API and behaviour follow the reference (layer_streaming/weight_store.py):
   unit in (:209-298) with the library's multi-threaded non-temporal memcpy
   (``cascade_host_copy``; ``copy_threads`` threads, default this process's
   CPUs up to 16) instead of one tensor copy.
+* Staging ring (added): the runtime stages units at consecutive byte ranges
+  of the same pinned slots, so several small units can be staged ahead of
+  their copies (``StagingRing``); ``prepare_unit`` keeps the reference's
+  one-unit-per-slot behaviour.
 * ``load_checkpoint`` fills the arena from a local safetensors file or
   sharded index with key and shape checks (:20-38, :109-171).
 * ``tensor_factory`` is injectable for tests (:55).
@@ -266,12 +270,76 @@ class FullPinnedWeightStore(BaseWeightStore):
         return future
 
 
+class StagingRing:
+    """Byte ring over the pinned staging slots.
+
+    The reference stages unit i into slot i % 2 once the copy that last read
+    that slot is done (weight_store.py:209-298, runtime.py:194-230).  After
+    a short copy (an 8 MiB k_proj) the next slot frees too late to stage the
+    following unit before the link runs dry.  Here units take consecutive
+    byte ranges of the slots, in order, a unit moving on to the next slot
+    (after the last, the first) when it does not fit in what is left of the
+    current one.  A range is placed once every unit still holding part of
+    it has had its copy enqueued, and the staging worker waits for those
+    copies' events before writing.  Several small units are then staged
+    ahead within the same pinned slots; units as large as a slot alternate
+    between them as before.  Used from the runtime's host thread only.
+    """
+
+    def __init__(self, slots):
+        self.slots = slots
+        self.slot_bytes = slots[0].numel() * slots[0].element_size()
+        self.reset()
+
+    def reset(self):
+        """Forget every placement (all copies reading the slots are done)."""
+
+        self.slot = 0
+        self.head = 0
+        self.live = []  # [slot, start, end, unit key, ready event or None]
+
+    def place(self, nbytes, key):
+        """(slot, byte start, events to wait for) for ``nbytes``, or None
+        while a unit whose copy is not yet enqueued holds part of the range."""
+
+        if nbytes > self.slot_bytes:
+            raise ValueError("unit larger than a staging slot")
+        slot, start = self.slot, self.head
+        if start + nbytes > self.slot_bytes:
+            slot, start = (slot + 1) % len(self.slots), 0
+        end = start + nbytes
+        waits, keep = [], []
+        for entry in self.live:
+            if entry[0] == slot and entry[1] < end and start < entry[2]:
+                if entry[4] is None:
+                    return None
+                waits.append(entry[4])
+                if start <= entry[1] and entry[2] <= end:
+                    continue  # wholly covered: the new unit owns its bytes
+            # kept, partial overlaps included: the rest of their range may
+            # be written by a later unit, which must wait for them too
+            keep.append(entry)
+        self.live = keep + [[slot, start, end, key, None]]
+        self.slot, self.head = slot, end
+        return slot, start, waits
+
+    def copied(self, key, event):
+        """The copy of unit ``key`` is enqueued; ``event`` marks its end."""
+
+        for entry in self.live:
+            if entry[3] == key:
+                entry[4] = event
+                return
+        raise KeyError(key)
+
+
 class PinnedStagingWeightStore(BaseWeightStore):
     """Pageable full store plus reusable page-locked staging slots."""
 
     def __init__(self, plan, allocate=True, tensor_factory=None, worker_count=2,
                  copy_threads=None):
         self.staging_slots = None
+        self.staging_ring = None
         self.worker_count = int(worker_count)
         self.copy_threads = int(copy_threads or _hip.default_copy_threads())
         self._executor = None
@@ -300,6 +368,7 @@ class PinnedStagingWeightStore(BaseWeightStore):
                 )
                 for _ in range(self.plan.slot_count)
             ]
+            self.staging_ring = StagingRing(self.staging_slots)
         if self._executor is None:
             self._executor = ThreadPoolExecutor(
                 max_workers=self.worker_count, thread_name_prefix="weight-stage"
@@ -322,6 +391,28 @@ class PinnedStagingWeightStore(BaseWeightStore):
         if self.staging_slots is None or self._executor is None:
             raise RuntimeError("staging store has not been allocated")
         return self._executor.submit(self._stage, unit, slot_index, reuse_event)
+
+    def _stage_at(self, unit, slot_index, start, waits):
+        started = time.perf_counter()
+        for event in waits:
+            event.synchronize()
+        slot = self.staging_slots[slot_index]
+        first = start // slot.element_size()
+        target = slot[first:first + unit.elements]
+        _hip.host_copy(target, self.unit_source(unit), self.copy_threads)
+        elapsed = (time.perf_counter() - started) * 1000.0
+        with self._profile_lock:
+            self._stage_durations_ms.append(elapsed)
+        return target
+
+    def stage_in_ring(self, unit, slot_index, start, waits):
+        """Stage ``unit`` at byte ``start`` of staging slot ``slot_index``
+        once ``waits`` (the copies that last read those bytes) are done;
+        returns a future of the pinned source view."""
+
+        if self._executor is None:
+            raise RuntimeError("staging store has not been allocated")
+        return self._executor.submit(self._stage_at, unit, slot_index, start, waits)
 
     def close(self):
         if self._executor is not None:

@@ -174,3 +174,49 @@ def test_fill_random_is_seeded_per_tensor():
     c = create_weight_store(plan, "full_pinned", tensor_factory=RecordingFactory())
     c.fill_random(seed=3)  # norms = 1
     assert c.tensor("resident.weight").tolist() == [1.0, 1.0]
+
+
+def test_staging_ring_packs_small_units_and_waits_for_copies():
+    # two 100-byte slots: units of 30, 30, 30 share slot 0; 60 moves on to
+    # slot 1; 50 wraps to slot 0 over the first two (their copies must be
+    # enqueued, and are waited for); a unit larger than a slot is refused
+    from layer_streaming.weight_store import StagingRing
+
+    ring = StagingRing([torch.empty(50, dtype=torch.bfloat16) for _ in range(2)])
+    assert ring.place(30, "a")[:2] == (0, 0)
+    assert ring.place(30, "b")[:2] == (0, 30)
+    assert ring.place(30, "c")[:2] == (0, 60)
+    assert ring.place(60, "d")[:2] == (1, 0)
+    assert ring.place(50, "e") is None  # a and b not copied yet
+    ev_a, ev_b = FakeEvent(), FakeEvent()
+    ring.copied("a", ev_a)
+    assert ring.place(50, "e") is None  # b still holds bytes 30-59
+    ring.copied("b", ev_b)
+    slot, start, waits = ring.place(50, "e")
+    assert (slot, start) == (0, 0) and waits == [ev_a, ev_b]
+    # a (0-29) is wholly covered by e (0-49) and drops out; b (30-59) is
+    # only partly covered and stays, as do c and d
+    assert [entry[3] for entry in ring.live] == ["b", "c", "d", "e"]
+    # the rest of b's bytes: a unit there waits for b's copy again
+    # (dropping b on the first overlap let such a unit overwrite bytes
+    # whose copy was still in flight)
+    slot, start, waits = ring.place(8, "f")
+    assert (slot, start) == (0, 50) and waits == [ev_b]
+    with pytest.raises(ValueError):
+        ring.place(101, "g")
+    ring.reset()
+    assert ring.place(10, "h")[:2] == (0, 0) and ring.live[0][3] == "h"
+
+
+def test_staging_in_ring_waits_then_copies():
+    plan = tiny_plan()
+    store = PinnedStagingWeightStore(plan, tensor_factory=RecordingFactory())
+    store.arena[:4] = torch.tensor([1.0, 2.0, 3.0, 4.0], dtype=torch.bfloat16)
+    log = []
+    slot_index, start, waits = store.staging_ring.place(plan.units[0].nbytes, 0)
+    staged = store.stage_in_ring(plan.units[0], slot_index, start,
+                                 [FakeEvent(log), FakeEvent(log)]).result()
+    assert log == ["wait", "wait"]
+    assert staged.float().tolist() == [1.0, 2.0, 3.0, 4.0]
+    assert staged.data_ptr() == store.staging_slots[slot_index].data_ptr()
+    store.close()
