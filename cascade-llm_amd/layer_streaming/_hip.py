@@ -847,13 +847,18 @@ def memcpy_h2d_async(dst, src, nbytes, stream):
 
 
 def default_copy_threads():
-    """Threads for host staging copies: this process's CPUs, at most 16."""
+    """Threads for host staging copies: this process's CPUs, at most 8.
+
+    Eight threads stage at about twice the link rate.  More slow the H2D
+    copies that read host memory at the same time: on MI355X, config 5
+    prefill took 286 ms with 16 threads, 277 ms with 6 to 10, and 281 ms
+    with 4."""
 
     try:
         cpus = len(os.sched_getaffinity(0))
     except AttributeError:  # not Linux
         cpus = os.cpu_count() or 1
-    return max(1, min(16, cpus))
+    return max(1, min(8, cpus))
 
 
 def host_copy(dst, src, threads=None):

@@ -9,7 +9,7 @@ API and behaviour follow the reference (layer_streaming/weight_store.py):
   ``reuse_event`` (the H2D copy that last read its slot) and then copies the
   unit in (:209-298) with the library's multi-threaded non-temporal memcpy
   (``cascade_host_copy``; ``copy_threads`` threads, default this process's
-  CPUs up to 16) instead of one tensor copy.
+  CPUs up to 8) instead of one tensor copy.
 * Staging ring (added): the runtime stages units at consecutive byte ranges
   of the same pinned slots, so several small units can be staged ahead of
   their copies (``StagingRing``); ``prepare_unit`` keeps the reference's
