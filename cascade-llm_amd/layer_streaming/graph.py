@@ -83,6 +83,10 @@ class DecodeGraph:
             raise ValueError("DecodeGraph needs layer_mode='stages'")
         if executor._device_step is not None:
             raise RuntimeError("the executor already runs a DecodeGraph")
+        if executor.capture is not None:
+            # its hidden-state clones would be captured and replayed into
+            # the graph's own memory pool
+            raise ValueError("DecodeGraph needs executor.capture = None")
         if int(max_new_tokens) < 2:
             raise ValueError("max_new_tokens must be at least 2")
         self.executor = executor
