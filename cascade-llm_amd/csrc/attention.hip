@@ -319,7 +319,9 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
   s_part[quarter][d] = r;
   __syncthreads();
   if (quarter == 0) {
-    r = s_part[0][d] + s_part[1][d] + s_part[2][d] + s_part[3][d];
+    r = s_part[0][d];
+#pragma unroll
+    for (int q = 1; q < kMergeQuarters; ++q) r += s_part[q][d];
     a.out[(static_cast<int64_t>(g) * G + h) * D + d] = f32_to_bf16(r / s_den);
   }
 }
