@@ -166,6 +166,7 @@ class DoubleBufferRuntime:
         # pinned_staging: units staged ahead of the one being copied (ring
         # room permitting)
         self.stage_lookahead = 8
+        self._staging_left = {}
         self.coordinator = torch.cuda.current_stream(self.device)
         count = len(plan.units)
         # Events are created once and re-recorded every token (each run()
@@ -232,8 +233,16 @@ class DoubleBufferRuntime:
             staged = {i: self.store.prepare_unit(units[i], i)
                       for i in range(min(slots, len(units)))}
         else:
-            # The previous run ended with every copy done; the ring starts
-            # empty.  (The copy stream is idle then, so this costs nothing.)
+            # The ring starts empty: every copy of the previous run is done
+            # (a normal run ends synchronised; the copy stream is then idle
+            # and this costs nothing), and so is every staging job it left
+            # behind if it ended in an exception.
+            for future in self._staging_left.values():
+                try:
+                    future.result()
+                except Exception:  # that run already raised
+                    pass
+            self._staging_left = {}
             copy_stream.synchronize()
             ring.reset()
 
@@ -249,6 +258,7 @@ class DoubleBufferRuntime:
                 next_stage += 1
 
         if ring is not None:
+            self._staging_left = staged  # drained by the next run if this one raises
             stage_ahead(-1)
 
         source_wait_ms = 0.0
