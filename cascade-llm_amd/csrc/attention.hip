@@ -28,7 +28,9 @@
 // fp32 values.  Rows past the end of the span are loaded from the span's last
 // row (always valid memory) and given a score of -inf.  K and V are read
 // once, with the nontemporal hint.
+#include <atomic>
 #include <cfloat>
+#include <mutex>
 
 #include "cascade_device.h"
 #include "cascade_internal.h"
@@ -666,7 +668,7 @@ static AttnShape attention_shape(int64_t len) {
   return s;
 }
 
-static size_t attention_workspace(int64_t nsplits, int64_t n_kv_heads) {
+constexpr size_t attention_workspace(int64_t nsplits, int64_t n_kv_heads) {
   const size_t per = static_cast<size_t>(n_kv_heads) * nsplits * kAttnG;
   return kAttnHeaderBytes + per * 2 * sizeof(float) +
          per * kAttnD * sizeof(float);
@@ -768,6 +770,80 @@ extern "C" int cascade_decode_attention_at_bf16(
   a.len_word = length;
   return launch_decode_attention<true>(a, n_kv_heads,
                                        static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------- no-allocation variant
+// The split partials of cascade_decode_attention_noalloc_bf16 live in this
+// file-scope device array (one copy per GPU, held until the process ends).
+// It covers up to kNoAllocMaxKvHeads KV heads at the largest split count.
+// In host code `scratch` names a host-side stand-in; its device address on
+// each GPU comes from hipGetSymbolAddress and is the only form host code
+// hands to a kernel.
+constexpr int64_t kNoAllocMaxKvHeads = CASCADE_DECODE_ATTENTION_NOALLOC_MAX_KV_HEADS;
+constexpr size_t kNoAllocScratchBytes =
+    attention_workspace(kAttnMaxSplits, kNoAllocMaxKvHeads);
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch[kMaxScratchDevices];
+std::mutex g_scratch_lock;
+
+// Device address of `scratch` on the device that owns `s`, looked up once
+// per device with that device current.
+int scratch_on_stream_device(hipStream_t s, void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (s != nullptr) {
+    hipDevice_t owner = 0;
+    e = hipStreamGetDevice(s, &owner);
+    if (e != hipSuccess) return e;
+    dev = static_cast<int>(owner);
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) return CASCADE_EINVAL;
+  void *p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p != nullptr) {
+    *out = p;
+    return 0;
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  p = g_scratch[dev].load(std::memory_order_relaxed);
+  if (p == nullptr) {
+    int current = 0;
+    e = hipGetDevice(&current);
+    if (e != hipSuccess) return e;
+    if (current != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (current != dev) {
+      const hipError_t back = hipSetDevice(current);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int cascade_decode_attention_noalloc_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, int64_t len, int64_t n_q_heads, int64_t n_kv_heads,
+    int64_t head_dim, float scale, void *out, void *stream) {
+  if (n_kv_heads > kNoAllocMaxKvHeads) return CASCADE_ESCRATCH;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void *ws = nullptr;
+  if (int e = scratch_on_stream_device(s, &ws)) return e;
+  AttnArgs a{};
+  if (int e = decode_attention_args(q, k_cache, v_cache, kv_head_stride, len,
+                                    n_q_heads, n_kv_heads, head_dim, scale,
+                                    out, ws, kNoAllocScratchBytes, a))
+    return e;
+  return launch_decode_attention<false>(a, n_kv_heads, s);
 }
 
 extern "C" int cascade_prefill_attention_bf16(

@@ -111,6 +111,9 @@ extern "C" const char *cascade_error_string(int code) {
       return "cascade: shape not supported by the kernels";
     case CASCADE_EWORKSPACE:
       return "cascade: workspace smaller than required";
+    case CASCADE_ESCRATCH:
+      return "cascade: shape needs more than the library's static scratch "
+             "(no-allocation entry point)";
     default:
       return hipGetErrorString(static_cast<hipError_t>(code));
   }

@@ -67,6 +67,8 @@ _SIGNATURES = {
         _INT,
         [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P],
     ),
+    "cascade_decode_attention_noalloc_bf16": (
+        _INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P]),
     "cascade_decode_layer_workspace_bytes": (_SZ, []),
     "cascade_decode_layer_bf16": (
         _INT,

@@ -39,6 +39,7 @@ extern "C" {
 #define CASCADE_EALIGN 1002     /* pointer or K not 16-byte / 8-element aligned */
 #define CASCADE_ESHAPE 1003     /* shape outside what the kernels support */
 #define CASCADE_EWORKSPACE 1004 /* workspace smaller than *_workspace_bytes() */
+#define CASCADE_ESCRATCH 1005   /* shape beyond the library's static scratch */
 
 int cascade_abi_version(void);
 const char *cascade_error_string(int code);
@@ -159,6 +160,28 @@ int cascade_decode_attention_at_bf16(const void *q, const void *k_cache,
                                      int64_t head_dim, float scale, void *out,
                                      void *workspace, size_t workspace_bytes,
                                      void *stream);
+
+/* The same computation as cascade_decode_attention_bf16 with no workspace
+ * argument and no allocation of any kind: the split partials live in a
+ * static device array of the library (one copy per GPU, about 1 MiB, held
+ * until the process ends), sized for n_kv_heads <=
+ * CASCADE_DECODE_ATTENTION_NOALLOC_MAX_KV_HEADS; larger shapes return
+ * CASCADE_ESCRATCH.  Results are bit-identical to
+ * cascade_decode_attention_bf16 (same kernels, same split plan).  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (two streams,
+ * or two host threads) race and must be serialised by the caller.  The first
+ * call on a GPU looks the array's device address up (hipGetSymbolAddress);
+ * later calls only read the cached address.
+ * No counterpart in the reference: this is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).                                                  */
+#define CASCADE_DECODE_ATTENTION_NOALLOC_MAX_KV_HEADS 8
+int cascade_decode_attention_noalloc_bf16(const void *q, const void *k_cache,
+                                          const void *v_cache,
+                                          int64_t kv_head_stride, int64_t len,
+                                          int64_t n_q_heads, int64_t n_kv_heads,
+                                          int64_t head_dim, float scale,
+                                          void *out, void *stream);
 
 /* One whole decoder layer of batch-1 decode in one launch (Llama-3.1-8B
  * shape only: hidden 4096, 32 query / 8 KV heads of 128, intermediate
