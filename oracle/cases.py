@@ -232,3 +232,60 @@ def softmax_attention_reference(q, k, v):
         q.float()[None], kf[None], vf[None], scale=1.0 / math.sqrt(q.shape[-1])
     )[0]
     return out.transpose(0, 1).reshape(q.shape[1], -1)
+
+
+def layer_teacher_forced(inp, out, weights, k_full, v_full, past, cos, sin,
+                         eps=1e-5):
+    """One decoder layer checked on the GPU's own inputs.
+
+    ``inp`` / ``out`` are the layer's input and output hidden rows [S, H]
+    (bf16) as the GPU produced them; ``k_full`` / ``v_full`` the layer's
+    cache [Hkv, past + S, D] after the call (positions < past are the
+    inputs, the rest are the GPU's new K / V rows).  The oracle recomputes
+    the layer from ``inp`` and the cache prefix (decoder_layer,
+    llama31.py:169-283); the output must lie within twice the summation-
+    order noise floor (within_noise_floor) and each new K / V row within
+    the north-star tolerance or that floor.
+    """
+
+    prefix = {"k": k_full[:, :past], "v": v_full[:, :past]} if past else {}
+    alt_prefix = dict(prefix)
+    expected = ref.decoder_layer(inp, weights, prefix, past, cos, sin, eps)
+    alternative = ref.decoder_layer(inp, weights, alt_prefix, past, cos, sin,
+                                    eps, linear_fn=sgemm_linear)
+    report = {"out": within_noise_floor(out, expected, alternative)}
+    ok = report["out"]["ok"]
+    for name, gpu in (("k", k_full), ("v", v_full)):
+        r = compare(gpu[:, past:], prefix[name][:, past:])
+        f = within_noise_floor(gpu[:, past:], prefix[name][:, past:],
+                               alt_prefix[name][:, past:])
+        r["ratio_to_noise_floor"] = f["ratio_to_floor"]
+        r["ok"] = r["ok"] or f["ok"]
+        report[name] = r
+        ok = ok and r["ok"]
+    report["ok"] = bool(ok)
+    return report
+
+
+def reference_metrics(reference_logits, candidate_logits):
+    """The reference's logit comparison (benchmarks/compare_real_logits.py:
+    35-73) over [steps, vocab] fp32 rows: max / mean abs error, RMSE, cosine
+    similarity, argmax match and top-10 overlap per step."""
+
+    ref_rows = reference_logits.float().cpu().reshape(
+        -1, reference_logits.shape[-1])
+    cand = candidate_logits.float().cpu().reshape(ref_rows.shape)
+    delta = cand - ref_rows
+    ref_top = torch.topk(ref_rows, k=10, dim=-1).indices
+    cand_top = torch.topk(cand, k=10, dim=-1).indices
+    return {
+        "max_abs_error": float(delta.abs().max()),
+        "mean_abs_error": float(delta.abs().mean()),
+        "rmse": float(delta.square().mean().sqrt()),
+        "cosine_similarity_per_step": torch.nn.functional.cosine_similarity(
+            ref_rows, cand, dim=-1).tolist(),
+        "argmax_match_per_step": (ref_rows.argmax(-1) == cand.argmax(-1)).tolist(),
+        "top10_overlap_per_step": [
+            len(set(a.tolist()) & set(b.tolist()))
+            for a, b in zip(ref_top, cand_top)],
+    }

@@ -253,14 +253,16 @@ class OracleLlama:
     """Greedy batch=1 decoding of a Llama-3.1-8B-shaped model on the CPU.
 
     ``tensor(key)`` returns the bf16 CPU tensor of a checkpoint key (e.g. a
-    weight store's ``tensor``).  Mirrors Llama31DecodeExecutor: begin
+    weight store's ``tensor``); ``linear_fn`` replaces the GEMV restatement
+    in every layer (default ``linear``).  Mirrors Llama31DecodeExecutor: begin
     (embedding row gather), the layers, finish (final norm, fp32 logits of
     the last position, top-k).
     """
 
     def __init__(self, tensor, num_layers=32, eps=1e-5, rope=None,
-                 n_heads=32, n_kv_heads=8, head_dim=128):
+                 n_heads=32, n_kv_heads=8, head_dim=128, linear_fn=None):
         self.tensor = tensor
+        self.linear_fn = linear_fn
         self.num_layers = int(num_layers)
         self.eps = float(eps)
         self.n_heads = n_heads
@@ -285,6 +287,7 @@ class OracleLlama:
             hidden = decoder_layer(
                 hidden, layer_weights(self.tensor, layer), self.caches[layer],
                 past, cos, sin, self.eps, self.n_heads, self.n_kv_heads,
+                linear_fn=self.linear_fn,
             )
         self.length = past + ids.numel()
         normalized = rms_norm(hidden[-1:], self.tensor("model.norm.weight"), self.eps)
