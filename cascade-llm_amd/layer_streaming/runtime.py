@@ -5,16 +5,18 @@
   reference layer_streaming/runtime.py:33-64.
 * ``DoubleBufferRuntime`` -- the per-token transfer loop of the reference
   (runtime.py:67-268): unit i is copied host->device into slot i % slots on
-  a copy stream while the compute stream runs unit i-1.  The copies are
-  hipMemcpyAsync calls and the ready / free handoff uses hipEvents, all
+  a copy stream while the compute stream runs the units before it.  The
+  copies are hipMemcpyAsync calls and the hand-off uses hipEvents, all
   through libcascade_hip (cascade_memcpy_h2d_async, cascade_event_*).
   Ordering invariants (runtime.py:70-74, :194-230):
-    - copy i waits for free[i - slots] (the compute that last read slot i);
-    - compute i waits for ready[i];
-    - a staging worker may refill host slot i % slots once ready[i] fired.
-  In addition both streams wait for the caller's stream at the start of
-  run(), so device work the caller enqueued before (e.g. the embedding
-  gather) is ordered before the first unit.
+    - a copy into a slot waits for the compute that last read the slot;
+    - compute i is enqueued once copy i is complete (the host waits for
+      its event; the reference makes the compute stream wait for it);
+    - a staging worker may refill pinned bytes once the copies that read
+      them fired.
+  Slots remember what they hold, so copies run ahead across calls (the LM
+  head's first chunks behind the last units, the next call's first units
+  behind the last chunks).
 * ``ResidentTransformerRuntime`` -- same ``run`` contract with every transfer
   unit resident in HBM (no streaming); the configuration used to measure
   the decode kernels against the HBM roofline.
@@ -144,7 +146,36 @@ def _unit_views(unit, base):
 
 
 class DoubleBufferRuntime:
-    """Two device slots with a copy stream and a compute stream."""
+    """Device slots filled on a copy stream, read on a compute stream.
+
+    Unit i goes to slot i % slot_count, as in the reference's loop
+    (runtime.py:137-268): its copy waits until the slot's last reader is
+    done, and its compute follows its copy.  Two things differ:
+
+    * The copy -> compute hand-off is made by the host.  The host waits for
+      copy i's event, then enqueues ``compute_unit(unit i)`` on the compute
+      stream, so the compute stream never waits on a copy-stream event.  On
+      MI355X such a cross-stream wait slowed every copy by about 0.6% (56.30
+      against 56.64 GB/s for a 48/32/224/112 MiB layer sequence); a copy
+      stream waiting for compute events costs nothing measurable.  The host
+      is idle otherwise: copy i + 1 is already queued while it waits.
+    * Slots are owned.  Each slot remembers the last transfer it received
+      (a unit of this runtime or an LM-head chunk of the vocabulary runtime
+      that shares the slots) and that copy's ready event, and a consumer
+      that finds its transfer already in the slot skips the copy.  Copies can
+      therefore run ahead of the calls that use them: as the last units free
+      their slots, the first LM-head chunks are copied in (``release_hook``,
+      set by VocabStreamingRuntime); as the last chunks (or, with a resident
+      vocabulary, the last units) free theirs, the next call's first units
+      are, when the store is full_pinned (``prefetch_across_calls``).  The
+      copy engine then never waits for the host between tokens.
+
+    run() returns once every unit's work is enqueued; the coordinator
+    (caller's) stream waits for the last unit, without a host
+    synchronisation (with profile=True run() synchronises to read its
+    events).  After a run that raised, the next run first waits for every
+    copy, kernel and staging job the failed one left in flight.
+    """
 
     def __init__(self, plan, store, resident, device="cuda:0", slot_count=None,
                  profile=False):
@@ -163,14 +194,21 @@ class DoubleBufferRuntime:
         ]
         self.copy_stream = torch.cuda.Stream(device=self.device)
         self.compute_stream = torch.cuda.Stream(device=self.device)
+        self.coordinator = torch.cuda.current_stream(self.device)
         # pinned_staging: units staged ahead of the one being copied (ring
         # room permitting)
         self.stage_lookahead = 8
+        self.prefetch_across_calls = True
+        # called with a slot index when the last unit of a call that uses
+        # that slot has been enqueued (VocabStreamingRuntime copies its
+        # first chunks from here)
+        self.release_hook = None
+        self._owner = [None] * self.slot_count      # (kind, index, ready event)
+        self._last_free = [None] * self.slot_count  # event of the last reader
+        self._failed = False
         self._staging_left = {}
-        self.coordinator = torch.cuda.current_stream(self.device)
+        self._timed_copies = {}
         count = len(plan.units)
-        # Events are created once and re-recorded every token (each run()
-        # ends with a full synchronisation, so reuse is safe).
         self._ready = [_hip.HipEvent() for _ in range(count)]
         self._free = [_hip.HipEvent() for _ in range(count)]
         self._start = _hip.HipEvent()
@@ -208,116 +246,198 @@ class DoubleBufferRuntime:
     def _unit_views(self, unit, slot):
         return _unit_views(unit, slot)
 
+    # ------------------------------------------------------ slot ownership
+
+    def slot_copy(self, slot, kind, index, source, nbytes, ready, timing=None):
+        """Copy ``nbytes`` of pinned ``source`` into device slot ``slot`` on
+        the copy stream once the slot's last reader is done; ``ready`` is
+        recorded after the copy, and the slot now holds (kind, index)."""
+
+        stream = self.copy_stream
+        if self._last_free[slot] is not None:
+            self._last_free[slot].wait(stream)
+        if timing is not None:
+            timing[0].record(stream)
+        _hip.memcpy_h2d_async(self.device_slots[slot], source, nbytes, stream)
+        if timing is not None:
+            timing[1].record(stream)
+        ready.record(stream)
+        self._owner[slot] = (kind, index, ready)
+
+    def slot_holding(self, slot, kind, index):
+        """Ready event of the copy that put (kind, index) in ``slot``, or
+        None when the slot holds something else."""
+
+        owner = self._owner[slot]
+        if owner is not None and owner[0] == kind and owner[1] == index:
+            return owner[2]
+        return None
+
+    def slot_released(self, slot, free):
+        """``free`` (a compute-stream event) marks the end of the last
+        reader of ``slot``: later copies into the slot wait for it."""
+
+        self._last_free[slot] = free
+
+    def discard_slots(self):
+        """Forget what the slots hold (after the host weights changed)."""
+
+        self._owner = [None] * self.slot_count
+
+    def prefetch_next_call(self, slot):
+        """Copy the first unit a call reads from ``slot`` ahead of that
+        call, when the store's source needs no staging (full_pinned)."""
+
+        units = self.plan.units
+        if (not self.prefetch_across_calls or slot >= len(units)
+                or self.store.mode.value != "full_pinned"):
+            return
+        if self.slot_holding(slot, "unit", slot) is not None:
+            return
+        unit = units[slot]
+        self.slot_copy(slot, "unit", slot, self.store.unit_source(unit),
+                       unit.nbytes, self._ready[slot])
+
+    # ----------------------------------------------------------------- run
+
+    def _recover(self):
+        """Wait for what a run that raised left in flight."""
+
+        for future in self._staging_left.values():
+            try:
+                future.result()
+            except Exception:  # that run already raised
+                pass
+        self._staging_left = {}
+        self.copy_stream.synchronize()
+        self.compute_stream.synchronize()
+        ring = getattr(self.store, "staging_ring", None)
+        if ring is not None:
+            ring.reset()
+        self._failed = False
+
     def run(self, compute_unit, state):
+        if not self.plan.units:
+            return state
+        if self._failed:
+            self._recover()
+        self._failed = True
+        state = self._run(compute_unit, state)
+        self._failed = False
+        return state
+
+    def _run(self, compute_unit, state):
         wall_started = time.perf_counter()
         units = self.plan.units
-        if not units:
-            return state
+        count = len(units)
         slots = self.slot_count
-        copy_stream = self.copy_stream
         compute_stream = self.compute_stream
         timing = self._timing_events() if self.profile else None
+        self.store.reset_profile()
+        self._timed_copies = {}
 
+        # work the caller enqueued before (the embedding) precedes the units
         self._start.record(self.coordinator)
-        self._start.wait(copy_stream)
         self._start.wait(compute_stream)
         if timing:
             timing["pipeline"][0].record(self.coordinator)
 
-        self.store.reset_profile()
         staging = self.store.mode.value == "pinned_staging"
         ring = getattr(self.store, "staging_ring", None) if staging else None
         staged = {}
+        self._staging_left = staged
         next_stage = 0
-        if ring is None:
-            staged = {i: self.store.prepare_unit(units[i], i)
-                      for i in range(min(slots, len(units)))}
-        else:
-            # The ring starts empty: every copy of the previous run is done
-            # (a normal run ends synchronised; the copy stream is then idle
-            # and this costs nothing), and so is every staging job it left
-            # behind if it ended in an exception.
-            for future in self._staging_left.values():
-                try:
-                    future.result()
-                except Exception:  # that run already raised
-                    pass
-            self._staging_left = {}
-            copy_stream.synchronize()
-            ring.reset()
 
         def stage_ahead(done):
-            # ring staging: units after ``done`` (whose copy is enqueued)
-            # go to the staging workers while the ring has room for them
+            # ring staging: units after ``done`` (whose copy is enqueued) go
+            # to the staging workers while the ring has room for them
             nonlocal next_stage
-            while next_stage < len(units) and next_stage - done <= self.stage_lookahead:
+            while next_stage < count and next_stage - done <= self.stage_lookahead:
                 placed = ring.place(units[next_stage].nbytes, next_stage)
                 if placed is None:
                     break
-                staged[next_stage] = self.store.stage_in_ring(units[next_stage], *placed)
+                staged[next_stage] = self.store.stage_in_ring(units[next_stage],
+                                                              *placed)
                 next_stage += 1
 
-        if ring is not None:
-            self._staging_left = staged  # drained by the next run if this one raises
-            stage_ahead(-1)
-
         source_wait_ms = 0.0
-        submit_started = time.perf_counter()
-        for index, unit in enumerate(units):
-            slot_index = index % slots
-            slot = self.device_slots[slot_index]
-            waited = time.perf_counter()
-            source = staged.pop(index).result()
-            source_wait_ms += (time.perf_counter() - waited) * 1000.0
 
-            if index >= slots:
-                self._free[index - slots].wait(copy_stream)
+        def copy_unit(i):
+            # the source (staged for pinned_staging), then the copy
+            nonlocal source_wait_ms
+            slot = i % slots
+            if staging:
+                waited = time.perf_counter()
+                source = staged.pop(i).result()
+                source_wait_ms += (time.perf_counter() - waited) * 1000.0
+            else:
+                source = self.store.unit_source(units[i])
+            pair = None
             if timing:
-                timing["copy_start"][index].record(copy_stream)
-            _hip.memcpy_h2d_async(slot, source, unit.nbytes, copy_stream)
-            if timing:
-                timing["copy_end"][index].record(copy_stream)
-            self._ready[index].record(copy_stream)
-
-            ahead = index + slots
+                pair = (timing["copy_start"][i], timing["copy_end"][i])
+                self._timed_copies[i] = units[i].nbytes
+            self.slot_copy(slot, "unit", i, source, units[i].nbytes,
+                           self._ready[i], pair)
             if ring is not None:
-                ring.copied(index, self._ready[index])
-                stage_ahead(index)
-            elif ahead < len(units):
-                # The staging worker may overwrite host slot `slot_index` as
-                # soon as this H2D copy has completed; it need not wait for
-                # the compute, which reads the device slot.
-                staged[ahead] = self.store.prepare_unit(
-                    units[ahead],
-                    slot_index,
-                    reuse_event=self._ready[index] if staging else None,
-                )
+                ring.copied(i, self._ready[i])
+                stage_ahead(i)
+            elif staging and i + slots < count:
+                # the staging worker may refill this pinned slot once this
+                # copy has read it (it need not wait for the compute)
+                staged[i + slots] = self.store.prepare_unit(
+                    units[i + slots], slot, reuse_event=self._ready[i])
 
-            self._ready[index].wait(compute_stream)
+        if ring is not None:
+            ring.reset()  # every copy that read the pinned slots is done
+            stage_ahead(-1)
+        elif staging:
+            for i in range(min(slots, count)):
+                staged[i] = self.store.prepare_unit(units[i], i)
+        ready = {}
+        for i in range(min(slots, count)):
+            held = self.slot_holding(i % slots, "unit", i)
+            if held is not None and not staging:
+                ready[i] = held  # copied ahead of this call
+            else:
+                copy_unit(i)
+                ready[i] = self._ready[i]
+
+        submit_started = time.perf_counter()
+        for i, unit in enumerate(units):
+            slot = i % slots
+            ready.pop(i).synchronize()  # host hand-off: copy i is in HBM
             with torch.cuda.stream(compute_stream):
                 if timing:
-                    timing["compute_start"][index].record(compute_stream)
-                state = compute_unit(unit, self._unit_views(unit, slot), state)
+                    timing["compute_start"][i].record(compute_stream)
+                state = compute_unit(unit, self._unit_views(unit, self.device_slots[slot]),
+                                     state)
                 if timing:
-                    timing["compute_end"][index].record(compute_stream)
-                self._free[index].record(compute_stream)
+                    timing["compute_end"][i].record(compute_stream)
+                self._free[i].record(compute_stream)
+            self.slot_released(slot, self._free[i])
+            following = i + slots
+            if following < count:
+                copy_unit(following)
+                ready[following] = self._ready[following]
+            elif self.release_hook is not None:
+                self.release_hook(slot)
+            else:
+                self.prefetch_next_call(slot)
 
         submit_ms = (time.perf_counter() - submit_started) * 1000.0
-        self._free[len(units) - 1].wait(self.coordinator)
+        self._free[count - 1].wait(self.coordinator)
         if timing:
             timing["pipeline"][1].record(self.coordinator)
-        self.coordinator.synchronize()
-        wall_ms = (time.perf_counter() - wall_started) * 1000.0
-        if timing:
-            h2d_ms = sum(
-                a.elapsed_time(b)
-                for a, b in zip(timing["copy_start"], timing["copy_end"])
-            )
+            timing["pipeline"][1].synchronize()
+            wall_ms = (time.perf_counter() - wall_started) * 1000.0
+            timed = self._timed_copies
+            h2d_ms = sum(timing["copy_start"][i].elapsed_time(timing["copy_end"][i])
+                         for i in timed)
             compute_ms = sum(
                 a.elapsed_time(b)
                 for a, b in zip(timing["compute_start"], timing["compute_end"])
             )
-            nbytes = self.plan.stream_bytes_per_token
+            nbytes = sum(timed.values())
             self.last_profile = {
                 "wall_ms": wall_ms,
                 "host_submit_ms": submit_ms,
@@ -327,8 +447,10 @@ class DoubleBufferRuntime:
                 ),
                 "h2d_event_sum_ms": h2d_ms,
                 "compute_event_sum_ms": compute_ms,
-                "h2d_bytes": nbytes,
-                "h2d_effective_gbps": (nbytes / 1e9) / (h2d_ms / 1000.0),
+                "h2d_bytes": self.plan.stream_bytes_per_token,
+                "h2d_timed_bytes": nbytes,
+                "h2d_effective_gbps": (nbytes / 1e9) / (h2d_ms / 1000.0)
+                if h2d_ms else 0.0,
             }
             self.last_profile.update(self.store.profile_stats())
         return state

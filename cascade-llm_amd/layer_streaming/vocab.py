@@ -1,20 +1,26 @@
-"""Row lookup and vocabulary-sharded LM head (reference layer_streaming/vocab.py).
+"""Host-only vocabulary of a streamed-vocabulary plan (reference
+layer_streaming/vocab.py).
 
-* ``embedding(ids)`` gathers the requested rows of the host-only embedding
-  into a page-locked staging buffer and copies them to the device
-  (vocab.py:100-131).
+* ``embedding(ids)`` gathers the requested rows of the host embedding into a
+  page-locked row buffer and copies them to the device on the caller's
+  stream (vocab.py:100-131).  Nothing waits on the host: an event guards the
+  row buffer until the copy that reads it is done.
 * ``lm_head_topk(h, top_k, return_full_logits)`` streams the LM head in row
   chunks through the transformer runtime's two device slots and keeps an
   exact running top-k on the device (vocab.py:149-300).  Per chunk there is
-  one kernel launch (cascade_lm_head_topk_bf16: GEMV to fp32 logits, block
-  top-k and the merge with the running list), and no host synchronisation
-  until the end of the call.
+  one kernel launch (cascade_lm_head_topk_bf16: fp32 logits GEMV, block
+  top-k and the merge with the running list).  Hand-off and slot ownership
+  follow DoubleBufferRuntime: the host waits for a chunk's copy, then
+  enqueues its kernel; with a full_pinned store the first two chunks are
+  copied while the transformer's last units still run, and the next call's
+  first units while the last chunks run.  The call returns when the top-k
+  is in HBM (the reference synchronises there too, vocab.py:268-271).
 * ``merge_topk`` is the reference's public helper (vocab.py:11-32) with a
   deterministic order on ties (value descending, index ascending).
 
 Logits are fp32 and not rounded to bf16 (the reference rounds them through
-bf16 first, which creates ties inside the top-10 for almost every step at
-this shape); the top-k order equals a stable descending sort of them.
+bf16 first, which ties inside the top-10 for almost every step at this
+shape); the top-k order equals a stable descending sort of them.
 """
 
 import time
@@ -49,97 +55,151 @@ def merge_topk(current_values, current_indices, candidate_values,
     return torch.gather(values, -1, order), torch.gather(indices, -1, order)
 
 
+def _pinned_rows(count, width):
+    return torch.empty((count, width), dtype=torch.bfloat16, device="cpu",
+                       pin_memory=True)
+
+
 class VocabStreamingRuntime:
-    """Share the transformer runtime's slots for the LM-head chunks."""
+    """Embedding rows and LM-head chunks of a host-only vocabulary, sharing
+    the transformer runtime's two device slots and streams."""
 
     def __init__(self, plan, store, transformer_runtime,
                  embedding_staging_rows=256, profile=False):
-        if plan.vocab is None:
-            raise ValueError("plan does not enable vocabulary streaming")
+        layout = plan.vocab
+        if layout is None:
+            raise ValueError("the plan keeps the vocabulary resident "
+                             "(build it with stream_vocab=True)")
+        row_buffer = int(embedding_staging_rows)
+        if row_buffer < 1:
+            raise ValueError("embedding_staging_rows must be at least 1, got "
+                             "{}".format(row_buffer))
+        runtime = transformer_runtime
+        if len(runtime.device_slots) != 2:
+            raise ValueError("the LM head streams through two device slots, the "
+                             "runtime has {}".format(len(runtime.device_slots)))
+        smallest = min(slot.numel() for slot in runtime.device_slots)
+        if smallest < layout.chunk_elements:
+            raise ValueError("a device slot of {} elements cannot take a "
+                             "{}-element LM-head chunk".format(
+                                 smallest, layout.chunk_elements))
         _hip.load()
         self.plan = plan
-        self.vocab = plan.vocab
+        self.vocab = layout
         self.store = store
-        self.transformer_runtime = transformer_runtime
-        self.device = transformer_runtime.device
-        self.device_slots = transformer_runtime.device_slots
-        self.copy_stream = transformer_runtime.copy_stream
-        self.compute_stream = transformer_runtime.compute_stream
-        self.coordinator = transformer_runtime.coordinator
+        self.transformer_runtime = runtime
+        self.device = runtime.device
+        self.device_slots = runtime.device_slots
+        self.copy_stream = runtime.copy_stream
+        self.compute_stream = runtime.compute_stream
+        self.coordinator = runtime.coordinator
         self.profile = bool(profile)
         self.last_profile = None
         self.last_embedding_bytes = 0
-        self.embedding_staging_rows = int(embedding_staging_rows)
-        if self.embedding_staging_rows < 1:
-            raise ValueError("embedding_staging_rows must be positive")
-        if len(self.device_slots) != 2:
-            raise ValueError("vocabulary streaming requires two GPU slots")
-        if self.device_slots[0].numel() < self.vocab.chunk_elements:
-            raise ValueError("shared GPU slot is smaller than vocab chunk")
-        self.embedding_staging = torch.empty(
-            (self.embedding_staging_rows, self.vocab.hidden_size),
-            dtype=torch.bfloat16, device="cpu", pin_memory=True,
-        )
+        self.embedding_staging_rows = row_buffer
+        self.embedding_staging = _pinned_rows(row_buffer, layout.hidden_size)
+        # pinned_staging: the pageable LM head passes through two pinned
+        # chunk buffers (one allocation, split in halves)
+        self._staged = store.mode == WeightStoreMode.PINNED_STAGING
         self.head_staging_slots = None
-        if self.store.mode == WeightStoreMode.PINNED_STAGING:
-            self.head_staging_slots = [
-                torch.empty(self.vocab.chunk_elements, dtype=torch.bfloat16,
-                            device="cpu", pin_memory=True)
-                for _ in range(2)
-            ]
-        count = self.vocab.chunk_count
-        self._ready = [_hip.HipEvent() for _ in range(count)]
-        self._free = [_hip.HipEvent() for _ in range(count)]
+        if self._staged:
+            both = torch.empty(2 * layout.chunk_elements, dtype=torch.bfloat16,
+                               device="cpu", pin_memory=True)
+            self.head_staging_slots = list(both.split(layout.chunk_elements))
+        chunks = layout.chunk_count
+        self._ready = [_hip.HipEvent() for _ in range(chunks)]
+        self._free = [_hip.HipEvent() for _ in range(chunks)]
+        self._staging_read = [None, None]  # copy that last read a pinned half
         self._start = _hip.HipEvent()
-        self._embed_done = _hip.HipEvent()
-        self._timing = None
+        self._rows_free = _hip.HipEvent()
+        self._timers = None
+        self._timed = {}
         self._workspaces = {}
+        if not self._staged:
+            # the first chunks follow the transformer's last units directly
+            runtime.release_hook = self._copy_first_chunk
 
     @property
     def gpu_slot_bytes(self):
-        return sum(s.numel() * s.element_size() for s in self.device_slots)
+        return sum(slot.numel() * slot.element_size() for slot in self.device_slots)
 
     @property
     def extra_pinned_cpu_bytes(self):
-        total = self.embedding_staging.numel() * self.embedding_staging.element_size()
-        if self.head_staging_slots is not None:
-            total += sum(s.numel() * s.element_size() for s in self.head_staging_slots)
-        return total
+        buffers = [self.embedding_staging] + list(self.head_staging_slots or ())
+        return sum(b.numel() * b.element_size() for b in buffers)
+
+    # --------------------------------------------------------- embedding
 
     def embedding(self, input_ids):
-        """Gather only the requested CPU rows and transfer them to the GPU."""
+        """Gather only the requested CPU rows and copy them to the GPU."""
 
         shape = tuple(input_ids.shape)
         ids = input_ids.detach().reshape(-1).to(device="cpu", dtype=torch.long)
-        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.vocab.vocab_size):
-            raise IndexError("token id outside the vocabulary")
+        count = ids.numel()
+        vocab, width = self.vocab.vocab_size, self.vocab.hidden_size
+        if count and (int(ids.min()) < 0 or int(ids.max()) >= vocab):
+            raise IndexError("token id outside [0, {})".format(vocab))
         table = self.store.tensor(self.vocab.embedding_key)
-        out = torch.empty((ids.numel(), self.vocab.hidden_size),
-                          dtype=torch.bfloat16, device=self.device)
-        self.last_embedding_bytes = ids.numel() * self.vocab.hidden_size * 2
-        group = self.embedding_staging_rows
-        for start in range(0, ids.numel(), group):
-            end = min(start + group, ids.numel())
-            staging = self.embedding_staging[: end - start]
-            torch.index_select(table, 0, ids[start:end], out=staging)
-            _hip.memcpy_h2d_async(out[start:end], staging,
-                                  staging.numel() * 2, self.copy_stream)
-            self._embed_done.record(self.copy_stream)
-            # the staging rows are reused by the next group
-            self._embed_done.synchronize()
-        return out.view(shape + (self.vocab.hidden_size,))
+        out = torch.empty((count, width), dtype=torch.bfloat16, device=self.device)
+        self.last_embedding_bytes = count * width * 2
+        stream = torch.cuda.current_stream(self.device)
+        for first in range(0, count, self.embedding_staging_rows):
+            rows = min(self.embedding_staging_rows, count - first)
+            # the row buffer is free once the copy that last read it is done
+            self._rows_free.synchronize()
+            buffer = self.embedding_staging[:rows]
+            torch.index_select(table, 0, ids[first:first + rows], out=buffer)
+            _hip.memcpy_h2d_async(out[first:first + rows], buffer,
+                                  rows * width * 2, stream)
+            self._rows_free.record(stream)
+        return out.view(shape + (width,))
 
-    def _head_source(self, start_row, end_row, slot_index, ready_event):
-        source = self.store.tensor(self.vocab.lm_head_key)[start_row:end_row].reshape(-1)
-        if self.head_staging_slots is None:
-            if not source.is_pinned():
-                raise RuntimeError("full_pinned LM-head source unexpectedly is not pinned")
-            return source
-        if ready_event is not None:
-            ready_event.synchronize()
-        target = self.head_staging_slots[slot_index][: source.numel()]
-        _hip.host_copy(target, source, getattr(self.store, "copy_threads", None))
+    # ----------------------------------------------------------- LM head
+
+    def _chunk_source(self, chunk):
+        """Pinned host rows of one chunk (staged first for pinned_staging)."""
+
+        first, end = self.vocab.chunk_bounds(chunk)
+        rows = self.store.tensor(self.vocab.lm_head_key)[first:end].reshape(-1)
+        if not self._staged:
+            if not rows.is_pinned():
+                raise RuntimeError("a full_pinned store must hold the LM head "
+                                   "in page-locked memory")
+            return rows
+        half = chunk % 2
+        reader = self._staging_read[half]
+        if reader is not None:
+            reader.synchronize()  # the copy that read this half is done
+        target = self.head_staging_slots[half][: rows.numel()]
+        _hip.host_copy(target, rows, getattr(self.store, "copy_threads", None))
+        self._staging_read[half] = self._ready[chunk]
         return target
+
+    def _copy_chunk(self, chunk):
+        first, end = self.vocab.chunk_bounds(chunk)
+        nbytes = (end - first) * self.vocab.hidden_size * 2
+        pair = None
+        if self.profile:
+            timers = self._timing()
+            pair = (timers["copy_start"][chunk], timers["copy_end"][chunk])
+            self._timed[chunk] = nbytes
+        self.transformer_runtime.slot_copy(chunk % 2, "chunk", chunk,
+                                           self._chunk_source(chunk), nbytes,
+                                           self._ready[chunk], pair)
+
+    def _copy_first_chunk(self, slot):
+        """Release hook of the transformer runtime: its last unit in
+        ``slot`` is enqueued, so chunk ``slot`` can follow it there."""
+
+        if slot < self.vocab.chunk_count:
+            self._copy_chunk(slot)
+
+    def _chunk_ready(self, chunk):
+        held = self.transformer_runtime.slot_holding(chunk % 2, "chunk", chunk)
+        if held is not None:
+            return held
+        self._copy_chunk(chunk)
+        return self._ready[chunk]
 
     def _workspace(self, top_k):
         ws = self._workspaces.get(top_k)
@@ -150,102 +210,106 @@ class VocabStreamingRuntime:
             self._workspaces[top_k] = ws
         return ws
 
-    def _timing_events(self):
-        if self._timing is None:
+    def _timing(self):
+        if self._timers is None:
             n = self.vocab.chunk_count
 
-            def make(k):
+            def events(k):
                 return [_hip.HipEvent(enable_timing=True) for _ in range(k)]
 
-            self._timing = {
-                "pipeline": make(2), "copy_start": make(n), "copy_end": make(n),
-                "compute_start": make(n), "compute_end": make(n),
+            self._timers = {
+                "pipeline": events(2), "copy_start": events(n), "copy_end": events(n),
+                "compute_start": events(n), "compute_end": events(n),
             }
-        return self._timing
+        return self._timers
 
     def lm_head_topk(self, hidden_states, top_k=10, return_full_logits=False):
         """Stream row shards and maintain an exact global top-k."""
 
-        if hidden_states.shape[-1] != self.vocab.hidden_size:
-            raise ValueError("hidden state width does not match vocabulary")
-        if top_k < 1 or top_k > self.vocab.vocab_size:
-            raise ValueError("top_k is outside vocabulary range")
+        width, vocab = self.vocab.hidden_size, self.vocab.vocab_size
+        if hidden_states.shape[-1] != width:
+            raise ValueError("hidden width {} does not match the vocabulary's "
+                             "{}".format(hidden_states.shape[-1], width))
+        if top_k < 1 or top_k > vocab:
+            raise ValueError("top_k must lie in [1, {}], got {}".format(vocab, top_k))
         if top_k > 64:
-            raise ValueError("top_k above 64 is not supported by the LM-head kernel")
-        hidden = hidden_states.reshape(-1, self.vocab.hidden_size)
-        if hidden.shape[0] != 1:
-            raise ValueError("the streamed LM head takes one position")
-        hidden = hidden[0].contiguous()
-        wall_started = time.perf_counter()
+            raise ValueError("the LM-head kernel keeps at most 64 candidates "
+                             "(top_k {})".format(top_k))
+        rows = hidden_states.reshape(-1, width)
+        if rows.shape[0] != 1:
+            raise ValueError("the streamed LM head scores one position, got "
+                             "{}".format(rows.shape[0]))
+        hidden = rows[0].contiguous()
+        started = time.perf_counter()
+        top_k = int(top_k)
+        runtime = self.transformer_runtime
         chunks = self.vocab.chunk_count
-        timing = self._timing_events() if self.profile else None
-        workspace = self._workspace(int(top_k))
+        timers = self._timing() if self.profile else None
+        workspace = self._workspace(top_k)
         lead = hidden_states.shape[:-1]
-        values = torch.empty(lead + (int(top_k),), dtype=torch.float32, device=self.device)
-        indices = torch.empty(lead + (int(top_k),), dtype=torch.int64, device=self.device)
+        values = torch.empty(lead + (top_k,), dtype=torch.float32, device=self.device)
+        indices = torch.empty(lead + (top_k,), dtype=torch.int64, device=self.device)
         logits = None
         if return_full_logits:
-            logits = torch.empty(lead + (self.vocab.vocab_size,),
-                                 dtype=torch.float32, device=self.device)
+            logits = torch.empty(lead + (vocab,), dtype=torch.float32,
+                                 device=self.device)
         flat_logits = None if logits is None else logits.view(-1)
 
+        # the hidden state (written on the caller's stream) precedes the kernels
         self._start.record(self.coordinator)
-        self._start.wait(self.copy_stream)
         self._start.wait(self.compute_stream)
-        if timing:
-            timing["pipeline"][0].record(self.coordinator)
-        transferred = 0
-        for c in range(chunks):
-            slot_index = c % 2
-            start_row, end_row = self.vocab.chunk_bounds(c)
-            rows = end_row - start_row
-            elements = rows * self.vocab.hidden_size
-            source = self._head_source(start_row, end_row, slot_index,
-                                       self._ready[c - 2] if c >= 2 else None)
-            slot = self.device_slots[slot_index]
-            if c >= 2:
-                self._free[c - 2].wait(self.copy_stream)
-            if timing:
-                timing["copy_start"][c].record(self.copy_stream)
-            _hip.memcpy_h2d_async(slot, source, elements * 2, self.copy_stream)
-            if timing:
-                timing["copy_end"][c].record(self.copy_stream)
-            self._ready[c].record(self.copy_stream)
-            transferred += elements * 2
+        if timers:
+            timers["pipeline"][0].record(self.coordinator)
+        ready = {c: self._chunk_ready(c) for c in range(min(2, chunks))}
+        for chunk in range(chunks):
+            first, end = self.vocab.chunk_bounds(chunk)
+            slot = chunk % 2
+            ready.pop(chunk).synchronize()  # host hand-off: the chunk is in HBM
+            weight = self.device_slots[slot][: (end - first) * width].view(-1, width)
+            with torch.cuda.stream(self.compute_stream):
+                if timers:
+                    timers["compute_start"][chunk].record(self.compute_stream)
+                _hip.lm_head_topk(
+                    weight, hidden, top_k, first, chunk == 0, workspace, values,
+                    indices,
+                    logits_out=None if flat_logits is None else flat_logits[first:end],
+                    stream=self.compute_stream,
+                )
+                if timers:
+                    timers["compute_end"][chunk].record(self.compute_stream)
+                self._free[chunk].record(self.compute_stream)
+            runtime.slot_released(slot, self._free[chunk])
+            if chunk + 2 < chunks:
+                ready[chunk + 2] = self._chunk_ready(chunk + 2)
+            else:
+                runtime.prefetch_next_call(slot)
 
-            self._ready[c].wait(self.compute_stream)
-            if timing:
-                timing["compute_start"][c].record(self.compute_stream)
-            weight = slot[:elements].view(rows, self.vocab.hidden_size)
-            _hip.lm_head_topk(
-                weight, hidden, int(top_k), start_row, c == 0, workspace,
-                values, indices,
-                logits_out=None if flat_logits is None else flat_logits[start_row:end_row],
-                stream=self.compute_stream,
-            )
-            if timing:
-                timing["compute_end"][c].record(self.compute_stream)
-            self._free[c].record(self.compute_stream)
-
-        self._free[chunks - 1].wait(self.coordinator)
-        if timing:
-            timing["pipeline"][1].record(self.coordinator)
-        self.coordinator.synchronize()
-        wall_ms = (time.perf_counter() - wall_started) * 1000.0
-        if timing:
-            h2d_ms = sum(a.elapsed_time(b) for a, b in
-                         zip(timing["copy_start"], timing["copy_end"]))
+        last = self._free[chunks - 1]
+        last.wait(self.coordinator)
+        if timers:
+            timers["pipeline"][1].record(self.coordinator)
+        last.synchronize()  # values / indices are in HBM on return
+        if timers:
+            timers["pipeline"][1].synchronize()
+            wall_ms = (time.perf_counter() - started) * 1000.0
+            h2d_ms = sum(timers["copy_start"][c].elapsed_time(timers["copy_end"][c])
+                         for c in self._timed)
             compute_ms = sum(a.elapsed_time(b) for a, b in
-                             zip(timing["compute_start"], timing["compute_end"]))
+                             zip(timers["compute_start"], timers["compute_end"]))
+            timed_bytes = sum(self._timed.values())
             self.last_profile = {
                 "wall_ms": wall_ms,
-                "pipeline_ms": timing["pipeline"][0].elapsed_time(timing["pipeline"][1]),
+                "pipeline_ms": timers["pipeline"][0].elapsed_time(timers["pipeline"][1]),
                 "h2d_event_sum_ms": h2d_ms,
                 "compute_event_sum_ms": compute_ms,
-                "h2d_bytes": transferred,
-                "h2d_effective_gbps": (transferred / 1e9) / (h2d_ms / 1000.0),
+                "h2d_bytes": vocab * width * 2,
+                "h2d_timed_bytes": timed_bytes,
+                "h2d_effective_gbps": (timed_bytes / 1e9) / (h2d_ms / 1000.0)
+                if h2d_ms else 0.0,
                 "chunk_count": chunks,
                 "chunk_rows": self.vocab.chunk_rows,
-                "requested_top_k": int(top_k),
+                "requested_top_k": top_k,
             }
+        # chunks copied from here on (ahead of the next call) count there
+        self._timed = {}
         return {"values": values, "indices": indices, "logits": logits}
