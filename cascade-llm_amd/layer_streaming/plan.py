@@ -53,7 +53,8 @@ MATRIX_GROUPS = (
 
 
 class Granularity(str, Enum):
-    """Smallest independently transferred model unit."""
+    """How weights are cut into transfer units: one projection, one
+    projection group, or one whole decoder layer per copy."""
 
     MATRIX = "matrix"
     MATRIX_GROUP = "matrix_group"
@@ -111,7 +112,7 @@ class ResidentPlacement:
 
 @dataclass(frozen=True)
 class HostPlacement:
-    """CPU-only tensor placement inside the shared packed host arena."""
+    """A tensor that lives only in the host arena (the streamed vocabulary)."""
 
     tensor: TensorSpec
     host_offset_elements: int
@@ -119,7 +120,8 @@ class HostPlacement:
 
 @dataclass(frozen=True)
 class VocabPlan:
-    """Row-contiguous CPU vocabulary layout shared by lookup and projection."""
+    """Embedding and LM head kept on the host: the row chunks the LM head
+    streams in and the keys both tables are read under."""
 
     embedding_key: str
     lm_head_key: str

@@ -1,37 +1,39 @@
-"""Host weight stores: one packed bf16 arena, fully pinned or staged.
+"""Host weight stores: one packed bf16 arena, page-locked whole or staged.
 
-API and behaviour follow the reference (layer_streaming/weight_store.py):
+Public surface as in the reference (layer_streaming/weight_store.py):
+``WeightStoreMode``, ``BaseWeightStore``, ``FullPinnedWeightStore``,
+``PinnedStagingWeightStore`` and ``create_weight_store``, with the same
+constructor arguments, ``tensor`` / ``unit_source`` / ``prepare_unit`` /
+``load_checkpoint`` / ``close`` / ``profile_stats`` and error types.
 
-* ``FullPinnedWeightStore`` page-locks the whole arena; ``prepare_unit``
-  returns an already-resolved future over the arena view (:184-206).
-* ``PinnedStagingWeightStore`` keeps a pageable arena plus ``slot_count``
-  page-locked staging slots filled by worker threads; a worker first waits on
-  ``reuse_event`` (the H2D copy that last read its slot) and then copies the
-  unit in (:209-298) with the library's multi-threaded non-temporal memcpy
-  (``cascade_host_copy``; ``copy_threads`` threads, default this process's
-  CPUs up to 8) instead of one tensor copy.
-* Staging ring (added): the runtime stages units at consecutive byte ranges
-  of the same pinned slots, so several small units can be staged ahead of
-  their copies (``StagingRing``); ``prepare_unit`` keeps the reference's
-  one-unit-per-slot behaviour.
-* ``load_checkpoint`` fills the arena from a local safetensors file or
-  sharded index with key and shape checks (:20-38, :109-171).
-* ``tensor_factory`` is injectable for tests (:55).
-
-Added here: ``fill_random`` writes the seeded synthetic weights the
-benchmark configurations use (there is no checkpoint on the GPU hosts).
+* The arena follows the plan's packed layout; a key -> (offset, shape)
+  table with aliases resolved is built once per store.
+* full_pinned page-locks the arena; a unit's source is its arena view
+  (``prepare_unit`` hands back a completed future).
+* pinned_staging keeps the arena pageable and moves units through pinned
+  staging buffers.  A ``_Stager`` owns those buffers, their byte ring
+  (``StagingRing``) and its own worker threads; each job waits for the copies
+  that last read its bytes, then copies with the library's multi-threaded
+  non-temporal memcpy (``cascade_host_copy``), where the reference makes one
+  tensor copy per unit (:258-268).
+* ``load_checkpoint`` parses safetensors headers and reads every tensor
+  straight into its arena bytes (``checkpoint.load_into``).
+* ``fill_random`` writes the seeded synthetic weights of the benchmark
+  configurations (there is no checkpoint on the GPU hosts).
+* ``tensor_factory`` stays injectable for tests, called as
+  ``factory(elements, dtype=torch.bfloat16, device="cpu", pin_memory=...)``.
 """
 
-import json
-from concurrent.futures import Future, ThreadPoolExecutor
+from concurrent.futures import Future
 from enum import Enum
-from pathlib import Path
+import queue
 import threading
 import time
 
 import torch
 
 from . import _hip
+from . import checkpoint as _checkpoint
 from .plan import ModelPlan
 
 __all__ = [
@@ -39,6 +41,7 @@ __all__ = [
     "BaseWeightStore",
     "FullPinnedWeightStore",
     "PinnedStagingWeightStore",
+    "StagingRing",
     "create_weight_store",
     "tensor_seed",
 ]
@@ -49,42 +52,43 @@ class WeightStoreMode(str, Enum):
     PINNED_STAGING = "pinned_staging"
 
 
-def _checkpoint_files(checkpoint):
-    """key -> file map of a sharded checkpoint, or None for a single file."""
-
-    root = Path(checkpoint)
-    index = root / "model.safetensors.index.json"
-    if index.exists():
-        with index.open("r", encoding="utf-8") as handle:
-            weight_map = json.load(handle).get("weight_map")
-        if not isinstance(weight_map, dict):
-            raise ValueError("{} has no weight_map".format(index))
-        return {key: root / name for key, name in weight_map.items()}
-    if (root / "model.safetensors").exists():
-        return None
-    raise FileNotFoundError(
-        "expected model.safetensors or model.safetensors.index.json in "
-        "{}".format(root)
-    )
-
-
 def tensor_seed(base_seed, tensor_index):
     """Seed of one tensor in the synthetic weights: base*1000 + index."""
 
     return int(base_seed) * 1000 + int(tensor_index)
 
 
+def _layout_table(plan):
+    """key -> (first element, element count, shape) for every tensor key and
+    alias of ``plan``, each alias resolved to the tensor that owns the
+    bytes."""
+
+    table = {}
+    for key, spec in plan.tensors.items():
+        owner = spec
+        while owner.alias_of is not None:
+            owner = plan.tensors[owner.alias_of]
+        table[key] = (plan.tensor_host_offset(owner.key), owner.numel,
+                      tuple(owner.shape))
+    for alias, target in plan.aliases.items():
+        table[alias] = table[target]
+    return table
+
+
 class BaseWeightStore:
-    """Packed CPU arena shared by both memory modes."""
+    """The packed host arena of a plan; subclasses decide whether it is
+    page-locked and how a unit reaches a pinned source for its copy."""
 
     def __init__(self, plan, pin_full_arena, allocate=True, tensor_factory=None):
         if not isinstance(plan, ModelPlan):
-            raise TypeError("plan must be a ModelPlan")
+            raise TypeError("expected a ModelPlan, got {}".format(
+                type(plan).__name__))
         self.plan = plan
         self.pin_full_arena = bool(pin_full_arena)
         self.tensor_factory = tensor_factory or torch.empty
         self.arena = None
         self._loaded = False
+        self._layout = _layout_table(plan)
         if allocate:
             self.allocate()
 
@@ -104,88 +108,42 @@ class BaseWeightStore:
     def loaded(self):
         return self._loaded
 
+    def _host_buffer(self, elements, pinned):
+        return self.tensor_factory(elements, dtype=torch.bfloat16, device="cpu",
+                                   pin_memory=bool(pinned))
+
     def allocate(self):
         if self.arena is None:
-            self.arena = self.tensor_factory(
-                self.plan.host_arena_elements,
-                dtype=torch.bfloat16,
-                device="cpu",
-                pin_memory=self.pin_full_arena,
-            )
+            self.arena = self._host_buffer(self.plan.host_arena_elements,
+                                           self.pin_full_arena)
         return self.arena
 
-    def _require_arena(self):
+    def _allocated_arena(self):
         if self.arena is None:
-            raise RuntimeError("weight arena has not been allocated")
+            raise RuntimeError("the host arena is not allocated (allocate() "
+                               "first)")
         return self.arena
-
-    def _view(self, key):
-        spec = self.plan.tensors[key]
-        if spec.alias_of is not None:
-            return self._view(spec.alias_of)
-        start = self.plan.tensor_host_offset(key)
-        return self._require_arena()[start : start + spec.numel].view(spec.shape)
 
     def tensor(self, key):
-        self._require_arena()
-        return self._view(self.plan.aliases.get(key, key))
+        arena = self._allocated_arena()
+        first, count, shape = self._layout[key]
+        return arena[first:first + count].view(shape)
 
     def unit_source(self, unit, slot_index=None):
-        arena = self._require_arena()
-        start = unit.host_offset_elements
-        return arena[start : start + unit.elements]
+        first = unit.host_offset_elements
+        return self._allocated_arena()[first:first + unit.elements]
 
     def required_keys(self):
-        return sorted(
-            key for key, spec in self.plan.tensors.items()
-            if spec.alias_of is None
-        )
+        """Keys a checkpoint must provide (aliases share their target)."""
+
+        return sorted(key for key, spec in self.plan.tensors.items()
+                      if spec.alias_of is None)
 
     def load_checkpoint(self, checkpoint):
         """Load a local safetensors checkpoint into the packed CPU arena."""
 
         self.allocate()
-        try:
-            from safetensors import safe_open
-        except ImportError as error:
-            raise RuntimeError(
-                "safetensors is required to load a checkpoint"
-            ) from error
-        weight_map = _checkpoint_files(checkpoint)
-        required = set(self.required_keys())
-        if weight_map is None:
-            files = [Path(checkpoint) / "model.safetensors"]
-        else:
-            missing = required.difference(weight_map)
-            if missing:
-                raise KeyError(
-                    "checkpoint index misses required tensors: {}".format(
-                        ", ".join(sorted(missing)[:8])
-                    )
-                )
-            files = sorted({weight_map[key] for key in required})
-        loaded = set()
-        with torch.inference_mode():
-            for filename in files:
-                with safe_open(str(filename), framework="pt", device="cpu") as src:
-                    for key in sorted(required.intersection(src.keys())):
-                        value = src.get_tensor(key)
-                        target = self._view(key)
-                        if tuple(value.shape) != tuple(target.shape):
-                            raise ValueError(
-                                "{} shape {} != expected {}".format(
-                                    key, tuple(value.shape), tuple(target.shape)
-                                )
-                            )
-                        target.copy_(value.to(dtype=torch.bfloat16))
-                        loaded.add(key)
-        missing = required.difference(loaded)
-        if missing:
-            raise KeyError(
-                "checkpoint misses required tensors: {}".format(
-                    ", ".join(sorted(missing)[:8])
-                )
-            )
+        _checkpoint.load_into(self, checkpoint)
         self._loaded = True
         return self
 
@@ -201,42 +159,29 @@ class BaseWeightStore:
         """
 
         self.allocate()
-        gen_device = torch.device(device) if device is not None else None
+        draw_on = torch.device(device) if device is not None else torch.device("cpu")
         with torch.inference_mode():
             for index, (key, spec) in enumerate(self.plan.tensors.items()):
                 if spec.alias_of is not None:
                     continue
-                target = self._view(key)
+                target = self.tensor(key)
                 is_norm = len(spec.shape) == 1
                 if is_norm and norm == "ones":
                     target.fill_(1.0)
                     continue
-                generator = torch.Generator(
-                    device=gen_device if gen_device is not None else "cpu"
-                )
+                generator = torch.Generator(device=draw_on)
                 generator.manual_seed(tensor_seed(seed, index))
-                scale = 0.1 if is_norm else float(std)
-                self._fill_normal(target, generator, gen_device, scale,
-                                  1.0 if is_norm else 0.0)
+                scale, shift = (0.1, 1.0) if is_norm else (float(std), 0.0)
+                flat = target.view(-1)
+                # bounded pieces: 16 GB of weights never needs an fp32 copy
+                step = 1 << 26
+                for first in range(0, flat.numel(), step):
+                    piece = flat[first:first + step]
+                    values = torch.randn(piece.numel(), generator=generator,
+                                         dtype=torch.float32, device=draw_on)
+                    piece.copy_(values.mul_(scale).add_(shift).to(torch.bfloat16))
         self._loaded = True
         return self
-
-    @staticmethod
-    def _fill_normal(target, generator, gen_device, scale, shift):
-        flat = target.view(-1)
-        # Draw in bounded pieces so 16 GB of weights never needs a full fp32
-        # copy in memory.
-        step = 1 << 26
-        for start in range(0, flat.numel(), step):
-            piece = flat[start : start + step]
-            values = torch.randn(
-                piece.numel(),
-                generator=generator,
-                dtype=torch.float32,
-                device=gen_device if gen_device is not None else "cpu",
-            )
-            values.mul_(scale).add_(shift)
-            piece.copy_(values.to(torch.bfloat16))
 
     def close(self):
         self.arena = None
@@ -252,22 +197,21 @@ class BaseWeightStore:
 class FullPinnedWeightStore(BaseWeightStore):
     """All checkpoint weights remain in page-locked CPU memory."""
 
+    mode = WeightStoreMode.FULL_PINNED
+
     def __init__(self, plan, allocate=True, tensor_factory=None):
         super().__init__(plan, True, allocate=allocate,
                          tensor_factory=tensor_factory)
-
-    @property
-    def mode(self):
-        return WeightStoreMode.FULL_PINNED
 
     @property
     def pinned_cpu_bytes(self):
         return self.plan.host_arena_bytes
 
     def prepare_unit(self, unit, slot_index, reuse_event=None):
-        future = Future()
-        future.set_result(self.unit_source(unit))
-        return future
+        # the arena itself is the pinned source: nothing to stage or wait for
+        done = Future()
+        done.set_result(self.unit_source(unit))
+        return done
 
 
 class StagingRing:
@@ -333,112 +277,160 @@ class StagingRing:
         raise KeyError(key)
 
 
+def _staging_summary(durations_ms):
+    """The reference's staging profile keys (weight_store.py:285-298)."""
+
+    return {
+        "staging_copy_count": len(durations_ms),
+        "staging_event_sum_ms": sum(durations_ms),
+        "staging_event_max_ms": max(durations_ms) if durations_ms else 0.0,
+    }
+
+
+class _Stager:
+    """Pinned staging buffers, their byte ring and the threads that fill
+    them.  A job names a source, a buffer, a byte offset and the events of
+    the copies that last read those bytes; a worker waits for the events,
+    copies, and resolves the job's future with the pinned view."""
+
+    def __init__(self, buffers, workers, copy_threads):
+        self.buffers = buffers
+        self.ring = StagingRing(buffers)
+        self.copy_threads = copy_threads
+        self._jobs = queue.SimpleQueue()
+        self._lock = threading.Lock()
+        self._durations_ms = []
+        self._threads = [
+            threading.Thread(target=self._serve, name="weight-stage-{}".format(i),
+                             daemon=True)
+            for i in range(max(1, int(workers)))
+        ]
+        for thread in self._threads:
+            thread.start()
+
+    def submit(self, source, buffer_index, byte_start, waits):
+        result = Future()
+        self._jobs.put((result, source, buffer_index, byte_start, tuple(waits)))
+        return result
+
+    def _serve(self):
+        while True:
+            job = self._jobs.get()
+            if job is None:
+                return
+            result, source, buffer_index, byte_start, waits = job
+            if not result.set_running_or_notify_cancel():
+                continue
+            try:
+                result.set_result(self._stage(source, buffer_index, byte_start,
+                                              waits))
+            except BaseException as error:  # handed to the waiting runtime
+                result.set_exception(error)
+
+    def _stage(self, source, buffer_index, byte_start, waits):
+        started = time.perf_counter()
+        for event in waits:
+            event.synchronize()  # the copies that read these bytes are done
+        buffer = self.buffers[buffer_index]
+        first = byte_start // buffer.element_size()
+        target = buffer[first:first + source.numel()]
+        _hip.host_copy(target, source, self.copy_threads)
+        with self._lock:
+            self._durations_ms.append((time.perf_counter() - started) * 1000.0)
+        return target
+
+    def stats(self, reset=False):
+        with self._lock:
+            durations = self._durations_ms
+            if reset:
+                self._durations_ms = []
+        return _staging_summary(durations)
+
+    def close(self):
+        for _ in self._threads:
+            self._jobs.put(None)
+        for thread in self._threads:
+            thread.join()
+
+
 class PinnedStagingWeightStore(BaseWeightStore):
     """Pageable full store plus reusable page-locked staging slots."""
 
+    mode = WeightStoreMode.PINNED_STAGING
+
     def __init__(self, plan, allocate=True, tensor_factory=None, worker_count=2,
                  copy_threads=None):
-        self.staging_slots = None
-        self.staging_ring = None
         self.worker_count = int(worker_count)
         self.copy_threads = int(copy_threads or _hip.default_copy_threads())
-        self._executor = None
-        self._profile_lock = threading.Lock()
-        self._stage_durations_ms = []
+        self._stager = None
         super().__init__(plan, False, allocate=allocate,
                          tensor_factory=tensor_factory)
-
-    @property
-    def mode(self):
-        return WeightStoreMode.PINNED_STAGING
 
     @property
     def pinned_cpu_bytes(self):
         return self.plan.two_slot_bytes
 
+    @property
+    def staging_slots(self):
+        return None if self._stager is None else self._stager.buffers
+
+    @property
+    def staging_ring(self):
+        return None if self._stager is None else self._stager.ring
+
     def allocate(self):
         arena = super().allocate()
-        if self.staging_slots is None:
-            self.staging_slots = [
-                self.tensor_factory(
-                    self.plan.slot_elements,
-                    dtype=torch.bfloat16,
-                    device="cpu",
-                    pin_memory=True,
-                )
-                for _ in range(self.plan.slot_count)
-            ]
-            self.staging_ring = StagingRing(self.staging_slots)
-        if self._executor is None:
-            self._executor = ThreadPoolExecutor(
-                max_workers=self.worker_count, thread_name_prefix="weight-stage"
-            )
+        if self._stager is None:
+            buffers = [self._host_buffer(self.plan.slot_elements, True)
+                       for _ in range(self.plan.slot_count)]
+            self._stager = _Stager(buffers, self.worker_count, self.copy_threads)
         return arena
 
-    def _stage(self, unit, slot_index, reuse_event):
-        started = time.perf_counter()
-        if reuse_event is not None:
-            # The slot is free once the H2D copy that last read it is done.
-            reuse_event.synchronize()
-        target = self.staging_slots[slot_index][: unit.elements]
-        _hip.host_copy(target, self.unit_source(unit), self.copy_threads)
-        elapsed = (time.perf_counter() - started) * 1000.0
-        with self._profile_lock:
-            self._stage_durations_ms.append(elapsed)
-        return target
+    def _running_stager(self):
+        if self._stager is None:
+            raise RuntimeError("the staging slots are not allocated (allocate() "
+                               "first)")
+        return self._stager
 
     def prepare_unit(self, unit, slot_index, reuse_event=None):
-        if self.staging_slots is None or self._executor is None:
-            raise RuntimeError("staging store has not been allocated")
-        return self._executor.submit(self._stage, unit, slot_index, reuse_event)
+        """Stage ``unit`` at the start of pinned slot ``slot_index`` once
+        ``reuse_event`` (the copy that last read the slot) is done."""
 
-    def _stage_at(self, unit, slot_index, start, waits):
-        started = time.perf_counter()
-        for event in waits:
-            event.synchronize()
-        slot = self.staging_slots[slot_index]
-        first = start // slot.element_size()
-        target = slot[first:first + unit.elements]
-        _hip.host_copy(target, self.unit_source(unit), self.copy_threads)
-        elapsed = (time.perf_counter() - started) * 1000.0
-        with self._profile_lock:
-            self._stage_durations_ms.append(elapsed)
-        return target
+        waits = () if reuse_event is None else (reuse_event,)
+        return self._running_stager().submit(self.unit_source(unit), slot_index,
+                                             0, waits)
 
     def stage_in_ring(self, unit, slot_index, start, waits):
         """Stage ``unit`` at byte ``start`` of staging slot ``slot_index``
         once ``waits`` (the copies that last read those bytes) are done;
         returns a future of the pinned source view."""
 
-        if self._executor is None:
-            raise RuntimeError("staging store has not been allocated")
-        return self._executor.submit(self._stage_at, unit, slot_index, start, waits)
+        return self._running_stager().submit(self.unit_source(unit), slot_index,
+                                             start, waits)
 
     def close(self):
-        if self._executor is not None:
-            self._executor.shutdown(wait=True)
-            self._executor = None
-        self.staging_slots = None
+        if self._stager is not None:
+            self._stager.close()
+            self._stager = None
         super().close()
 
     def reset_profile(self):
-        with self._profile_lock:
-            self._stage_durations_ms = []
+        if self._stager is not None:
+            self._stager.stats(reset=True)
 
     def profile_stats(self):
-        with self._profile_lock:
-            durations = list(self._stage_durations_ms)
-        return {
-            "staging_copy_count": len(durations),
-            "staging_event_sum_ms": sum(durations),
-            "staging_event_max_ms": max(durations) if durations else 0.0,
-        }
+        if self._stager is None:
+            return _staging_summary(())
+        return self._stager.stats()
+
+
+_STORE_CLASSES = {
+    WeightStoreMode.FULL_PINNED: FullPinnedWeightStore,
+    WeightStoreMode.PINNED_STAGING: PinnedStagingWeightStore,
+}
 
 
 def create_weight_store(plan, mode=WeightStoreMode.FULL_PINNED, allocate=True,
                         tensor_factory=None):
-    if WeightStoreMode(mode) == WeightStoreMode.FULL_PINNED:
-        return FullPinnedWeightStore(plan, allocate=allocate,
-                                     tensor_factory=tensor_factory)
-    return PinnedStagingWeightStore(plan, allocate=allocate,
-                                    tensor_factory=tensor_factory)
+    return _STORE_CLASSES[WeightStoreMode(mode)](plan, allocate=allocate,
+                                                 tensor_factory=tensor_factory)
