@@ -60,14 +60,27 @@ __global__ __launch_bounds__(kGatherThreads) void decode_step_begin_kernel(
 
 constexpr int kStreamThreads = 256;
 
+// Streaming read for the achievable-bandwidth measurement: each thread keeps
+// kReadUnroll nontemporal 16-byte loads in flight per step, the grid walks
+// the buffer in strides of its whole width.
+constexpr int kReadUnroll = 4;
+
 __global__ __launch_bounds__(kStreamThreads) void hbm_read_kernel(
     const u32x4 *src, int64_t nvec, float *sink) {
   float s = 0.0f;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kStreamThreads;
-  for (int64_t j = static_cast<int64_t>(blockIdx.x) * kStreamThreads +
-                   threadIdx.x;
-       j < nvec; j += stride) {
-    const u32x4 v = src[j];
+  int64_t j = static_cast<int64_t>(blockIdx.x) * kStreamThreads + threadIdx.x;
+  for (; j + (kReadUnroll - 1) * stride < nvec; j += kReadUnroll * stride) {
+    u32x4 v[kReadUnroll];
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u)
+      v[u] = __builtin_nontemporal_load(src + j + u * stride);
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u)
+      s += __uint_as_float(v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
+  }
+  for (; j < nvec; j += stride) {
+    const u32x4 v = __builtin_nontemporal_load(src + j);
     s += __uint_as_float(v.x ^ v.y ^ v.z ^ v.w);
   }
   // Data-dependent store so the loads cannot be removed; never taken for
@@ -239,11 +252,14 @@ extern "C" int cascade_time_next_launch(uint64_t start_event,
 }
 
 extern "C" int cascade_hbm_read(const void *src, size_t bytes, float *sink,
-                                void *stream) {
+                                int64_t blocks, void *stream) {
   if (src == nullptr || sink == nullptr || bytes == 0) return CASCADE_EINVAL;
   if ((bytes & 15) || !aligned16(src)) return CASCADE_EALIGN;
+  if (blocks < 0 || blocks > (int64_t{1} << 20)) return CASCADE_EINVAL;
   const int64_t nvec = static_cast<int64_t>(bytes >> 4);
-  return launch_kernel(hbm_read_kernel, dim3(stream_blocks(nvec)),
+  return launch_kernel(hbm_read_kernel,
+                       dim3(blocks ? static_cast<unsigned>(blocks)
+                                   : stream_blocks(nvec)),
                        dim3(kStreamThreads), 0,
                        static_cast<hipStream_t>(stream),
                        static_cast<const u32x4 *>(src), nvec, sink);

@@ -69,14 +69,6 @@ _SIGNATURES = {
     ),
     "cascade_decode_attention_noalloc_bf16": (
         _INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P]),
-    "cascade_decode_layer_workspace_bytes": (_SZ, []),
-    "cascade_decode_layer_bf16": (
-        _INT,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _I64,
-         _I64, _F, _P, _SZ, _P],
-    ),
-    "cascade_decode_mlp_bf16": (
-        _INT, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
     "cascade_gemm_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "cascade_gemm_residual_bf16": (
         _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
@@ -112,7 +104,7 @@ _SIGNATURES = {
     "cascade_event_query": (_INT, [_U64]),
     "cascade_event_elapsed_ms": (_INT, [_U64, _U64, ctypes.POINTER(_F)]),
     "cascade_host_copy": (_INT, [_P, _P, _SZ, _INT]),
-    "cascade_hbm_read": (_INT, [_P, _SZ, _P, _P]),
+    "cascade_hbm_read": (_INT, [_P, _SZ, _P, _I64, _P]),
     "cascade_device_copy": (_INT, [_P, _P, _SZ, _P]),
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
 }
@@ -689,95 +681,6 @@ def decode_step_begin(table, ids, out, length, history, error_flag=None,
     return out
 
 
-# Byte offsets inside the decode-layer workspace (include/cascade_hip.h).
-DECODE_LAYER_Q = 1024
-DECODE_LAYER_ATTN = 9216
-DECODE_LAYER_INTER = 17408
-DECODE_LAYER_ERROR = 640
-DECODE_LAYER_SHAPE = {"hidden": 4096, "intermediate": 14336, "n_heads": 32,
-                      "n_kv_heads": 8, "head_dim": 128}
-
-
-def decode_layer_workspace_bytes():
-    return int(load().cascade_decode_layer_workspace_bytes())
-
-
-def decode_layer(w, x, rope_cos, rope_sin, k_cache, v_cache, kv_head_stride,
-                 length, workspace, eps, scale, stream=None):
-    """One whole decoder layer of batch-1 decode (Llama-3.1-8B shape) in one
-    launch; x [4096] bf16 is updated in place, the new token's K / V go to
-    slot length - 1.  ``w`` maps q, k, v, o, gate, up, down (bf16 [rows, K])
-    and ln1, ln2 (bf16 [4096]).  k_cache / v_cache are views starting at
-    position 0 of KV head 0.  Returns the library status (0, or
-    CASCADE_ESHAPE where the device cannot run the kernel); raises on any
-    other failure."""
-
-    shape = DECODE_LAYER_SHAPE
-    h, i = shape["hidden"], shape["intermediate"]
-    kv = shape["n_kv_heads"] * shape["head_dim"]
-    for name, rows, k in (("q", h, h), ("k", kv, h), ("v", kv, h), ("o", h, h),
-                          ("gate", i, h), ("up", i, h), ("down", h, i)):
-        _bf16(w[name], name, rows * k)
-        if tuple(w[name].shape) != (rows, k):
-            raise ValueError("{} must be [{}, {}]".format(name, rows, k))
-    for name in ("ln1", "ln2"):
-        _bf16(w[name], name, h)
-    _bf16(x, "x", h)
-    _bf16(rope_cos, "rope_cos", shape["head_dim"] // 2)
-    _bf16(rope_sin, "rope_sin", shape["head_dim"] // 2)
-    for name, buf in (("k_cache", k_cache), ("v_cache", v_cache)):
-        require_device(buf, name, torch.bfloat16, contiguous=False)
-        end = buf.storage_offset() + (shape["n_kv_heads"] - 1) * kv_head_stride + (
-            length * shape["head_dim"])
-        if end > buf.untyped_storage().nbytes() // 2:
-            raise ValueError("{} is too small for length {}".format(name, length))
-    require_device(workspace, "workspace", torch.uint8)
-    code = load().cascade_decode_layer_bf16(
-        w["q"].data_ptr(), w["k"].data_ptr(), w["v"].data_ptr(),
-        w["o"].data_ptr(), w["gate"].data_ptr(), w["up"].data_ptr(),
-        w["down"].data_ptr(), w["ln1"].data_ptr(), w["ln2"].data_ptr(),
-        float(eps), x.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
-        k_cache.data_ptr(), v_cache.data_ptr(), int(kv_head_stride),
-        int(length), float(scale), workspace.data_ptr(), workspace.numel(),
-        stream_handle(stream))
-    if code not in (0, ESHAPE):
-        _check("cascade_decode_layer_bf16", code)
-    return code
-
-
-def decode_mlp(w, attn, x, workspace, eps, stream=None):
-    """o_proj + residual, RMSNorm + gate/up + SwiGLU, down_proj + residual
-    of one token in one launch; x [4096] bf16 updated in place.  ``w`` maps
-    o, gate, up, down and ln2.  Returns the library status (0, or
-    CASCADE_ESHAPE where the device cannot run the kernel)."""
-
-    shape = DECODE_LAYER_SHAPE
-    h, i = shape["hidden"], shape["intermediate"]
-    for name, rows, k in (("o", h, h), ("gate", i, h), ("up", i, h), ("down", h, i)):
-        _bf16(w[name], name, rows * k)
-        if tuple(w[name].shape) != (rows, k):
-            raise ValueError("{} must be [{}, {}]".format(name, rows, k))
-    _bf16(w["ln2"], "ln2", h)
-    _bf16(attn, "attn", h)
-    _bf16(x, "x", h)
-    require_device(workspace, "workspace", torch.uint8)
-    code = load().cascade_decode_mlp_bf16(
-        w["o"].data_ptr(), w["gate"].data_ptr(), w["up"].data_ptr(),
-        w["down"].data_ptr(), w["ln2"].data_ptr(), float(eps), attn.data_ptr(),
-        x.data_ptr(), workspace.data_ptr(), workspace.numel(),
-        stream_handle(stream))
-    if code not in (0, ESHAPE):
-        _check("cascade_decode_mlp_bf16", code)
-    return code
-
-
-def decode_layer_error(workspace):
-    """The barrier error word of a decode-layer workspace (synchronises)."""
-
-    word = workspace[DECODE_LAYER_ERROR:DECODE_LAYER_ERROR + 4].cpu()
-    return int(word.view(torch.int32)[0])
-
-
 def lm_head_workspace_bytes(rows, top_k):
     size = load().cascade_lm_head_workspace_bytes(int(rows), int(top_k))
     if size == 0:
@@ -816,11 +719,11 @@ def embedding_gather(table, ids, out, error_flag=None, stream=None):
     return out
 
 
-def hbm_read(src, sink, stream=None):
+def hbm_read(src, sink, blocks=0, stream=None):
     require_device(src, "src")
     require_device(sink, "sink", torch.float32, 1)
     call("cascade_hbm_read", src.data_ptr(),
-         src.numel() * src.element_size(), sink.data_ptr(),
+         src.numel() * src.element_size(), sink.data_ptr(), int(blocks),
          stream_handle(stream))
 
 

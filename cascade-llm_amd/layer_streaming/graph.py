@@ -79,8 +79,6 @@ class DecodeGraph:
             raise TypeError("DecodeGraph needs a ResidentTransformerRuntime")
         if executor.vocab_runtime is not None:
             raise ValueError("DecodeGraph needs the resident LM head")
-        if executor.layer_mode != "stages":
-            raise ValueError("DecodeGraph needs layer_mode='stages'")
         if executor._device_step is not None:
             raise RuntimeError("the executor already runs a DecodeGraph")
         if executor.capture is not None:
@@ -89,6 +87,8 @@ class DecodeGraph:
             raise ValueError("DecodeGraph needs executor.capture = None")
         if int(max_new_tokens) < 2:
             raise ValueError("max_new_tokens must be at least 2")
+        # a bad id in the eager steps before raises here, not in the graph
+        executor.check_errors()
         self.executor = executor
         self.runtime = runtime
         self.device = executor.device

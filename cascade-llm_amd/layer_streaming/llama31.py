@@ -200,11 +200,50 @@ _EXPECTED = {
 # Kernel groups whose entry point launches exactly one kernel.
 _KERNEL_TIMED_GROUPS = frozenset((
     "gate_up", "qkv", "o_proj", "down_proj",
-    # one-launch decoder layer and its MLP half
-    "layer", "mlp",
     # prefill (S > 1 tokens): one MFMA GEMM / attention launch per unit
     "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_gate", "gemm_up", "gemm_down",
     "gemm_lm_head", "prefill_attention"))
+
+
+def _check_ids(ids, vocab):
+    if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= vocab):
+        raise IndexError("token id outside [0, {})".format(vocab))
+
+
+class _ErrorWord:
+    """An int32 device flag that kernels set on bad input, read back without
+    blocking: ``publish`` copies it to pinned memory behind the step's work,
+    ``raise_if_set`` raises once that copy has landed (or waits for it)."""
+
+    def __init__(self, device, message):
+        self.message = message
+        self.flag = torch.zeros(1, dtype=torch.int32, device=device)
+        self.host = torch.zeros(1, dtype=torch.int32,
+                                pin_memory=device.type == "cuda")
+        self.event = _hip.HipEvent() if device.type == "cuda" else None
+        self.pending = False
+
+    def publish(self):
+        """Copy the flag to the host behind the current stream's work."""
+
+        self.host.copy_(self.flag, non_blocking=True)
+        if self.event is not None:
+            self.event.record()
+        self.pending = True
+
+    def raise_if_set(self, block=False):
+        if not self.pending:
+            return
+        if self.event is not None:
+            if block:
+                self.event.synchronize()
+            elif not self.event.query():
+                return
+        self.pending = False
+        if int(self.host[0]) != 0:
+            self.flag.zero_()
+            self.host.zero_()
+            raise IndexError(self.message)
 
 
 class Llama31DecodeExecutor:
@@ -212,7 +251,7 @@ class Llama31DecodeExecutor:
     multi-token prefill, then one-token decode calls)."""
 
     def __init__(self, config, resident, kv_cache=None, vocab_runtime=None,
-                 top_k=10, return_full_logits=False, layer_mode="stages"):
+                 top_k=10, return_full_logits=False):
         _hip.load()  # no kernels, no executor
         layers = getattr(resident, "plan", None)
         layers = layers.num_layers if layers is not None else 32
@@ -276,8 +315,6 @@ class Llama31DecodeExecutor:
         self._k_silu_gemm = lib.cascade_gate_silu_gemm_bf16
         self._k_mul_gemm = lib.cascade_up_mul_gemm_bf16
         self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
-        self._k_layer = lib.cascade_decode_layer_bf16
-        self._k_mlp = lib.cascade_decode_mlp_bf16
         self._k_qkv_at = lib.cascade_qkv_rope_at_bf16
         self._k_attn_at = lib.cascade_decode_attention_at_bf16
         self._k_step_begin = lib.cascade_decode_step_begin_bf16
@@ -296,18 +333,8 @@ class Llama31DecodeExecutor:
         self._attn_ws = None
         self._attn_ws_len = 0
         self._head_ws = None
-        # Launches of a single-token "layer" unit (decode): "stages" = the
-        # per-stage kernels (six launches); "mlp" = q|k|v and attention per
-        # stage, o_proj .. down_proj in one launch (four); "one" = the whole
-        # layer in one launch.  _fused_ok: None until the first fused launch,
-        # then True, or False where the device cannot run those kernels
-        # (the per-stage kernels run from then on).
-        if layer_mode not in ("stages", "mlp", "one"):
-            raise ValueError("layer_mode must be stages, mlp or one")
-        self.layer_mode = layer_mode
-        self._fused_ok = None
-        self._layer_ws = None
-        self._layer_err = None
+        self._id_errors = _ErrorWord(self.device, "token id outside [0, {})".format(
+            config.vocab_size))
         self._ensure_buffers(1)
 
     # ------------------------------------------------------------ buffers
@@ -378,15 +405,24 @@ class Llama31DecodeExecutor:
         self.rope.reserve(max(positions) + 1)
         self._ensure_buffers(sequence)
         if self.vocab_runtime is None:
+            if self._device_step is None:
+                self._id_errors.raise_if_set()
             hidden = torch.empty((1, sequence, self.hidden),
                                  dtype=torch.bfloat16, device=self.device)
             ids = input_ids.reshape(-1)
+            table = self.resident["model.embed_tokens.weight"]
+            if ids.device.type == "cpu" or sequence > 1:
+                # ids the host has (or a prompt, read back once): checked
+                # here, as F.embedding raises on them
+                _check_ids(ids.to("cpu"), table.shape[0])
             if ids.device != self.device or ids.dtype != torch.long:
                 ids = ids.to(device=self.device, dtype=torch.long)
-            table = self.resident["model.embed_tokens.weight"]
             step = self._device_step
             if step is None:
-                _hip.embedding_gather(table, ids, hidden)
+                # a device-held id (the previous step's top-1) is checked by
+                # the gather kernel, which flags it; finish() publishes the
+                # flag and the next begin() / finish() raises
+                _hip.embedding_gather(table, ids, hidden, self._id_errors.flag)
             else:
                 if sequence != 1:
                     raise ValueError("a device-position step decodes one token")
@@ -526,90 +562,11 @@ class Llama31DecodeExecutor:
         self._mark_end("o_proj", ev, rc)
         _hip.check("cascade_gemv_residual_bf16", rc)
 
-    def _layer_fused(self, layer, ptrs, state, stream):
-        """A single-token layer unit through the one-launch kernels --
-        layer_mode "one": the whole layer in one launch
-        (cascade_decode_layer_bf16); "mlp": q|k|v and attention per stage,
-        then o_proj .. down_proj in one launch (cascade_decode_mlp_bf16).
-        False when they do not apply; the per-stage kernels run instead."""
-
-        if (self.layer_mode == "stages" or self._fused_ok is False
-                or len(state.positions) != 1):
-            return False
-        names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
-                 "down_proj")
-        if any(n not in ptrs for n in names):
-            return False
-        if self._layer_ws is None:
-            self._layer_ws = torch.zeros(_hip.decode_layer_workspace_bytes(),
-                                         dtype=torch.uint8, device=self.device)
-        ws = self._layer_ws
-        x = state.hidden_states.data_ptr()
-        norm_in, norm_post = self._norm_ptrs[layer]
-        if self.layer_mode == "one":
-            slot = self._first_slot
-            pos = state.positions[0]
-            half = self.head_dim // 2
-            ev = self._mark_begin("layer")
-            rc = self._k_layer(
-                *(ptrs[n] for n in names), norm_in, norm_post, self.eps, x,
-                self.rope.cos.data_ptr() + 2 * half * pos,
-                self.rope.sin.data_ptr() + 2 * half * pos,
-                self._kv_pointer(layer, 0, 0), self._kv_pointer(layer, 1, 0),
-                self.kv_cache.head_stride, slot + 1, self.scale, ws.data_ptr(),
-                ws.numel(), stream)
-            self._mark_end("layer", ev, rc)
-            if rc == _hip.ESHAPE and self._fused_ok is None:
-                self._fused_ok = False
-                return False
-            _hip.check("cascade_decode_layer_bf16", rc)
-            self.kv_cache.set_length(layer, slot + 1)
-        else:
-            self._qkv(layer, ptrs, state, stream)
-            self._attention_o(layer, ptrs, state, stream, with_o=False)
-            ev = self._mark_begin("mlp")
-            rc = self._k_mlp(ptrs["o_proj"], ptrs["gate_proj"], ptrs["up_proj"],
-                             ptrs["down_proj"], norm_post, self.eps, self._attn_ptr,
-                             x, ws.data_ptr(), ws.numel(), stream)
-            self._mark_end("mlp", ev, rc)
-            if rc == _hip.ESHAPE and self._fused_ok is None:
-                # the device cannot run it: finish this layer per stage
-                self._fused_ok = False
-                self._o_residual(ptrs, state, 0, stream)
-                self._gate_up(layer, ptrs, state, stream)
-                self._down(layer, ptrs, state, stream)
-                return True
-            _hip.check("cascade_decode_mlp_bf16", rc)
-        self._fused_ok = True
-        if self.capture is not None:
-            self.capture.append((layer, state.hidden_states.detach().clone()))
-        return True
-
-    def _check_layer_errors(self):
-        """Surface a grid-barrier timeout of the one-launch layer.  Non-
-        blocking: the error word is copied to pinned memory behind each
-        token's work and read one token later, once its event completed."""
-
-        if self._layer_ws is None or self._layer_ws.device.type != "cuda":
-            return
-        if self._layer_err is None:
-            self._layer_err = (torch.zeros(1, dtype=torch.int32, pin_memory=True),
-                               torch.cuda.Event())
-        host, event = self._layer_err
-        if event.query() and int(host[0]) != 0:
-            self._layer_ws.zero_()
-            host.zero_()
-            raise RuntimeError(
-                "cascade_decode_layer_bf16 / cascade_decode_mlp_bf16: a grid "
-                "barrier timed out (not all workgroups resident); the results "
-                "of the last tokens are invalid")
-        word = _hip.DECODE_LAYER_ERROR
-        host.copy_(self._layer_ws[word:word + 4].view(torch.int32), non_blocking=True)
-        event.record()
-
     def instrument(self, name, launches, stride=1, offset=0):
-        """Time ``launches`` launches of kernel group ``name`` ("layer", "mlp",
-        "gate_up", "qkv", "attention", "o_proj", "down_proj", "lm_head"): of the group's
+        """Time ``launches`` launches of kernel group ``name`` ("gate_up",
+        "qkv", "attention", "o_proj", "down_proj", "lm_head"; at prefill
+        "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_gate", "gemm_up",
+        "gemm_down", "gemm_lm_head", "prefill_attention"): of the group's
         coming launches, numbers offset, offset + stride, ...; read them back
         with :meth:`kernel_times_ms` after a synchronize.  The one-kernel
         groups (gate_up, qkv, o_proj, down_proj) bind the events to the
@@ -831,8 +788,6 @@ class Llama31DecodeExecutor:
         if self._batched:
             return self._call_batched(layer, op, ptrs, state, stream)
         if op == "layer":
-            if self._layer_fused(layer, ptrs, state, stream):
-                return state
             self._qkv(layer, ptrs, state, stream)
             self._attention_o(layer, ptrs, state, stream)
             self._gate_up(layer, ptrs, state, stream)
@@ -854,7 +809,6 @@ class Llama31DecodeExecutor:
         return state
 
     def finish(self, state):
-        self._check_layer_errors()
         rows = self._token_rows(state)
         count = rows.shape[0]
         stream = self._stream()
@@ -871,6 +825,9 @@ class Llama31DecodeExecutor:
             state.topk_indices = result["indices"]
             state.logits = result["logits"]
             return state
+        step = self._device_step
+        if step is None:
+            self._id_errors.raise_if_set()
         normed = self._normed[:count]
         _hip.check("cascade_rmsnorm_bf16", self._k_rmsnorm(
             rows.data_ptr(), final_norm.data_ptr(), normed.data_ptr(), count,
@@ -916,4 +873,12 @@ class Llama31DecodeExecutor:
         state.logits = logits
         state.topk_values = values
         state.topk_indices = indices
+        if step is None:
+            self._id_errors.publish()
         return state
+
+    def check_errors(self):
+        """Wait for the last step's error flags and raise if one is set
+        (begin() / finish() check them without waiting, one step late)."""
+
+        self._id_errors.raise_if_set(block=True)

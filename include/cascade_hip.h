@@ -183,64 +183,6 @@ int cascade_decode_attention_noalloc_bf16(const void *q, const void *k_cache,
                                           int64_t head_dim, float scale,
                                           void *out, void *stream);
 
-/* One whole decoder layer of batch-1 decode in one launch (Llama-3.1-8B
- * shape only: hidden 4096, 32 query / 8 KV heads of 128, intermediate
- * 14336), computing what the six calls above compute for a layer unit:
- *   n = RMSNorm(x, norm_in); q|k|v = RoPE(W . n); K / V of the new token
- *   -> slot len - 1 of the layer cache; attn = softmax(q K^T scale) V over
- *   positions [0, len); x += bf16(Wo . attn); n2 = RMSNorm(x, norm_post);
- *   inter = SwiGLU(Wg . n2, Wu . n2); x += bf16(Wd . inter).
- * x [4096] bf16 is updated in place.  rope_cos / rope_sin are the 64-entry
- * bf16 rows of this token's position.  k_cache / v_cache point at position
- * 0 of KV head 0 (layout as cascade_decode_attention_bf16), 1 <= len <= 2^23.
- * The GEMV rows round as the per-stage entry points do (bit for bit on the
- * same input); attention splits differ, so attn agrees to fp32 rounding.
- * One launch of 256 workgroups with grid barriers between the stages, so
- * all 256 must be resident at once: needs a 256-CU device that can hold one
- * per CU (CASCADE_ESHAPE otherwise; the caller then uses the per-stage
- * calls), and no other work holding CUs for long.  The workspace
- * (>= cascade_decode_layer_workspace_bytes(), zero-filled once by the
- * caller) carries the barrier state from call to call on one stream; calls
- * that overlap on one workspace race.  After a call it holds q at byte
- * CASCADE_DECODE_LAYER_Q, attn at CASCADE_DECODE_LAYER_ATTN and inter at
- * CASCADE_DECODE_LAYER_INTER (bf16).  A grid barrier that waits past its
- * bound (about 2 s: some workgroup never became resident) sets the uint32 at
- * byte CASCADE_DECODE_LAYER_ERROR to nonzero,
- * and the launch then drains with undefined results; read it at a
- * synchronisation point, and zero the workspace again before the next call.
- * Replaces, for op == "layer" units, llama31.py:169-279 (_start_attention,
- * _attention_output, _execute_matrix for q..down).                        */
-#define CASCADE_DECODE_LAYER_Q 1024
-#define CASCADE_DECODE_LAYER_ATTN 9216
-#define CASCADE_DECODE_LAYER_INTER 17408
-#define CASCADE_DECODE_LAYER_ERROR 640
-size_t cascade_decode_layer_workspace_bytes(void);
-int cascade_decode_layer_bf16(const void *wq, const void *wk, const void *wv,
-                              const void *wo, const void *w_gate,
-                              const void *w_up, const void *w_down,
-                              const void *norm_in, const void *norm_post,
-                              float eps, void *x, const void *rope_cos,
-                              const void *rope_sin, void *k_cache,
-                              void *v_cache, int64_t kv_head_stride,
-                              int64_t len, float scale, void *workspace,
-                              size_t workspace_bytes, void *stream);
-
-/* The MLP half of the same layer in one launch (stages o_proj .. down of
- * cascade_decode_layer_bf16), after the caller ran q|k|v and attention with
- * the per-stage calls:
- *   x += bf16(Wo . attn); n2 = RMSNorm(x, norm_post);
- *   inter = SwiGLU(Wg . n2, Wu . n2); x += bf16(Wd . inter)
- * attn [4096] bf16 (the attention output), x [4096] bf16 updated in place.
- * Same shape, device, workspace and error-word rules as
- * cascade_decode_layer_bf16 (one workspace may serve both); rounds as the
- * per-stage calls do, bit for bit.
- * Replaces llama31.py:246-279 (o_proj .. down_proj) for a layer unit.      */
-int cascade_decode_mlp_bf16(const void *wo, const void *w_gate,
-                            const void *w_up, const void *w_down,
-                            const void *norm_post, float eps, const void *attn,
-                            void *x, void *workspace, size_t workspace_bytes,
-                            void *stream);
-
 /* ------------------------------------------------------ prefill (M > 1)
  * MFMA GEMMs over the token rows of a prefill call: Y[M, N] =
  * epilogue(X[M, K] . W[N, K]^T), X row-major [M, K] (already normalised:
@@ -379,12 +321,15 @@ int cascade_event_elapsed_ms(uint64_t start, uint64_t end, float *ms);
 int cascade_host_copy(void *dst, const void *src, size_t bytes, int threads);
 
 /* ----------------------------------------------------------- measurement
- * Streaming-read kernel: sums `bytes` of device memory (16-byte loads) into
- * *sink; used to measure achievable HBM read bandwidth (no reference
- * counterpart; the reference measures only H2D, h2d_driver_bench.c).
+ * Streaming-read kernel: reads `bytes` of device memory (nontemporal 16-byte
+ * loads, four in flight per thread) and folds them into *sink; `blocks`
+ * workgroups of 256 threads (0: the library's default of up to 4096).  Used
+ * to measure achievable HBM read bandwidth (no reference counterpart; the
+ * reference measures only H2D, h2d_driver_bench.c).
  * Plain device copy of `bytes`: the calibration kernel for HBM traffic
  * counters.                                                                */
-int cascade_hbm_read(const void *src, size_t bytes, float *sink, void *stream);
+int cascade_hbm_read(const void *src, size_t bytes, float *sink,
+                     int64_t blocks, void *stream);
 int cascade_device_copy(void *dst, const void *src, size_t bytes, void *stream);
 
 /* Binds two timing events (either may be 0) to the calling thread's next

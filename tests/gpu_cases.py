@@ -103,83 +103,6 @@ def run_layer_case(seed, past, device="cuda:0"):
     return report
 
 
-def run_layer_fused_gpu(case, device="cuda:0", capacity_pad=256, workspace=None):
-    """The same decode step through the one-launch decoder layer
-    (cascade_decode_layer_bf16); CPU outputs, q / attn / inter read from the
-    workspace.  Returns None when the device cannot run the kernel."""
-
-    dev = torch.device(device)
-    past = case["past"]
-    n_kv, dim = case["n_kv_heads"], case["head_dim"]
-    w = {k: case[k].to(dev) for k in ("q", "k", "v", "o", "gate", "up", "down",
-                                      "ln1", "ln2")}
-    capacity = past + capacity_pad
-    k_cache = torch.zeros((n_kv, capacity, dim), dtype=torch.bfloat16, device=dev)
-    v_cache = torch.zeros_like(k_cache)
-    if past:
-        k_cache[:, :past].copy_(case["k_cache"].to(dev))
-        v_cache[:, :past].copy_(case["v_cache"].to(dev))
-    rope = RopeTable(dim, rope_parameters(Llama31Config()), dev, capacity)
-    cos, sin = rope.row(past)
-    x = case["x"].to(dev).clone()
-    if workspace is None:
-        workspace = torch.zeros(_hip.decode_layer_workspace_bytes(),
-                                dtype=torch.uint8, device=dev)
-    _say("decode_layer (one launch) past={}".format(past))
-    code = _hip.decode_layer(w, x, cos, sin, k_cache.view(-1), v_cache.view(-1),
-                             capacity * dim, past + 1, workspace, case["eps"],
-                             dim ** -0.5)
-    if code != 0:
-        return None
-    torch.cuda.synchronize(dev)
-
-    def ws_bf16(offset, n):
-        return workspace[offset:offset + 2 * n].view(torch.bfloat16).cpu()
-
-    hidden = case["x"].numel()
-    return {
-        "q": ws_bf16(_hip.DECODE_LAYER_Q, hidden),
-        "k_new": k_cache[:, past].cpu(),
-        "v_new": v_cache[:, past].cpu(),
-        "attn": ws_bf16(_hip.DECODE_LAYER_ATTN, hidden),
-        "inter": ws_bf16(_hip.DECODE_LAYER_INTER, w["gate"].shape[0]),
-        "out": x.cpu(),
-        "error": _hip.decode_layer_error(workspace),
-        "k_cache_prefix_intact": bool(torch.equal(
-            k_cache[:, :past].cpu(), case["k_cache"])) if past else True,
-    }
-
-
-def run_layer_fused_case(seed, past, device="cuda:0"):
-    """The one-launch layer against the oracle (as run_layer_case) and
-    against the per-stage kernels: q, k, v bit for bit (same GEMV rows, same
-    RMSNorm), the rest within the oracle tolerance."""
-
-    case = cases.layer_case(seed, past)
-    got = run_layer_fused_gpu(case, device)
-    if got is None:
-        return None
-    expected = cases.layer_expected(case)
-    alternative = cases.layer_expected(case, cases.sgemm_linear)
-    staged = run_layer_gpu(case, device)
-    report = {"seed": seed, "past": past, "error_word": got["error"]}
-    ok = got["k_cache_prefix_intact"] and got["error"] == 0
-    for key in ("q", "k_new", "v_new", "attn", "inter", "out"):
-        r = cases.compare(got[key], expected[key])
-        f = cases.within_noise_floor(got[key], expected[key], alternative[key])
-        r["ratio_to_noise_floor"] = f["ratio_to_floor"]
-        r["ok"] = r["ok"] or f["ok"]
-        report[key] = {k: round(v, 6) if isinstance(v, float) else v
-                       for k, v in r.items()}
-        ok = ok and r["ok"]
-    for key in ("q", "k_new", "v_new"):
-        same = bool(torch.equal(got[key], staged[key]))
-        report[key]["equals_per_stage"] = same
-        ok = ok and same
-    report["ok"] = bool(ok)
-    return report
-
-
 def run_lm_head_gpu(case, chunk_rows, top_k=10, device="cuda:0"):
     dev = torch.device(device)
     w = case["w"].to(dev)

@@ -41,7 +41,7 @@ def test_binding_types_exactly_the_declared_functions():
 def test_abi_version_and_error_strings():
     lib = _hip.load()
     assert lib.cascade_abi_version() == _hip.ABI_VERSION
-    for code in (0, 1001, 1002, 1003, 1004):
+    for code in (0, 1001, 1002, 1003, 1004, 1005):
         assert lib.cascade_error_string(code)
 
 
@@ -67,21 +67,6 @@ def test_argument_checks_reject_without_launching():
                                               32, 8, 64, 0.1, 16, None) == 1003
     assert lib.cascade_prefill_attention_bf16(16, 16, 16, 64 * 128, 0, 4,
                                               16, 8, 128, 0.1, 16, None) == 1003
-    # one-launch decoder layer: pointers, alignment, length, cache stride and
-    # workspace size are checked before anything touches the device
-    ws = _hip.decode_layer_workspace_bytes()
-
-    def layer(ptr=16, length=5, stride=128 * 8, ws_bytes=ws):
-        return lib.cascade_decode_layer_bf16(
-            ptr, 16, 16, 16, 16, 16, 16, 16, 16, 1e-5, 16, 16, 16, 16, 16,
-            stride, length, 0.1, 16, ws_bytes, None)
-
-    assert layer(ptr=None) == 1001
-    assert layer(ptr=24) == 1002
-    assert layer(length=0) == 1001
-    assert layer(length=(1 << 23) + 1, stride=128 << 24) == 1001
-    assert layer(stride=128 * 4) == 1001   # stride < len * head_dim
-    assert layer(ws_bytes=ws - 1) == 1004
     # device-position forms: the length word must be given and 8-byte
     # aligned, the capacity positive, the cache stride >= capacity * 128
     def qkv_at(length=16, capacity=10, stride=128 * 10):
@@ -118,11 +103,7 @@ def test_argument_checks_reject_without_launching():
 
 
 def test_workspace_sizes():
-    # one-launch layer: barrier words, q, attn, inter, then (m, l) and
-    # acc[128] per (kv head, split of 32, q head)
-    assert _hip.decode_layer_workspace_bytes() == (
-        1024 + 2 * 4096 * 2 + 14336 * 2 + 8 * 32 * 4 * 2 * 4 + 8 * 32 * 4 * 128 * 4)
-    # attention: counters + (m, l, acc[128]) per (kv head, split, q head),
+    # attention: header + (m, l, acc[128]) per (kv head, split, q head),
     # sized for the maximum of 64 splits whatever the length
     for length in (1, 2048, 32769, 1 << 20):
         assert _hip.attention_workspace_bytes(length) == 256 + 8 * 64 * 4 * (2 + 128) * 4

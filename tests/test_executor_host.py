@@ -178,41 +178,6 @@ class FakeKernels:
         at(indices, top_k, torch.int64).copy_(i + offset)
         return 0
 
-
-    def layer(self, wq, wk, wv, wo, wg, wu, wd, norm_in, norm_post, eps, x,
-              cos, sin, k0, v0, stride, length, scale, ws, ws_bytes, stream):
-        # the one-launch layer: the five per-stage doubles through the same
-        # pointers (new K / V at slot length - 1, x updated in place)
-        before = len(self.calls)
-        h, i, kv, dim = 4096, 14336, 1024, 128
-        slot = length - 1
-        q = torch.empty(h, dtype=BF16)
-        attn = torch.empty(h, dtype=BF16)
-        inter = torch.empty(i, dtype=BF16)
-        self.qkv(wq, wk, wv, h, kv, kv, h, x, norm_in, eps, cos, sin, q.data_ptr(),
-                 k0 + 2 * slot * dim, v0 + 2 * slot * dim, stride, stream)
-        self.attention(q.data_ptr(), k0, v0, stride, length, 32, 8, dim, scale,
-                       attn.data_ptr(), 0, 0, stream)
-        self.residual(wo, attn.data_ptr(), x, x, h, h, stream)
-        self.swiglu(wg, wu, i, h, x, norm_post, eps, inter.data_ptr(), stream)
-        self.residual(wd, inter.data_ptr(), x, x, h, i, stream)
-        del self.calls[before:]
-        self.calls.append("layer")
-        return 0
-
-    def mlp(self, wo, wg, wu, wd, norm_post, eps, attn, x, ws, ws_bytes, stream):
-        # the one-launch MLP half: o_proj + residual, gate/up + SwiGLU, down
-        # + residual through the same pointers
-        before = len(self.calls)
-        h, i = 4096, 14336
-        inter = torch.empty(i, dtype=BF16)
-        self.residual(wo, attn, x, x, h, h, stream)
-        self.swiglu(wg, wu, i, h, x, norm_post, eps, inter.data_ptr(), stream)
-        self.residual(wd, inter.data_ptr(), x, x, h, i, stream)
-        del self.calls[before:]
-        self.calls.append("mlp")
-        return 0
-
     # -------------------------------------- batched (S > 1) entry points
 
     def qkv_gemm(self, x, m, wq, wk, wv, nq, nk, nv, k, cos, sin, positions,
@@ -329,7 +294,7 @@ def exact_oracle(monkeypatch):
     monkeypatch.setattr(_hip, "require_device", lenient_require)
 
 
-def make_executor(monkeypatch, plan, store, layer_mode="stages"):
+def make_executor(monkeypatch, plan, store):
     fakes = FakeKernels()
 
     def gather(table, ids, out, error_flag=None, stream=None):
@@ -339,8 +304,7 @@ def make_executor(monkeypatch, plan, store, layer_mode="stages"):
     monkeypatch.setattr(_hip, "embedding_gather", gather)
     cache = SimpleKVCache(LAYERS, device="cpu")
     ex = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
-                               HostResident(plan, store), kv_cache=cache, top_k=5,
-                               layer_mode=layer_mode)
+                               HostResident(plan, store), kv_cache=cache, top_k=5)
     ex._stream = lambda: 0
     ex._k_qkv, ex._k_attn, ex._k_residual = fakes.qkv, fakes.attention, fakes.residual
     ex._k_swiglu, ex._k_silu, ex._k_mul = fakes.swiglu, fakes.silu, fakes.mul
@@ -349,8 +313,6 @@ def make_executor(monkeypatch, plan, store, layer_mode="stages"):
     ex._k_gemm_residual, ex._k_swiglu_gemm = fakes.gemm_residual, fakes.swiglu_gemm
     ex._k_silu_gemm, ex._k_mul_gemm = fakes.silu_gemm, fakes.mul_gemm
     ex._k_f32_gemm = fakes.f32_gemm
-    ex._k_layer = fakes.layer
-    ex._k_mlp = fakes.mlp
     ex._k_qkv_at, ex._k_attn_at = fakes.qkv_at, fakes.attention_at
     ex._k_step_begin = fakes.step_begin
     return ex, fakes
@@ -363,19 +325,15 @@ def run_units(plan, store, executor, state):
     return state
 
 
-@pytest.mark.parametrize("granularity", ["matrix_group", "matrix", "layer",
-                                         "layer/mlp", "layer/one"])
+@pytest.mark.parametrize("granularity", ["matrix_group", "matrix", "layer"])
 def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
                                                         exact_oracle, granularity):
-    # layer/mlp, layer/one: layer units whose decode steps run through
-    # cascade_decode_mlp_bf16 / cascade_decode_layer_bf16 (doubles above)
-    base, _, layer_mode = granularity.partition("/")
-    plan = build_llama31_8b_plan(base, num_layers=LAYERS)
+    plan = build_llama31_8b_plan(granularity, num_layers=LAYERS)
     # every granularity packs the arena identically, so one store serves all
     for key in plan.tensors:
         assert plan.tensor_host_offset(key) == weights.plan.tensor_host_offset(key)
     store = weights
-    executor, fakes = make_executor(monkeypatch, plan, store, layer_mode or "stages")
+    executor, fakes = make_executor(monkeypatch, plan, store)
     oracle = ref.OracleLlama(store.tensor, LAYERS)
     prompt = [7, 99, 1234, 5, 128255, 0]
     expected_logits, ev, ei = oracle.step(prompt, 5)
@@ -399,13 +357,10 @@ def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
         k, v = executor.kv_cache.entries[layer]
         assert torch.equal(k[0], oracle.caches[layer]["k"])
         assert torch.equal(v[0], oracle.caches[layer]["v"])
-    # (a layer unit of one token is one launch of the whole layer)
-    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5, "layer/mlp": 3,
-                 "layer/one": 1}[granularity]
+    per_token = {"matrix_group": 5, "matrix": 8, "layer": 5}[granularity]
     # prefill, per layer: input norm, q/k/v GEMM(s), causal attention,
     # o GEMM, post-attention norm, MLP GEMM(s), down GEMM
-    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7, "layer/mlp": 7,
-                   "layer/one": 7}[granularity]
+    per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7}[granularity]
     # decode, per layer and token: qkv launch(es), attention, o residual,
     # MLP, down; finish: one rmsnorm, then (prefill) one logits GEMM over
     # every position and one LM-head launch for the last
@@ -506,3 +461,16 @@ def test_begin_rejects_multi_token_after_prefill(monkeypatch, weights, exact_ora
     with pytest.raises(ValueError):
         Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS, hidden_size=8),
                               HostResident(plan, weights))
+
+
+def test_begin_rejects_token_ids_outside_the_vocabulary(monkeypatch, weights,
+                                                        exact_oracle):
+    # F.embedding raises on such an id (the reference's resident table,
+    # llama31.py:144-148); host-held ids are checked before any launch
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    executor, fakes = make_executor(monkeypatch, plan, weights)
+    for bad in ([[128256]], [[-1]], [[5, 128256, 7]]):
+        with pytest.raises(IndexError):
+            executor.begin(torch.tensor(bad))
+    assert fakes.calls == []
+    executor.begin(torch.tensor([[128255]]))  # the last valid id

@@ -99,10 +99,6 @@ def copy_weights(src, dst):
 
 
 def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
-    # "layer/mlp", "layer/one": layer units whose decode steps run the MLP
-    # half (cascade_decode_mlp_bf16) or the whole layer
-    # (cascade_decode_layer_bf16) as one launch
-    granularity, _, layer_mode = granularity.partition("/")
     plan = build_llama31_8b_plan(granularity, stream_vocab=(vocab_mode == "streamed"),
                                  num_layers=LAYERS)
     store = create_weight_store(plan, store_mode)
@@ -117,8 +113,7 @@ def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
         vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
     executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
                                      resident, vocab_runtime=vocab, top_k=TOP_K,
-                                     return_full_logits=True,
-                                     layer_mode=layer_mode or "stages")
+                                     return_full_logits=True)
     return store, runtime, executor
 
 
@@ -168,8 +163,7 @@ CONFIGS = [
     ("full_pinned", "layer", "resident", "double"),
     ("pinned_staging", "matrix_group", "resident", "double"),
     ("full_pinned", "matrix_group", "resident", "resident"),
-    ("full_pinned", "layer/mlp", "resident", "resident"),
-    ("full_pinned", "layer/one", "resident", "resident"),
+    ("full_pinned", "layer", "resident", "resident"),
 ]
 
 
@@ -244,3 +238,33 @@ def test_decode_continues_after_cache_growth(gpu_device, source_store):
         assert executor.kv_cache.capacity >= 259
         store.close()
     assert outs[0] == outs[1]
+
+
+def test_out_of_vocabulary_ids_raise(gpu_device, source_store):
+    # A prompt (read back once) and a host-held id raise in begin(); a
+    # device-held decode id is flagged by the gather kernel (zero row, no
+    # fault) and raises at the next check, as F.embedding would raise.
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    store = create_weight_store(plan, "full_pinned")
+    copy_weights(source_store, store)
+    resident = ResidentDeviceArena(plan, store, gpu_device)
+    runtime = ResidentTransformerRuntime(plan, store, resident, gpu_device)
+    executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
+                                     resident, top_k=TOP_K)
+    with torch.inference_mode():
+        with pytest.raises(IndexError):
+            executor.begin(torch.tensor([[5, 128256]], device=gpu_device))
+        with pytest.raises(IndexError):
+            executor.begin(torch.tensor([[-3]]))
+        state = executor.finish(runtime.run(executor, executor.begin(
+            torch.tensor([PROMPT], device=gpu_device))))
+        executor.check_errors()  # nothing flagged
+        bad = torch.tensor([[128256]], device=gpu_device)
+        state = executor.finish(runtime.run(executor, executor.begin(bad)))
+        with pytest.raises(IndexError):
+            executor.check_errors()
+        executor.check_errors()  # the flag was cleared
+        good = state.topk_indices.reshape(1, -1)[:, :1].clone().fill_(7)
+        state = executor.finish(runtime.run(executor, executor.begin(good)))
+        executor.check_errors()
+    store.close()
