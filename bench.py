@@ -95,8 +95,9 @@ def parse_args():
                         "timed launch adds ~5 us of queue time)")
     p.add_argument("--probe", action="store_true",
                    help="only run the HBM-counter probe: 4 plain device copies "
-                        "of 256 MiB, then 12 gate/up SwiGLU launches over 3 "
-                        "rotating weight copies (for rocprofv3 --pmc runs)")
+                        "of 256 MiB, then 12 launches of each decode kernel "
+                        "over 3 rotating operand copies (for rocprofv3 --pmc "
+                        "runs)")
     p.add_argument("--hbm-only", action="store_true",
                    help="only measure and print the achievable HBM read "
                         "bandwidth sweep")
@@ -108,10 +109,16 @@ TRAFFIC_FILE = ROOT / "profiles" / "gate_up_traffic.txt"
 
 
 def counter_probe():
-    """Known-size copies (counter calibration) then the dominant kernel."""
+    """Known-size copies (counter calibration), then each decode kernel at
+    its config-4 shape over 3 rotating operand copies (beyond the 256 MB
+    MALL), 12 launches each, in this order: gate/up SwiGLU, q|k|v + RoPE,
+    o_proj + residual, down_proj + residual, decode attention at L = 32769
+    (main kernel + split merge)."""
 
     import torch
     from layer_streaming import _hip
+    from layer_streaming.llama31 import Llama31Config
+    from layer_streaming.rope import RopeTable, rope_parameters
 
     dev = torch.device("cuda:0")
     src = torch.randn(PROBE_COPY_BYTES // 4, device=dev)
@@ -120,17 +127,61 @@ def counter_probe():
         _hip.device_copy(dst, src)
     torch.cuda.synchronize(dev)
     log("probe: 4 device copies of {} bytes done".format(PROBE_COPY_BYTES))
-    mats = [(torch.randn(INTER, HIDDEN, device=dev).mul_(0.02).to(torch.bfloat16),
-             torch.randn(INTER, HIDDEN, device=dev).mul_(0.02).to(torch.bfloat16))
-            for _ in range(3)]
-    x = torch.randn(HIDDEN, device=dev).to(torch.bfloat16)
+    del src, dst
+
+    def weights(rows, k):
+        return [torch.randn(rows, k, device=dev).mul_(0.02).to(torch.bfloat16)
+                for _ in range(3)]
+
+    x = torch.randn(INTER, device=dev).to(torch.bfloat16)
     norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
     y = torch.empty(INTER, dtype=torch.bfloat16, device=dev)
+    gates, ups = weights(INTER, HIDDEN), weights(INTER, HIDDEN)
     for i in range(12):
-        g, u = mats[i % 3]
-        _hip.gate_up_swiglu(g, u, x, norm, 1e-5, y)
+        _hip.gate_up_swiglu(gates[i % 3], ups[i % 3], x[:HIDDEN], norm, 1e-5, y)
     torch.cuda.synchronize(dev)
     log("probe: 12 gate/up launches done")
+    del gates, ups
+
+    length = 32769
+    capacity = 32800
+    kv = [torch.randn(2, 8, capacity, 128, device=dev).to(torch.bfloat16)
+          for _ in range(3)]
+    rope = RopeTable(128, rope_parameters(Llama31Config()), dev, capacity)
+    cos, sin = rope.row(length - 1)
+    q = torch.empty(HIDDEN, dtype=torch.bfloat16, device=dev)
+    wqs, wks, wvs = weights(HIDDEN, HIDDEN), weights(1024, HIDDEN), weights(1024, HIDDEN)
+    stride = capacity * 128
+    for i in range(12):
+        cache = kv[i % 3]
+        _hip.qkv_rope(wqs[i % 3], wks[i % 3], wvs[i % 3], x[:HIDDEN], norm, 1e-5,
+                      cos, sin, q, cache[0].view(-1)[(length - 1) * 128:],
+                      cache[1].view(-1)[(length - 1) * 128:], stride)
+    torch.cuda.synchronize(dev)
+    log("probe: 12 q|k|v launches done")
+    del wqs, wks, wvs
+    h = torch.randn(HIDDEN, device=dev).to(torch.bfloat16)
+    wos = weights(HIDDEN, HIDDEN)
+    for i in range(12):
+        _hip.gemv_residual(wos[i % 3], x[:HIDDEN], h, h)
+    torch.cuda.synchronize(dev)
+    log("probe: 12 o_proj launches done")
+    del wos
+    wds = weights(HIDDEN, INTER)
+    for i in range(12):
+        _hip.gemv_residual(wds[i % 3], x, h, h)
+    torch.cuda.synchronize(dev)
+    log("probe: 12 down_proj launches done")
+    del wds
+    out = torch.empty(HIDDEN, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(_hip.attention_workspace_bytes(length), dtype=torch.uint8,
+                     device=dev)
+    for i in range(12):
+        cache = kv[i % 3]
+        _hip.decode_attention(q, cache[0].view(-1), cache[1].view(-1), stride,
+                              length, out, ws, 128 ** -0.5)
+    torch.cuda.synchronize(dev)
+    log("probe: 12 attention launches done")
 
 
 def measured_traffic(path):
@@ -172,7 +223,7 @@ def hbm_plateau():
     buf.view(torch.int32).random_(0, 1 << 30)
     sink = torch.zeros(1, dtype=torch.float32, device=dev)
     sweep = {}
-    for blocks in (1024, 2048, 4096, 8192, 16384):
+    for blocks in (512, 1024, 2048, 4096, 8192, 16384, 32768):
         times = []
         for rep in range(10):
             start = _hip.HipEvent(enable_timing=True)
@@ -194,9 +245,9 @@ def hbm_plateau():
         "bytes": HBM_SWEEP_BYTES,
         "peak_gbps": HBM_PEAK_GBPS,
         "frac_of_peak": round(sweep[best] / HBM_PEAK_GBPS, 4),
-        "method": "cascade_hbm_read: nontemporal 16-byte loads, 4 in flight per "
-                  "thread, 256-thread workgroups; kernel-bound events, median "
-                  "of 8 launches per width",
+        "method": "cascade_hbm_read: nontemporal 16-byte loads, 8 in flight per "
+                  "thread, 32 KiB contiguous per 256-thread workgroup and step; "
+                  "kernel-bound events, median of 8 launches per width",
     }
 
 

@@ -60,28 +60,31 @@ __global__ __launch_bounds__(kGatherThreads) void decode_step_begin_kernel(
 
 constexpr int kStreamThreads = 256;
 
-// Streaming read for the achievable-bandwidth measurement: each thread keeps
-// kReadUnroll nontemporal 16-byte loads in flight per step, the grid walks
-// the buffer in strides of its whole width.
-constexpr int kReadUnroll = 4;
+// Streaming read for the achievable-bandwidth measurement.  A workgroup
+// reads tiles of kReadUnroll x 4 KiB contiguous bytes (load u of its 256
+// threads covers bytes [4 KiB u, 4 KiB (u + 1)) of the tile, all kReadUnroll
+// nontemporal loads in flight before any is used), and the grid walks the
+// tiles in strides of its width: each DRAM page is read by one workgroup in
+// one go, as the decode GEMVs read their weight rows.
+constexpr int kReadUnroll = 8;
+constexpr int64_t kReadTileVecs = int64_t{kStreamThreads} * kReadUnroll;
 
 __global__ __launch_bounds__(kStreamThreads) void hbm_read_kernel(
     const u32x4 *src, int64_t nvec, float *sink) {
   float s = 0.0f;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kStreamThreads;
-  int64_t j = static_cast<int64_t>(blockIdx.x) * kStreamThreads + threadIdx.x;
-  for (; j + (kReadUnroll - 1) * stride < nvec; j += kReadUnroll * stride) {
+  const int64_t tiles = (nvec + kReadTileVecs - 1) / kReadTileVecs;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t base = tile * kReadTileVecs + threadIdx.x;
     u32x4 v[kReadUnroll];
 #pragma unroll
-    for (int u = 0; u < kReadUnroll; ++u)
-      v[u] = __builtin_nontemporal_load(src + j + u * stride);
+    for (int u = 0; u < kReadUnroll; ++u) {
+      const int64_t j = base + int64_t{u} * kStreamThreads;
+      v[u] = j < nvec ? __builtin_nontemporal_load(src + j)
+                      : u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int u = 0; u < kReadUnroll; ++u)
       s += __uint_as_float(v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
-  }
-  for (; j < nvec; j += stride) {
-    const u32x4 v = __builtin_nontemporal_load(src + j);
-    s += __uint_as_float(v.x ^ v.y ^ v.z ^ v.w);
   }
   // Data-dependent store so the loads cannot be removed; never taken for
   // ordinary data.

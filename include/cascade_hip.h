@@ -322,7 +322,8 @@ int cascade_host_copy(void *dst, const void *src, size_t bytes, int threads);
 
 /* ----------------------------------------------------------- measurement
  * Streaming-read kernel: reads `bytes` of device memory (nontemporal 16-byte
- * loads, four in flight per thread) and folds them into *sink; `blocks`
+ * loads, eight in flight per thread, 32 KiB contiguous per workgroup and
+ * step) and folds them into *sink; `blocks`
  * workgroups of 256 threads (0: the library's default of up to 4096).  Used
  * to measure achievable HBM read bandwidth (no reference counterpart; the
  * reference measures only H2D, h2d_driver_bench.c).
