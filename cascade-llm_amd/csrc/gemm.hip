@@ -8,22 +8,31 @@
 // input (layer_streaming/llama31.py:241-279 during the prefill call, and the
 // resident LM head, llama31.py:330-334).
 //
-// Tiling.  A workgroup of 4 waves computes a BM x 128 output tile (BM = 128,
-// or 64 when 128-row tiles would leave CUs idle: short prompts and the
-// N = 1024 K / V projections); K is walked in 64-deep slabs.  Each wave
-// owns 64 rows x 64 (or 32) columns of v_mfma_f32_16x16x32_bf16 fragments
-// and reads its A and B fragments (16 bytes a lane) from LDS.
+// Tiling.  A workgroup computes a BM x 128 output tile, K walked in 64-deep
+// slabs; each wave owns 64 rows x 64 (or 32) columns of
+// v_mfma_f32_16x16x32_bf16 fragments and reads its A and B fragments (16
+// bytes a lane) from LDS.  Three shapes (launch_gemm picks one):
+//   GemmTile256  256 x 128, 8 waves, a ring of 3 slab buffers (two slabs in
+//                flight while the third is read): the large GEMMs (M > 128
+//                with at least 256 such tiles: q, o, gate, up, down at
+//                M = 2048);
+//   GemmTile64   64 x 128, 4 waves, a ring of 4 slab buffers: where 128-row
+//                tiles would leave CUs idle (the N = 1024 K / V
+//                projections, prompts of at most 64 tokens);
+//   GemmTile128  128 x 128, 4 waves, two slab buffers: everything else.
 //
 // Staging.  Slabs move global -> LDS by buffer loads that write LDS
 // themselves (buffer_load_dwordx4 ... lds: no staging registers, no
-// ds_write), into two slab buffers.  Slab s: each wave waits (vmcnt) for
-// its own loads of slab s, one barrier publishes slab s to the workgroup
-// and frees slab s - 1's buffer, the loads of slab s + 1 go out, and slab
-// s's MFMAs run while they fly.  Each buffer is its own __shared__ array
-// and the loop is unrolled by two, so the compiler can tell a slab's LDS
-// reads from the loads in flight and adds no waits of its own.  (With three
-// or four buffers this compiler falls back to waiting for every load in
-// flight at each barrier, so deeper staging does not pay.)
+// ds_write).  With two buffers the loads use the LDS-DMA builtin; slab s:
+// each wave waits (vmcnt) for its own loads of slab s, one barrier publishes
+// slab s to the workgroup and frees slab s - 1's buffer, the loads of slab
+// s + 1 go out, and slab s's MFMAs run while they fly.  Each buffer is its
+// own __shared__ array and the loop is unrolled by two, so the compiler can
+// tell a slab's LDS reads from the loads in flight.  With a ring of three or
+// four buffers the compiler would wait for every load in flight at each
+// barrier, so those loads are issued from inline asm (dma_lds16), invisible
+// to it, and each slab step waits with an explicit vmcnt for exactly its
+// own slab.
 //
 // LDS layout of a slab: 128-byte rows (64 bf16) back to back; 16-byte
 // chunk c of row r sits at chunk c ^ ((r / 2) % 8).  A fragment read (16
