@@ -11,28 +11,30 @@
 // Tiling.  A workgroup computes a BM x 128 output tile, K walked in 64-deep
 // slabs; each wave owns 64 rows x 64 (or 32) columns of
 // v_mfma_f32_16x16x32_bf16 fragments and reads its A and B fragments (16
-// bytes a lane) from LDS.  Three shapes (launch_gemm picks one):
-//   GemmTile256  256 x 128, 8 waves, a ring of 3 slab buffers (two slabs in
-//                flight while the third is read): the large GEMMs (M > 128
-//                with at least 256 such tiles: q, o, gate, up, down at
-//                M = 2048);
-//   GemmTile64   64 x 128, 4 waves, a ring of 4 slab buffers: where 128-row
-//                tiles would leave CUs idle (the N = 1024 K / V
-//                projections, prompts of at most 64 tokens);
-//   GemmTile128  128 x 128, 4 waves, two slab buffers: everything else.
+// bytes a lane) from LDS.  Shapes (launch_gemm picks one):
+//   GemmTile256  256 x 128, 8 waves, a ring of 3 slab buffers: the large
+//                GEMMs (at least as many 256-row tiles as CUs: q, o, gate,
+//                up, down at M = 2048);
+//   GemmTile128  128 x 128, 4 waves, a ring of 4;
+//   GemmTile64   64 x 128, 4 waves, a ring of 6: where 128-row tiles would
+//                leave CUs idle (the N = 1024 K / V projections at M = 2048,
+//                prompts of at most 64 tokens).
+// When the last round of tiles would leave at least half of the CUs idle,
+// the last tile columns run as tiles of half the height in the same launch
+// (GemmTile128x8 for GemmTile256, GemmTile64 for GemmTile128): M = 2048,
+// N = 14336 runs 768 full tiles in three rounds, then 256 half tiles,
+// instead of three and a half rounds of full tiles.
 //
 // Staging.  Slabs move global -> LDS by buffer loads that write LDS
 // themselves (buffer_load_dwordx4 ... lds: no staging registers, no
-// ds_write).  With two buffers the loads use the LDS-DMA builtin; slab s:
-// each wave waits (vmcnt) for its own loads of slab s, one barrier publishes
-// slab s to the workgroup and frees slab s - 1's buffer, the loads of slab
-// s + 1 go out, and slab s's MFMAs run while they fly.  Each buffer is its
-// own __shared__ array and the loop is unrolled by two, so the compiler can
-// tell a slab's LDS reads from the loads in flight.  With a ring of three or
-// four buffers the compiler would wait for every load in flight at each
-// barrier, so those loads are issued from inline asm (dma_lds16), invisible
-// to it, and each slab step waits with an explicit vmcnt for exactly its
-// own slab.
+// ds_write), issued from inline asm (dma_lds16) so that the compiler, which
+// cannot tell which ring buffer such a load writes, adds no waits of its
+// own.  Slab s lives in ring buffer s % STAGES.  Step s waits (explicit
+// vmcnt) for this wave's loads of slab s + 1 only, one barrier publishes
+// slab s + 1 and frees slab s's buffer, slab s + STAGES goes out into it,
+// and slab s + 1's fragments are read into registers while slab s's MFMAs
+// run from the registers filled one step earlier, so the MFMAs never wait
+// on an LDS read.
 //
 // LDS layout of a slab: 128-byte rows (64 bf16) back to back; 16-byte
 // chunk c of row r sits at chunk c ^ ((r / 2) % 8).  A fragment read (16
@@ -66,6 +68,8 @@
 //   silu / mul  the matrix-granularity halves of swiglu
 //   f32       fp32 output (LM-head logits, not rounded)
 #include <algorithm>
+#include <atomic>
+#include <type_traits>
 
 #include "cascade_device.h"
 #include "cascade_internal.h"
@@ -107,7 +111,10 @@ struct GemmArgs {
   uint16_t *v_out;
   int64_t kv_head_stride;
   int64_t slot0;
-  int32_t tiles_m, tiles_n, tiles;
+  // full tiles: a tiles_m x tiles_n grid (tiles of them, per_xcd on each
+  // XCD); half-height tiles: an htiles_m x htiles_n grid right of it
+  int32_t tiles_m, tiles_n, tiles, per_xcd;
+  int32_t htiles_m, htiles_n, htiles, hper_xcd;
   int32_t vec_out;  // row pitches and widths allow 16-byte output accesses
 };
 
@@ -115,16 +122,16 @@ __device__ __forceinline__ float gemm_silu(float g) {
   return g / (1.0f + expf(-g));
 }
 
-// Logical tile of this workgroup (false: padding workgroup, no work).
-__device__ __forceinline__ bool gemm_tile(const GemmArgs &a, int &tm, int &tn) {
-  const int per = static_cast<int>(gridDim.x) / kXcds;
-  const int t = static_cast<int>(blockIdx.x % kXcds) * per +
-                static_cast<int>(blockIdx.x / kXcds);
-  if (t >= a.tiles) return false;
-  const int group_size = kGroupM * a.tiles_n;
+// Tile (tm, tn) of logical tile t in a tiles_m x tiles_n grid (false:
+// padding workgroup, no work).  Logical tiles run in groups of kGroupM
+// tile rows, column-major inside a group.
+__device__ __forceinline__ bool gemm_tile(int t, int tiles, int tiles_m, int tiles_n,
+                                          int &tm, int &tn) {
+  if (t >= tiles) return false;
+  const int group_size = kGroupM * tiles_n;
   const int group = t / group_size;
   const int first = group * kGroupM;
-  const int gm = min(kGroupM, a.tiles_m - first);
+  const int gm = min(kGroupM, tiles_m - first);
   const int r = t - group * group_size;
   tm = first + r % gm;
   tn = r / gm;
@@ -152,6 +159,7 @@ struct GemmTile {
 using GemmTile256 = GemmTile<256, 4, 2>;  // 8 waves of 64 x 64
 using GemmTile128 = GemmTile<128, 2, 2>;  // 4 waves of 64 x 64
 using GemmTile64 = GemmTile<64, 1, 4>;    // 4 waves of 64 x 32
+using GemmTile128x8 = GemmTile<128, 2, 4>;  // 8 waves of 64 x 32 (half of GemmTile256)
 
 // Tile column of fragment j of wave column wn for lane row lr.  A wave's
 // first-half fragments (j < H) and second-half fragments (j >= H) sit 64
@@ -442,15 +450,8 @@ struct DmaSlab {
   static_assert(BK == 32 || BK == 64, "slab depth");
 };
 
-// Buffer resource over [base, base + bytes).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const uint16_t *base,
-                                                           int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0,
-                                           static_cast<int>(bytes), 0x00020000);
-}
-
-// The same resource as four words (for inline asm): base, stride 0,
-// num_records, the flags above.
+// Buffer resource over [base, base + bytes) as four words (for inline asm):
+// base, stride 0, num_records, raw-buffer flags.
 __device__ __forceinline__ u32x4 gemm_rsrc_words(const uint16_t *base, int64_t bytes) {
   const uint64_t p = reinterpret_cast<uint64_t>(base);
   u32x4 r;
@@ -462,51 +463,48 @@ __device__ __forceinline__ u32x4 gemm_rsrc_words(const uint16_t *base, int64_t b
 }
 
 // buffer_load_dwordx4 ... lds issued from inline asm: lane l's 16 bytes at
-// voffset land at LDS byte (lds + 16 l).  The compiler does not see these
-// loads, so it adds no vmcnt waits of its own for them (the caller waits);
-// the memory clobber keeps LDS accesses from moving across the issue.
-// The descriptor words pass through readfirstlane (a no-op on values the
-// compiler already keeps in SGPRs): where it cannot prove a selected
+// voffset land at LDS byte address (lds + 16 l).  The compiler does not see
+// these loads, so it adds no vmcnt waits of its own for them (the caller
+// waits); the memory clobber keeps LDS accesses from moving across the
+// issue.  The descriptor words pass through readfirstlane (a no-op on values
+// the compiler already keeps in SGPRs): where it cannot prove a selected
 // descriptor uniform it would otherwise hand the asm VGPRs.
-__device__ __forceinline__ void dma_lds16(const u32x4 &rsrc, int voff, const uint16_t *lds) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)lds)));
+__device__ __forceinline__ void dma_lds16(const u32x4 &rsrc, int voff, uint32_t lds) {
   u32x4 r;
   r.x = __builtin_amdgcn_readfirstlane(rsrc.x);
   r.y = __builtin_amdgcn_readfirstlane(rsrc.y);
   r.z = __builtin_amdgcn_readfirstlane(rsrc.z);
   r.w = __builtin_amdgcn_readfirstlane(rsrc.w);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(m0), "v"(voff), "s"(r) : "memory", "m0");
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r)
+               : "memory", "m0");
 }
 
-// STAGES = 2: two slab buffers, the slab loads through the LDS-DMA builtin
-// (the compiler waits for them exactly).  STAGES = 3 or 4: a ring of slab
-// buffers with STAGES - 1 slabs in flight; the loads go through dma_lds16
-// and each slab step waits for exactly its own slab (vmcnt = the later
-// slabs' loads), since with more than two buffers the compiler would wait
-// for every load in flight at each barrier.
-template <int EPI, class T, int STAGES = 2, int BK = kTileK>
-__global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
-  static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 slab buffers");
+// Ring geometry of a tile shape: bf16 elements of one slab buffer (X rows,
+// then W rows), and of the LDS a workgroup needs (the ring, or the staged
+// output tile of the vectorised epilogue, which reuses it).
+template <class T, int STAGES, int BK = kTileK>
+struct GemmRing {
+  static constexpr int XB = T::BM * BK;
+  static constexpr int WB = kTileN * BK;
+  static constexpr int SLAB = XB + WB;
+  static constexpr int STAGE = kTileN * T::STAGE_COL;
+  static constexpr int LDS = STAGES * SLAB > STAGE ? STAGES * SLAB : STAGE;
+};
+
+// Output tile (tm, tn) of shape T: rows tm * BM .., columns tn * 128 ..
+// (q|k|v: head tn; SwiGLU: gate / up rows tn * 64 ..).  sb0 holds the ring.
+template <int EPI, class T, int STAGES, int BK = kTileK>
+__device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
+                                              uint16_t *sb0) {
+  static_assert(STAGES >= 3, "a ring of at least 3 slab buffers");
   using L = DmaSlab<BK>;
+  using R = GemmRing<T, STAGES, BK>;
   constexpr int XI = T::BM * L::ROWB / 1024;  // load instructions per X slab
   constexpr int WI = kTileN * L::ROWB / 1024;
   constexpr int XW = XI / T::WAVES, WW = WI / T::WAVES;  // per wave
   static_assert(XI % T::WAVES == 0 && WI % T::WAVES == 0, "whole loads per wave");
-  constexpr int XB = T::BM * BK, WB = kTileN * BK;  // bf16 per slab buffer
-  // STAGES = 2: one array per slab buffer (X slab, then W slab); sb0 also
-  // holds the staged output tile of the vectorised epilogue.  STAGES >= 3:
-  // sb0 holds the ring (slab buffer k at sb0 + k (XB + WB)) and, after the
-  // loop, the staged tile.
-  constexpr int kStage = kTileN * T::STAGE_COL;
-  constexpr int kSlab = XB + WB;
-  constexpr int kRing = (STAGES == 2 ? 1 : STAGES) * kSlab;
-  constexpr int kSb0 = kRing > kStage ? kRing : kStage;
-  __shared__ __attribute__((aligned(16))) uint16_t sb0[kSb0];
-  __shared__ __attribute__((aligned(16))) uint16_t sb1[STAGES == 2 ? kSlab : 8];
-  int tm, tn;
-  if (!gemm_tile(a, tm, tn)) return;  // whole workgroup: no barrier skipped
+  constexpr int XB = R::XB, kSlab = R::SLAB;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -517,7 +515,6 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
   const int64_t k_bytes = a.k * 2;
 
   // operands as buffer resources; W instruction i reads matrix wsel(i)
-  const __amdgpu_buffer_rsrc_t xr = gemm_rsrc(a.x, a.m * k_bytes);
   const uint16_t *wbase0, *wbase1;
   int64_t wrows0, wrows1, wrow0, wrow1;  // rows of each matrix, first tile row in it
   if constexpr (EPI == kGemmSwiglu) {
@@ -537,8 +534,9 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
     wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kTileN;
     wbase1 = wbase0; wrows1 = wrows0; wrow1 = wrow0;
   }
-  const __amdgpu_buffer_rsrc_t wr0 = gemm_rsrc(wbase0, wrows0 * k_bytes);
-  const __amdgpu_buffer_rsrc_t wr1 = gemm_rsrc(wbase1, wrows1 * k_bytes);
+  const u32x4 xw = gemm_rsrc_words(a.x, a.m * k_bytes);
+  const u32x4 ww0 = gemm_rsrc_words(wbase0, wrows0 * k_bytes);
+  const u32x4 ww1 = gemm_rsrc_words(wbase1, wrows1 * k_bytes);
 
   // lane part of a load: row L / CH of the instruction's RPI rows, physical
   // chunk L % CH, i.e. logical chunk (L % CH) ^ f(row); f depends on the
@@ -549,31 +547,6 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
     return ld_r * static_cast<int>(k_bytes) + 16 * ((lane % L::CH) ^ f);
   };
   const int ld_off0 = ld_off(0), ld_off1 = ld_off(1);
-
-  // The whole byte offset goes in voffset: the buffer range check covers
-  // voffset (not soffset), so rows past the end read as zeros instead of
-  // leaving the allocation.  Offsets stay below 2^31 (checked on the host).
-  auto load_slab = [&](int slab, uint16_t *dx, uint16_t *dw) {
-    const int kb = slab * BK * 2;
-#pragma unroll
-    for (int h = 0; h < XW; ++h) {
-      const int i = wave * XW + h;
-      const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xr, (__attribute__((address_space(3))) void *)(dx + i * 512), 16,
-          ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb, 0, 0, 0);
-    }
-#pragma unroll
-    for (int h = 0; h < WW; ++h) {
-      const int i = wave * WW + h;
-      const int trow = L::RPI * i;  // tile row of the instruction
-      const bool second = EPI == kGemmSwiglu && trow >= kGemmHalfHead;
-      const int64_t row = (second ? wrow1 : wrow0) + (second ? trow - kGemmHalfHead : trow);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          second ? wr1 : wr0, (__attribute__((address_space(3))) void *)(dw + i * 512), 16,
-          ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb, 0, 0, 0);
-    }
-  };
 
   // fragment reads: rows 16 q + lr (q: fragment), chunk 4 ks + g4 at
   // physical chunk (4 ks + g4) ^ f(lr), f(lr) = (lr / RPB) % CH
@@ -588,181 +561,237 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](const uint16_t *bx, const uint16_t *bw) {
-    const char *ax = reinterpret_cast<const char *>(bx) + arow0 * L::ROWB;
-    const char *aw = reinterpret_cast<const char *>(bw);
+  const int slabs = static_cast<int>(a.k / BK);
+  // LDS byte address of sb0 (the ring's buffer b starts kSlab * 2 b bytes
+  // later)
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)sb0)));
+  // The whole byte offset goes in voffset: the buffer range check covers
+  // voffset (not soffset), so rows past the end read as zeros instead of
+  // leaving the allocation.  Offsets stay below 2^31 (checked on the host).
+  auto ring_load = [&](int slab, int buf) {
+    const uint32_t dx = ring_lds + static_cast<uint32_t>(buf * kSlab * 2);
+    const uint32_t dw = dx + XB * 2;
+    const int kb = slab * BK * 2;
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
+    for (int h = 0; h < XW; ++h) {
+      const int i = wave * XW + h;
+      const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
+      dma_lds16(xw, ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
+                dx + i * 1024);
+    }
+#pragma unroll
+    for (int h = 0; h < WW; ++h) {
+      const int i = wave * WW + h;
+      const int trow = L::RPI * i;  // tile row of the instruction
+      const bool second = EPI == kGemmSwiglu && trow >= kGemmHalfHead;
+      const int64_t row = (second ? wrow1 : wrow0) + (second ? trow - kGemmHalfHead : trow);
+      dma_lds16(second ? ww1 : ww0,
+                ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
+                dw + i * 1024);
+    }
+  };
+  // Slab j lives in ring buffer j % STAGES.  Step s (one per slab):
+  //   wait for this wave's loads of slab s + 1 (the loads of the
+  //   STAGES - 2 slabs after it may stay in flight) and for its LDS reads
+  //   of slab s (lgkmcnt 0); one barrier publishes slab s + 1 and frees
+  //   slab s's buffer;
+  //   slab s + STAGES goes out into that buffer;
+  //   slab s + 1's fragments are read into registers while slab s's
+  //   MFMAs, whose fragments were read one step earlier, run: the MFMA
+  //   queue never waits on an LDS read.
+  // Steps past the end reload the last slab and read fragments that are
+  // never used, so every step issues the same loads and a constant vmcnt
+  // covers every wait.
+  constexpr int D = XW + WW;
+  constexpr int kAhead = (STAGES - 2) * D;
+  constexpr int kAheadFirst = (STAGES - 1) * D;
+  static_assert(kAheadFirst < 64, "vmcnt holds 6 bits");
+  constexpr int kWaitStep = (kAhead & 15) | ((kAhead >> 4) << 14) | (7 << 4);
+  constexpr int kWaitFirst = (kAheadFirst & 15) | ((kAheadFirst >> 4) << 14) | (7 << 4);
+  constexpr int kWaitAll = 7 << 4;  // vmcnt(0) lgkmcnt(0)
+  constexpr int KS = BK / 32;
+  constexpr int kReads = KS * (T::FM + T::FN);
+  constexpr int kMfmas = KS * T::FM * T::FN;
+  static_assert(kMfmas >= kReads, "one MFMA ahead of every fragment read");
+  using FragA = u32x4[KS][T::FM];
+  using FragB = u32x4[KS][T::FN];
+  auto read_frags = [&](int buf, FragA &fa, FragB &fb) {
+    const char *ax = reinterpret_cast<const char *>(sb0 + buf * kSlab) + arow0 * L::ROWB;
+    const char *aw = reinterpret_cast<const char *>(sb0 + buf * kSlab + XB);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
       const int off = ks ? rd_off1 : rd_off0;
-      u32x4 af[T::FM], bfr[T::FN];
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
-        af[i] = *reinterpret_cast<const u32x4 *>(ax + off + 16 * i * L::ROWB);
+        fa[ks][i] = *reinterpret_cast<const u32x4 *>(ax + off + 16 * i * L::ROWB);
 #pragma unroll
       for (int j = 0; j < T::FN; ++j)
-        bfr[j] = *reinterpret_cast<const u32x4 *>(
+        fb[ks][j] = *reinterpret_cast<const u32x4 *>(
             aw + off + (gemm_col<T>(wn, j, lr) - lr) * L::ROWB);
+    }
+  };
+  // publish: every LDS read issued so far stays above the wait (the empty
+  // asm pins memory accesses in program order)
+  auto publish_step = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitStep);
+    __builtin_amdgcn_s_barrier();
+  };
+  int cur = 0;  // buffer of slab s
+  auto step = [&](int s, const FragA &fa, const FragB &fb, FragA &na, FragB &nb) {
+    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
+    publish_step();
+    ring_load(min(s + STAGES, slabs - 1), cur);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(nxt, na, nb);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
 #pragma unroll
         for (int j = 0; j < T::FN; ++j)
-          acc[i][j] = mfma_16x16x32_bf16(af[i], bfr[j], acc[i][j]);
+          acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
+    // MFMA, read, MFMA, read, ..., then the remaining MFMAs
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kReads, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = nxt;
   };
-
-  const int slabs = static_cast<int>(a.k / BK);
-  // s_waitcnt vmcnt(0), expcnt / lgkmcnt left alone
-  constexpr int kWaitLoads = (7 << 4) | (15 << 8);
-  if constexpr (STAGES >= 3) {
-    const u32x4 xw = gemm_rsrc_words(a.x, a.m * k_bytes);
-    const u32x4 ww0 = gemm_rsrc_words(wbase0, wrows0 * k_bytes);
-    const u32x4 ww1 = gemm_rsrc_words(wbase1, wrows1 * k_bytes);
-    auto ring_load = [&](int slab, uint16_t *dx) {
-      uint16_t *dw = dx + XB;
-      const int kb = slab * BK * 2;
 #pragma unroll
-      for (int h = 0; h < XW; ++h) {
-        const int i = wave * XW + h;
-        const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
-        dma_lds16(xw, ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
-                  dx + i * 512);
-      }
-#pragma unroll
-      for (int h = 0; h < WW; ++h) {
-        const int i = wave * WW + h;
-        const int trow = L::RPI * i;
-        const bool second = EPI == kGemmSwiglu && trow >= kGemmHalfHead;
-        const int64_t row = (second ? wrow1 : wrow0) + (second ? trow - kGemmHalfHead : trow);
-        dma_lds16(second ? ww1 : ww0,
-                  ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
-                  dw + i * 512);
-      }
-    };
-    // wait for this wave's loads of the slab about to be computed (the
-    // STAGES - 2 later slabs, D loads each, may stay in flight), then the
-    // barrier publishes it to the workgroup and frees the buffer read one
-    // step earlier
-    // (lgkmcnt(0) too: this wave's LDS reads of the buffer about to be
-    // refilled have completed before the barrier lets a refill start)
-    constexpr int D = XW + WW;
-    constexpr int kAhead = (STAGES - 2) * D;
-    static_assert(kAhead < 64, "vmcnt holds 6 bits");
-    constexpr int kWaitOne = (kAhead & 15) | ((kAhead >> 4) << 14) | (7 << 4);
-    auto publish1 = [&]() {
-      __builtin_amdgcn_s_waitcnt(kWaitOne);
-      __builtin_amdgcn_s_barrier();
-    };
-    // slab j lives in buffer j % STAGES; the loops are unrolled by STAGES so
-    // that every buffer is a constant offset.  Loads past the last slab
-    // reload it into the free buffer (never read), so every step that a
-    // later step's wait counts on has the same loads in flight.  Only a
-    // remainder step that is the last one skips its loads (the main loop
-    // stays free of branches).
-#pragma unroll
-    for (int p = 0; p < STAGES - 1; ++p)
-      ring_load(min(p, slabs - 1), sb0 + p * kSlab);
-    int s = 0;
-    for (; s + STAGES <= slabs; s += STAGES) {
-#pragma unroll
-      for (int i = 0; i < STAGES; ++i) {
-        publish1();
-        ring_load(min(s + i + STAGES - 1, slabs - 1),
-                  sb0 + ((i + STAGES - 1) % STAGES) * kSlab);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(sb0 + i * kSlab, sb0 + i * kSlab + XB);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < STAGES - 1; ++i) {
-      if (s + i < slabs) {
-        publish1();
-        if (s + i + 1 < slabs)
-          ring_load(min(s + i + STAGES - 1, slabs - 1),
-                    sb0 + ((i + STAGES - 1) % STAGES) * kSlab);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(sb0 + i * kSlab, sb0 + i * kSlab + XB);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitLoads);
-    if (EPI != kGemmF32 && a.vec_out) {
-      __builtin_amdgcn_s_barrier();  // every wave's loads landed, ring read
-      gemm_epilogue_staged<EPI, T>(a, tm, tn, wm, wn, lane, wave, acc, sb0);
-    } else {
-      gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
-    }
-    return;
-  }
-  // slab s: this wave's loads of s done; barrier (everyone's slab s has
-  // landed, slab s - 1 has been read); slab s + 1 into the other buffer;
-  // compute s.  The buffers are named directly at every call, and the
-  // MFMAs sit in straight-line code (a branch around them makes the compiler
-  // copy every accumulator between AGPRs and VGPRs each iteration).
-  // (lgkmcnt(0) too: this wave's LDS reads of the buffer about to be
-  // refilled have completed before the barrier lets a refill start)
-  auto publish = [&]() {
-    __builtin_amdgcn_s_waitcnt(kWaitLoads & ~(15 << 8));
-    __builtin_amdgcn_s_barrier();
-  };
-  load_slab(0, sb0, sb0 + XB);
+  for (int p = 0; p < STAGES; ++p) ring_load(min(p, slabs - 1), p);
+  FragA fa0, fa1;
+  FragB fb0, fb1;
+  __builtin_amdgcn_s_waitcnt(kWaitFirst);
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, fa0, fb0);
   int s = 0;
-  // sched_barrier: the next slab's loads go out before any of this slab's
-  // reads or MFMAs (the scheduler would otherwise sink them)
   for (; s + 2 <= slabs; s += 2) {
-    publish();
-    load_slab(s + 1, sb1, sb1 + XB);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sb0, sb0 + XB);
-    publish();
-    // the last pair reloads its final slab into sb0 (never read again):
-    // the load stays unconditional and in range
-    load_slab(min(s + 2, slabs - 1), sb0, sb0 + XB);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sb1, sb1 + XB);
+    step(s, fa0, fb0, fa1, fb1);
+    step(s + 1, fa1, fb1, fa0, fb0);
   }
-  if (s < slabs) {  // odd slab count: the last slab sits in sb0
-    publish();
-    compute(sb0, sb0 + XB);
-  }
-  // no load may land in LDS after the workgroup has left (or in sb0 while
-  // it holds the staged tile)
-  __builtin_amdgcn_s_waitcnt(kWaitLoads);
+  if (s < slabs) step(s, fa0, fb0, fa1, fb1);
+  // every load landed and every LDS read done before the ring is reused
+  // for the staged tile (or the workgroup leaves)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
   if (EPI != kGemmF32 && a.vec_out) {
-    __builtin_amdgcn_s_barrier();  // every wave's loads landed, slabs read
+    __builtin_amdgcn_s_barrier();  // every wave's loads landed, ring read
     gemm_epilogue_staged<EPI, T>(a, tm, tn, wm, wn, lane, wave, acc, sb0);
   } else {
     gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
   }
 }
 
-template <int EPI, class T, int STAGES = 2>
-static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+// One launch covers the output with tiles of shape T and, when the last
+// round of T tiles would leave at least half of the CUs idle, the last
+// tail_n tile columns with tiles of half the height (TH, the same wave
+// count): those columns then take one round of half tiles instead of a
+// partial round of full ones (M = 2048, N = 14336: 768 full tiles in 3
+// rounds of 256, then 256 half tiles, instead of 3.5 rounds of full tiles).
+// Workgroup b runs on XCD b % 8 (see "Tile order"); each XCD takes a
+// contiguous range of full tiles first, then of half tiles, so the half
+// tiles are dispatched last on every XCD.
+template <int EPI, class T, int STAGES, class TH, int STAGES_H, int BK>
+__global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
+  static_assert(TH::WAVES == T::WAVES, "one workgroup size");
+  constexpr int kLds = GemmRing<T, STAGES, BK>::LDS > GemmRing<TH, STAGES_H, BK>::LDS
+                           ? GemmRing<T, STAGES, BK>::LDS
+                           : GemmRing<TH, STAGES_H, BK>::LDS;
+  static_assert(kLds * 2 <= 160 * 1024, "LDS of one CU");
+  __shared__ __attribute__((aligned(16))) uint16_t sb0[kLds];
+  const int xcd = static_cast<int>(blockIdx.x % kXcds);
+  const int j = static_cast<int>(blockIdx.x / kXcds);
+  int tm, tn;
+  // padding workgroups leave as a whole: no barrier is skipped
+  if (j < a.per_xcd) {
+    if (!gemm_tile(xcd * a.per_xcd + j, a.tiles, a.tiles_m, a.tiles_n, tm, tn)) return;
+    gemm_tile_run<EPI, T, STAGES, BK>(a, tm, tn, sb0);
+    return;
+  }
+  if constexpr (!std::is_same<T, TH>::value) {
+    if (!gemm_tile(xcd * a.hper_xcd + (j - a.per_xcd), a.htiles, a.htiles_m, a.htiles_n,
+                   tm, tn))
+      return;
+    gemm_tile_run<EPI, TH, STAGES_H, BK>(a, tm, a.tiles_n + tn, sb0);
+  }
+}
+
+// CUs of the device a stream runs on (cached per device; 256 on MI355X).
+static int gemm_device_cus(hipStream_t s) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (s != nullptr) {
+    hipDevice_t owner = 0;
+    if (hipStreamGetDevice(s, &owner) != hipSuccess) return 256;
+    dev = static_cast<int>(owner);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return 256;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
+template <int EPI, int BK, class T, int STAGES, class TH = T, int STAGES_H = STAGES>
+static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_t s) {
   const int64_t tiles_m = (a.m + T::BM - 1) / T::BM;
-  const int64_t tiles = tiles_m * tiles_n;
-  if (tiles > (int64_t{1} << 30)) return static_cast<hipError_t>(CASCADE_ESHAPE);
+  const int64_t htiles_m = (a.m + TH::BM - 1) / TH::BM;
+  int64_t tail_n = 0;
+  if (!std::is_same<T, TH>::value) {
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t rem = tiles % cus;
+    if (tiles > cus && rem > 0 && 2 * rem <= cus) {
+      const int64_t cols = (rem + tiles_m - 1) / tiles_m;
+      if (cols < tiles_n && cols * htiles_m <= cus) tail_n = cols;
+    }
+  }
+  const int64_t tiles = tiles_m * (tiles_n - tail_n);
+  const int64_t htiles = htiles_m * tail_n;
+  if (tiles + htiles > (int64_t{1} << 30)) return static_cast<hipError_t>(CASCADE_ESHAPE);
   a.tiles_m = static_cast<int32_t>(tiles_m);
-  a.tiles_n = static_cast<int32_t>(tiles_n);
+  a.tiles_n = static_cast<int32_t>(tiles_n - tail_n);
   a.tiles = static_cast<int32_t>(tiles);
+  a.per_xcd = static_cast<int32_t>((tiles + kXcds - 1) / kXcds);
+  a.htiles_m = static_cast<int32_t>(htiles_m);
+  a.htiles_n = static_cast<int32_t>(tail_n);
+  a.htiles = static_cast<int32_t>(htiles);
+  a.hper_xcd = static_cast<int32_t>((htiles + kXcds - 1) / kXcds);
   // 16-byte output accesses need 16-byte aligned rows in every buffer the
   // epilogue touches; otherwise the element-wise epilogue runs
   auto ok16 = [](const void *p) { return p == nullptr || aligned16(p); };
   a.vec_out = (a.ldy % 8 == 0) && ok16(a.y) && ok16(a.aux) && ok16(a.rope_cos) &&
               ok16(a.rope_sin) && ok16(a.k_out) && ok16(a.v_out) &&
               (a.kv_head_stride % 8 == 0);
-  const int64_t grid = (tiles + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(gemm_kernel<EPI, T, STAGES>, dim3(static_cast<unsigned>(grid)),
-                       dim3(T::WAVES * kWave), 0, s, a);
+  const int64_t grid = static_cast<int64_t>(kXcds) * (a.per_xcd + a.hper_xcd);
+  return launch_kernel(gemm_kernel<EPI, T, STAGES, TH, STAGES_H, BK>,
+                       dim3(static_cast<unsigned>(grid)), dim3(T::WAVES * kWave), 0, s, a);
 }
 
-// 128-row tiles unless they would leave CUs idle: at most 64 rows of X
-// (short prefills) or fewer 128-row tiles than the 256 CUs (the K / V
-// projections, N = 1024, at M = 2048) take 64-row tiles.
+// 256-row tiles when there are at least as many as CUs (a partial last
+// round runs as 128-row half tiles); else 128-row tiles (a partial last
+// round as 64-row half tiles), unless there are fewer of those than CUs or
+// at most 64 rows of X: then 64-row tiles (the K / V projections, N = 1024,
+// at M = 2048, and short prompts).
 template <int EPI>
 static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+  const int cus = gemm_device_cus(s);
   const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
-  if (a.m > 128 && tiles256 >= 256) return launch_tiles<EPI, GemmTile256, 3>(a, tiles_n, s);
+  if (a.m > 128 && tiles256 >= cus)
+    return launch_tiles<EPI, kTileK, GemmTile256, 3, GemmTile128x8, 4>(a, tiles_n, cus, s);
   const int64_t tiles128 = (a.m + 127) / 128 * tiles_n;
-  if (a.m <= 64 || tiles128 < 256) return launch_tiles<EPI, GemmTile64, 4>(a, tiles_n, s);
-  return launch_tiles<EPI, GemmTile128>(a, tiles_n, s);
+  if (a.m <= 64 || tiles128 < cus) return launch_tiles<EPI, kTileK, GemmTile64, 6>(a, tiles_n, cus, s);
+  return launch_tiles<EPI, kTileK, GemmTile128, 4, GemmTile64, 6>(a, tiles_n, cus, s);
 }
 
 // Shared argument checks: X [m, k], K a multiple of the 64-deep slab.

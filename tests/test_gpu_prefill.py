@@ -48,9 +48,9 @@ def linear_bound_report(actual, x, w):
     (2048, 1024, 448), (40, 512, 1088)])
 def test_gemm_matches_oracle(gpu_device, m, n, k):
     # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs.
-    # Slab rings (K / 64 slabs): 256-row tiles (3 slabs) at 3 and 5 slabs
-    # (no remainder, remainder 2); 64-row tiles (4 slabs) at 6, 7 and 17
-    # slabs (main loop plus a remainder of 2, 3 and 1), besides 1, 2, 64, 224
+    # Slab counts (K / 64): odd and even counts (1, 2, 3, 5, 6, 7, 17, 64,
+    # 224) below and above the ring depth of each tile shape (256-row
+    # tiles: 3 buffers; 128-row: 4; 64-row: 6)
     print("gemm m={} n={} k={}".format(m, n, k), flush=True)
     dev = gpu_device
     x = cases.normal_bf16((m, k), 101)
@@ -121,6 +121,48 @@ def test_swiglu_gemm_fused_and_split_match_oracle(gpu_device, m):
     _hip.up_mul_gemm(xd, wud, g, split)
     r = cases.compare(g, gate)
     assert r["ok"], r
+    assert torch.equal(fused.cpu(), split.cpu())
+
+
+# Shapes whose last round of full tiles would leave at least half of the
+# 256 CUs idle: the last tile columns run as half-height tiles in the same
+# launch (256-row tiles with 128-row halves; 128-row tiles with 64-row
+# halves), through every epilogue.
+@pytest.mark.parametrize("m,n,k", [(512, 20480, 256), (200, 18432, 128),
+                                   (1100, 14336, 128)])
+def test_gemm_half_tile_tail_matches_oracle(gpu_device, m, n, k):
+    print("half-tile tail m={} n={} k={}".format(m, n, k), flush=True)
+    dev = gpu_device
+    x = cases.normal_bf16((m, k), 161)
+    w = cases.normal_bf16((n, k), 162, 0.05)
+    w2 = cases.normal_bf16((n, k), 163, 0.05)
+    res = cases.normal_bf16((m, n), 164)
+    xd, wd, w2d = x.to(dev), w.to(dev), w2.to(dev)
+    lin = ref.linear(x, w)
+    y = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm(xd, wd, y)
+    assert linear_bound_report(y, x, w) <= 1.0
+    r = cases.compare(y, lin)
+    assert r["ok"], r
+    yf = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _hip.gemm_f32out(xd, wd, yf)
+    r = cases.compare(yf, ref.linear_exact(x, w).float(), atol=1e-4, rtol=1e-4)
+    assert r["ok"], r
+    out = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm_residual(xd, wd, res.to(dev), out)
+    r = cases.compare(out, res + lin)
+    assert r["ok"], r
+    gate = F.silu(lin)
+    g = torch.empty((m, n), dtype=BF16, device=dev)
+    split = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gate_silu_gemm(xd, wd, g)
+    _hip.up_mul_gemm(xd, w2d, g, split)
+    r = cases.compare(g, gate)
+    assert r["ok"], r
+    r = cases.compare(split, gate * ref.linear(x, w2))
+    assert r["ok"], r
+    fused = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gate_up_swiglu_gemm(xd, wd, w2d, fused)
     assert torch.equal(fused.cpu(), split.cpu())
 
 
