@@ -342,6 +342,9 @@ def resident_decode(args):
                 "last_token": int(decoder.tokens()[0, -1]),
             }
             decoder.close()
+    prefill = None
+    if not args.no_prefill:
+        prefill = resident_prefill(args, executor, runtime, dev)
     mean_context = args.context + args.warmup + (args.steps - 1) / 2.0
     result = {
         "ms_per_step": ms_per_step,
@@ -356,9 +359,75 @@ def resident_decode(args):
     }
     if graph is not None:
         result["decode_graph"] = graph
+    if prefill is not None:
+        result["prefill_resident"] = prefill
     del executor, runtime, resident, cache
     torch.cuda.empty_cache()
     return result
+
+
+# Resident prefill launch groups of the matrix_group granularity: fused
+# q|k|v (+ RoPE + KV write) and gate|up (+ SwiGLU) GEMMs, and their
+# multiply-accumulates per token row.
+RESIDENT_PREFILL_GEMMS = (
+    ("qkv_rope", "gemm_qkv", (HIDDEN + 2 * 1024) * HIDDEN),
+    ("o_proj", "gemm_o", HIDDEN * HIDDEN),
+    ("gate_up_swiglu", "gemm_gate_up", 2 * INTER * HIDDEN),
+    ("down_proj", "gemm_down", HIDDEN * INTER),
+)
+
+
+def resident_prefill(args, executor, runtime, dev):
+    """A 2048-token prefill through the config-4 executor, weights resident:
+    the prefill GEMMs and causal attention back to back (no H2D waits
+    between launches), as a compute-bound counterpart of config 5."""
+
+    import torch
+
+    tokens = args.prefill_tokens
+    gen = torch.Generator().manual_seed(args.seed + 3)
+    prompt = torch.randint(0, VOCAB, (1, tokens), generator=gen).to(dev)
+    groups = {name: LAYERS for _, name, _ in RESIDENT_PREFILL_GEMMS}
+    groups["prefill_attention"] = LAYERS
+    walls = []
+    with torch.inference_mode():
+        # warm-up, timed prefills, then one with every launch timed
+        for rep in range(1 + args.prefill_repeats + 1):
+            executor.kv_cache.clear()
+            last = rep == args.prefill_repeats + 1
+            if last:
+                for name, count in groups.items():
+                    executor.instrument(name, count)
+            torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            executor.finish(runtime.run(executor, executor.begin(prompt)))
+            torch.cuda.synchronize(dev)
+            wall = (time.perf_counter() - t0) * 1000.0
+            log("resident prefill {} {:.1f} ms{}".format(rep, wall, " (profiled)" if last else ""))
+            if 0 < rep and not last:
+                walls.append(wall)
+    executor.check_errors()
+    gemms = {}
+    for label, group, macs in RESIDENT_PREFILL_GEMMS:
+        avg = statistics.mean(executor.kernel_times_ms(group))
+        tflops = 2.0 * tokens * macs / (avg * 1e-3) / 1e12
+        gemms[label] = {"avg_us": round(1000 * avg, 1), "tflops": round(tflops, 1),
+                        "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    attn = statistics.mean(executor.kernel_times_ms("prefill_attention"))
+    attn_tflops = 4.0 * 32 * 128 * tokens * (tokens + 1) / 2 / (attn * 1e-3) / 1e12
+    median = statistics.median(walls)
+    return {
+        "workload": "{}-token random-ID prompt through the config-4 executor "
+                    "(matrix_group, all weights HBM-resident): 1 warm-up + {} "
+                    "timed prefills + 1 with every GEMM and attention launch "
+                    "timed".format(tokens, args.prefill_repeats),
+        "prefill_ms_median": round(median, 2),
+        "prompt_tokens_per_s": round(tokens / (median / 1e3), 1),
+        "gemm": gemms,
+        "attention": {"avg_us": round(1000 * attn, 1), "tflops": round(attn_tflops, 1),
+                      "mfma_frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+    }
 
 
 # ------------------------------------------------- config 3 (H2D streamed)
@@ -813,6 +882,8 @@ def main():
     }
     if "decode_graph" in resident:
         line["decode_graph"] = resident["decode_graph"]
+    if "prefill_resident" in resident:
+        line["prefill_resident"] = resident["prefill_resident"]
     if not args.no_streamed:
         s = streamed_decode(args)
         line["streamed"] = {

@@ -20,6 +20,49 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Buffer resource over [base, base + bytes) as four words (for inline asm):
+// base, stride 0, num_records, raw-buffer flags.  Loads past num_records
+// return zeros.
+__device__ __forceinline__ u32x4 buffer_rsrc_words(const void *base, int64_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
+  r.z = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bytes));
+  r.w = 0x00020000u;
+  return r;
+}
+
+// LDS byte address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const void *)p)));
+}
+
+// buffer_load_dwordx4 ... lds issued from inline asm: lane l's 16 bytes at
+// voffset land at LDS byte address (lds + 16 l).  The compiler does not see
+// these loads, so it adds no vmcnt waits of its own for them (the caller
+// waits with an explicit s_waitcnt); the memory clobber keeps LDS accesses
+// from moving across the issue.  The descriptor words pass through
+// readfirstlane (a no-op on values the compiler already keeps in SGPRs):
+// where it cannot prove a selected descriptor uniform it would otherwise
+// hand the asm VGPRs.
+__device__ __forceinline__ void dma_lds16(const u32x4 &rsrc, int voff, uint32_t lds) {
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(rsrc.x);
+  r.y = __builtin_amdgcn_readfirstlane(rsrc.y);
+  r.z = __builtin_amdgcn_readfirstlane(rsrc.z);
+  r.w = __builtin_amdgcn_readfirstlane(rsrc.w);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+
+// s_waitcnt immediate: vmcnt(vm) lgkmcnt(lgkm), expcnt left alone.
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }

@@ -450,36 +450,6 @@ struct DmaSlab {
   static_assert(BK == 32 || BK == 64, "slab depth");
 };
 
-// Buffer resource over [base, base + bytes) as four words (for inline asm):
-// base, stride 0, num_records, raw-buffer flags.
-__device__ __forceinline__ u32x4 gemm_rsrc_words(const uint16_t *base, int64_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
-  r.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
-  r.z = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bytes));
-  r.w = 0x00020000u;
-  return r;
-}
-
-// buffer_load_dwordx4 ... lds issued from inline asm: lane l's 16 bytes at
-// voffset land at LDS byte address (lds + 16 l).  The compiler does not see
-// these loads, so it adds no vmcnt waits of its own for them (the caller
-// waits); the memory clobber keeps LDS accesses from moving across the
-// issue.  The descriptor words pass through readfirstlane (a no-op on values
-// the compiler already keeps in SGPRs): where it cannot prove a selected
-// descriptor uniform it would otherwise hand the asm VGPRs.
-__device__ __forceinline__ void dma_lds16(const u32x4 &rsrc, int voff, uint32_t lds) {
-  u32x4 r;
-  r.x = __builtin_amdgcn_readfirstlane(rsrc.x);
-  r.y = __builtin_amdgcn_readfirstlane(rsrc.y);
-  r.z = __builtin_amdgcn_readfirstlane(rsrc.z);
-  r.w = __builtin_amdgcn_readfirstlane(rsrc.w);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
-
 // Ring geometry of a tile shape: bf16 elements of one slab buffer (X rows,
 // then W rows), and of the LDS a workgroup needs (the ring, or the staged
 // output tile of the vectorised epilogue, which reuses it).
@@ -534,9 +504,9 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
     wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kTileN;
     wbase1 = wbase0; wrows1 = wrows0; wrow1 = wrow0;
   }
-  const u32x4 xw = gemm_rsrc_words(a.x, a.m * k_bytes);
-  const u32x4 ww0 = gemm_rsrc_words(wbase0, wrows0 * k_bytes);
-  const u32x4 ww1 = gemm_rsrc_words(wbase1, wrows1 * k_bytes);
+  const u32x4 xw = buffer_rsrc_words(a.x, a.m * k_bytes);
+  const u32x4 ww0 = buffer_rsrc_words(wbase0, wrows0 * k_bytes);
+  const u32x4 ww1 = buffer_rsrc_words(wbase1, wrows1 * k_bytes);
 
   // lane part of a load: row L / CH of the instruction's RPI rows, physical
   // chunk L % CH, i.e. logical chunk (L % CH) ^ f(row); f depends on the
@@ -564,8 +534,7 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   const int slabs = static_cast<int>(a.k / BK);
   // LDS byte address of sb0 (the ring's buffer b starts kSlab * 2 b bytes
   // later)
-  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)sb0)));
+  const uint32_t ring_lds = lds_address(sb0);
   // The whole byte offset goes in voffset: the buffer range check covers
   // voffset (not soffset), so rows past the end read as zeros instead of
   // leaving the allocation.  Offsets stay below 2^31 (checked on the host).
@@ -607,9 +576,9 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   constexpr int kAhead = (STAGES - 2) * D;
   constexpr int kAheadFirst = (STAGES - 1) * D;
   static_assert(kAheadFirst < 64, "vmcnt holds 6 bits");
-  constexpr int kWaitStep = (kAhead & 15) | ((kAhead >> 4) << 14) | (7 << 4);
-  constexpr int kWaitFirst = (kAheadFirst & 15) | ((kAheadFirst >> 4) << 14) | (7 << 4);
-  constexpr int kWaitAll = 7 << 4;  // vmcnt(0) lgkmcnt(0)
+  constexpr int kWaitStep = waitcnt_imm(kAhead, 0);
+  constexpr int kWaitFirst = waitcnt_imm(kAheadFirst, 0);
+  constexpr int kWaitAll = waitcnt_imm(0, 0);
   constexpr int KS = BK / 32;
   constexpr int kReads = KS * (T::FM + T::FN);
   constexpr int kMfmas = KS * T::FM * T::FN;
