@@ -430,6 +430,109 @@ def resident_prefill(args, executor, runtime, dev):
     }
 
 
+# One decoder layer's seven projections, as the prefill's matrix-granularity
+# launches: (name, [N, K], epilogue).
+SWEEP_ROWS = (16, 64, 256, 1024, 2048, 4096, 8192, 16384, 32768)
+LAYER_MACS = (HIDDEN + 2 * 1024 + HIDDEN + 3 * INTER) * HIDDEN  # 218,103,808
+
+
+def prefill_sweep(args):
+    """The copy/compute crossover of a streamed prefill, measured the way the
+    reference measures it (an M sweep of one layer's projections,
+    benchmarks/torch_llama32_1b_bench.py:351-385): one layer's seven
+    projections through this library's prefill GEMMs at M prompt rows --
+    q, k, v, o (+ residual), gate (+ SiLU), up (* gate), down (+ residual),
+    each weight ~ N(0, 0.02) and read from HBM -- timed back to back with
+    HIP events (2 warm-up + 5 timed passes, median), against the time one
+    layer's 436 MB take over PCIe from pinned host memory (5 timed copies
+    with this library's hipMemcpyAsync, median)."""
+
+    import torch
+    from layer_streaming import _hip
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 4)
+
+    def draw(*shape, scale=0.02):
+        return (torch.randn(*shape, generator=gen, device=dev) * scale).to(torch.bfloat16)
+
+    wq, wk, wv, wo = draw(HIDDEN, HIDDEN), draw(1024, HIDDEN), draw(1024, HIDDEN), draw(HIDDEN, HIDDEN)
+    wg, wu, wd = draw(INTER, HIDDEN), draw(INTER, HIDDEN), draw(HIDDEN, INTER)
+    layer_bytes = LAYER_MACS * 2
+    # the layer's copy time over PCIe
+    host = torch.empty(LAYER_MACS, dtype=torch.bfloat16, pin_memory=True)
+    slot = torch.empty(LAYER_MACS, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.Stream(dev)
+    copies = []
+    for rep in range(2 + 5):
+        a = _hip.HipEvent(enable_timing=True)
+        b = _hip.HipEvent(enable_timing=True)
+        a.record(stream)
+        _hip.memcpy_h2d_async(slot, host, layer_bytes, stream)
+        b.record(stream)
+        b.synchronize()
+        if rep >= 2:
+            copies.append(a.elapsed_time(b))
+    copy_ms = statistics.median(copies)
+    del host, slot
+    rows = []
+    for m in SWEEP_ROWS:
+        x = draw(m, HIDDEN, scale=1.0)
+        q = torch.empty(m, HIDDEN, dtype=torch.bfloat16, device=dev)
+        k = torch.empty(m, 1024, dtype=torch.bfloat16, device=dev)
+        v = torch.empty_like(k)
+        h = torch.zeros(m, HIDDEN, dtype=torch.bfloat16, device=dev)
+        g = torch.empty(m, INTER, dtype=torch.bfloat16, device=dev)
+        u = torch.empty_like(g)
+
+        def layer():
+            _hip.gemm(x, wq, q)
+            _hip.gemm(x, wk, k)
+            _hip.gemm(x, wv, v)
+            _hip.gemm_residual(q, wo, h, h)
+            _hip.gate_silu_gemm(x, wg, g)
+            _hip.up_mul_gemm(x, wu, g, u)
+            _hip.gemm_residual(u, wd, h, h)
+
+        times = []
+        for rep in range(2 + 5):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            layer()
+            b.record()
+            b.synchronize()
+            if rep >= 2:
+                times.append(a.elapsed_time(b))
+        ms = statistics.median(times)
+        tflops = 2.0 * LAYER_MACS * m / (ms * 1e-3) / 1e12
+        rows.append({"rows_M": m, "gpu_elapsed_ms": round(ms, 4),
+                     "effective_tflops": round(tflops, 1),
+                     "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "nominal_weight_gbps": round(layer_bytes / 1e9 / (ms / 1e3), 1),
+                     "compute_over_copy": round(ms / copy_ms, 4)})
+        log("prefill sweep M={}: {:.3f} ms, {:.1f} TFLOP/s".format(m, ms, tflops))
+        del x, q, k, v, h, g, u
+    crossover = None
+    for lo, hi in zip(rows, rows[1:]):
+        if lo["compute_over_copy"] < 1.0 <= hi["compute_over_copy"]:
+            # compute time is linear in M between the two sweep points
+            f = (1.0 - lo["compute_over_copy"]) / (hi["compute_over_copy"] - lo["compute_over_copy"])
+            crossover = int(round(lo["rows_M"] + f * (hi["rows_M"] - lo["rows_M"])))
+    del wq, wk, wv, wo, wg, wu, wd
+    torch.cuda.empty_cache()
+    return {
+        "workload": "one layer's seven projections (q, k, v, o + residual, "
+                    "gate + SiLU, up * gate, down + residual) at M prompt rows, "
+                    "weights read from HBM; 2 warm-up + 5 timed passes per M",
+        "layer_weight_bytes": layer_bytes,
+        "layer_copy_ms": round(copy_ms, 3),
+        "layer_copy_gbps": round(layer_bytes / 1e9 / (copy_ms / 1e3), 2),
+        "rows": rows,
+        "crossover_rows_M": crossover,
+    }
+
+
 # ------------------------------------------------- config 3 (H2D streamed)
 
 
@@ -905,6 +1008,7 @@ def main():
         }
     if not args.no_prefill:
         line["prefill"] = prefill_streamed(args)
+        line["prefill_sweep"] = prefill_sweep(args)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(line), flush=True)
