@@ -747,13 +747,122 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_
                        dim3(static_cast<unsigned>(grid)), dim3(T::WAVES * kWave), 0, s, a);
 }
 
-// 256-row tiles when there are at least as many as CUs (a partial last
-// round runs as 128-row half tiles); else 128-row tiles (a partial last
-// round as 64-row half tiles), unless there are fewer of those than CUs or
-// at most 64 rows of X: then 64-row tiles (the K / V projections, N = 1024,
-// at M = 2048, and short prompts).
+// Short prompts (M <= 16 rows).  The weights are nearly all the traffic, and
+// 64-row tiles would leave N / 128 workgroups to stream them.  Here a
+// workgroup computes one pair of 16-column fragments of a 128-column tile
+// (the columns of wave column wn of a GemmTileSkinny, so the epilogues'
+// pairing of column c with c + 64 holds) for all M rows, with K split over
+// its kSkinnyWaves waves: each wave loads its K range of the X rows (the
+// MFMA A operand, rows past M reading as zeros) and of the 32 W rows (the B
+// operand, 16 bytes a lane straight from memory, nontemporal), and the
+// waves' fp32 partials are summed through LDS in wave order before wave 0
+// runs the element-wise epilogue.  4 x more workgroups than 128-column
+// tiles: q / o / down_proj 128, gate / up 448.
+using GemmTileSkinny = GemmTile<16, 1, 4>;
+constexpr int kSkinnyWaves = 16;
+constexpr int kSkinnyRows = 16;  // prompt rows one launch covers
+constexpr int kSkinnyUnroll = 8;  // 32-deep K chunks loaded before their MFMAs
+
+template <int EPI>
+__global__ __launch_bounds__(kSkinnyWaves *kWave) void gemm_skinny_kernel(GemmArgs a) {
+  using T = GemmTileSkinny;
+  __shared__ f32x4 partial[kSkinnyWaves][T::FN][kWave];
+  const int tn = static_cast<int>(blockIdx.x) / T::WN;
+  const int wn = static_cast<int>(blockIdx.x) % T::WN;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int lr = lane & 15;
+  const int g4 = lane >> 4;
+
+  // W row of fragment j for this lane's column (tile column gemm_col).
+  // Rows past the matrix (and X rows past M) are clamped to row 0 instead
+  // of predicated: they only feed output columns (rows) the epilogue never
+  // stores, and every load stays unconditional.
+  const uint16_t *wrow[T::FN];
+#pragma unroll
+  for (int j = 0; j < T::FN; ++j) {
+    const int tc = gemm_col<T>(wn, j, lr);
+    const uint16_t *base;
+    int64_t rows, row;
+    if constexpr (EPI == kGemmSwiglu) {
+      base = tc < kGemmHalfHead ? a.w0 : a.w1;
+      rows = a.n0;
+      row = static_cast<int64_t>(tn) * kGemmHalfHead + (tc % kGemmHalfHead);
+    } else if constexpr (EPI == kGemmQkvRope) {
+      const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
+      if (tn < hq) {
+        base = a.w0; rows = a.n0; row = static_cast<int64_t>(tn) * kGemmHead + tc;
+      } else if (tn < hq + hk) {
+        base = a.w1; rows = a.n1; row = (tn - hq) * kGemmHead + tc;
+      } else {
+        base = a.w2; rows = a.n2; row = (tn - hq - hk) * kGemmHead + tc;
+      }
+    } else {
+      base = a.w0; rows = a.n0; row = static_cast<int64_t>(tn) * kTileN + tc;
+    }
+    wrow[j] = base + (row < rows ? row : 0) * a.k;
+  }
+  const uint16_t *xrow = a.x + (lr < a.m ? lr : 0) * a.k;
+
+  // wave w takes 32-deep K chunks [c_begin, c_end); a batch of
+  // kSkinnyUnroll chunks is loaded before its MFMAs, chunks past c_end
+  // load chunk c_end - 1 and enter the MFMAs as zeros
+  const int chunks = static_cast<int>(a.k / 32);
+  const int per = (chunks + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int c_begin = min(wave * per, chunks);
+  const int c_end = min(c_begin + per, chunks);
+  f32x4 acc[1][T::FN];
+#pragma unroll
+  for (int j = 0; j < T::FN; ++j) acc[0][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = c_begin; c < c_end; c += kSkinnyUnroll) {
+    u32x4 xa[kSkinnyUnroll], wb[kSkinnyUnroll][T::FN];
+#pragma unroll
+    for (int u = 0; u < kSkinnyUnroll; ++u) {
+      const int64_t k0 = static_cast<int64_t>(min(c + u, c_end - 1)) * 32 + 8 * g4;
+      xa[u] = *reinterpret_cast<const u32x4 *>(xrow + k0);
+#pragma unroll
+      for (int j = 0; j < T::FN; ++j)
+        wb[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow[j] + k0));
+    }
+    // every load of the batch is in flight before the first MFMA waits
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kSkinnyUnroll; ++u) {
+      if (c + u >= c_end) xa[u] = u32x4{0u, 0u, 0u, 0u};  // wave-uniform
+#pragma unroll
+      for (int j = 0; j < T::FN; ++j) acc[0][j] = mfma_16x16x32_bf16(xa[u], wb[u][j], acc[0][j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < T::FN; ++j) partial[wave][j][lane] = acc[0][j];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int j = 0; j < T::FN; ++j) {
+    f32x4 sum = partial[0][j][lane];
+    for (int w = 1; w < kSkinnyWaves; ++w) sum += partial[w][j][lane];
+    acc[0][j] = sum;
+  }
+  gemm_epilogue<EPI, T>(a, 0, tn, 0, wn, lane, acc);
+}
+
+template <int EPI>
+static hipError_t launch_skinny(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+  const int64_t grid = tiles_n * GemmTileSkinny::WN;
+  if (grid > (int64_t{1} << 30)) return static_cast<hipError_t>(CASCADE_ESHAPE);
+  return launch_kernel(gemm_skinny_kernel<EPI>, dim3(static_cast<unsigned>(grid)),
+                       dim3(kSkinnyWaves * kWave), 0, s, a);
+}
+
+// At most 16 rows of X: the skinny kernel.  Else 256-row tiles when there
+// are at least as many as CUs (a partial last round runs as 128-row half
+// tiles); else 128-row tiles (a partial last round as 64-row half tiles),
+// unless there are fewer of those than CUs or at most 64 rows of X: then
+// 64-row tiles (the K / V projections, N = 1024, at M = 2048, and short
+// prompts).
 template <int EPI>
 static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
+  if (a.m <= kSkinnyRows) return launch_skinny<EPI>(a, tiles_n, s);
   const int cus = gemm_device_cus(s);
   const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
   if (a.m > 128 && tiles256 >= cus)

@@ -45,8 +45,10 @@ def linear_bound_report(actual, x, w):
     (257, 4096, 14336), (1, 256, 4096), (300, 28672, 4096),
     (5, 1000, 4096), (129, 200, 128), (7, 1001, 128),
     (2048, 4096, 192), (2048, 4096, 320), (2048, 1024, 384),
-    (2048, 1024, 448), (40, 512, 1088)])
+    (2048, 1024, 448), (40, 512, 1088), (16, 4096, 4096), (11, 1024, 14336),
+    (17, 384, 4096)])
 def test_gemm_matches_oracle(gpu_device, m, n, k):
+    # m <= 16: the skinny kernel (K split over a workgroup's waves);
     # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs.
     # Slab counts (K / 64): odd and even counts (1, 2, 3, 5, 6, 7, 17, 64,
     # 224) below and above the ring depth of each tile shape (256-row
@@ -101,7 +103,7 @@ def test_gemm_residual_matches_oracle(gpu_device, m, n, k):
     assert torch.equal(out.cpu(), res + xs)
 
 
-@pytest.mark.parametrize("m", [2, 6, 200, 700])
+@pytest.mark.parametrize("m", [2, 6, 16, 200, 700])
 def test_swiglu_gemm_fused_and_split_match_oracle(gpu_device, m):
     dev = gpu_device
     inter, hidden = 14336, 4096
@@ -172,7 +174,7 @@ def _rope_tables(positions):
     return cos[:, :64].contiguous(), sin[:, :64].contiguous()
 
 
-@pytest.mark.parametrize("m,pos0", [(6, 0), (2048, 0), (33, 4000), (2, 32766)])
+@pytest.mark.parametrize("m,pos0", [(6, 0), (16, 100), (2048, 0), (33, 4000), (2, 32766)])
 def test_qkv_rope_gemm_matches_oracle(gpu_device, m, pos0):
     print("qkv_rope_gemm m={} pos0={}".format(m, pos0), flush=True)
     dev = gpu_device
