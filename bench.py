@@ -432,7 +432,7 @@ def resident_prefill(args, executor, runtime, dev):
 
 # One decoder layer's seven projections, as the prefill's matrix-granularity
 # launches: (name, [N, K], epilogue).
-SWEEP_ROWS = (16, 64, 256, 1024, 2048, 4096, 8192, 16384, 32768)
+SWEEP_ROWS = (16, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768)
 LAYER_MACS = (HIDDEN + 2 * 1024 + HIDDEN + 3 * INTER) * HIDDEN  # 218,103,808
 
 

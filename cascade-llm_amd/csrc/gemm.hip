@@ -747,114 +747,194 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_
                        dim3(static_cast<unsigned>(grid)), dim3(T::WAVES * kWave), 0, s, a);
 }
 
-// Short prompts (M <= 16 rows).  The weights are nearly all the traffic, and
-// 64-row tiles would leave N / 128 workgroups to stream them.  Here a
-// workgroup computes one pair of 16-column fragments of a 128-column tile
-// (the columns of wave column wn of a GemmTileSkinny, so the epilogues'
-// pairing of column c with c + 64 holds) for all M rows, with K split over
-// its kSkinnyWaves waves: each wave loads its K range of the X rows (the
-// MFMA A operand, rows past M reading as zeros) and of the 32 W rows (the B
-// operand, 16 bytes a lane straight from memory, nontemporal), and the
-// waves' fp32 partials are summed through LDS in wave order before wave 0
-// runs the element-wise epilogue.  4 x more workgroups than 128-column
-// tiles: q / o / down_proj 128, gate / up 448.
-using GemmTileSkinny = GemmTile<16, 1, 4>;
-constexpr int kSkinnyWaves = 16;
-constexpr int kSkinnyRows = 16;  // prompt rows one launch covers
-constexpr int kSkinnyUnroll = 8;  // 32-deep K chunks loaded before their MFMAs
+// Short prompts (M <= 64 rows).  The weights are nearly all the traffic, so
+// they must stream at HBM rate, which needs long runs of one row per load
+// (64-byte pieces of 16 rows per instruction, the layout of an MFMA operand,
+// stream at only 2-3 TB/s).  A workgroup computes one pair of 16-column
+// fragments of a 128-column tile (the columns of wave column wn of a
+// GemmTile<MR, 1, 4>, so the epilogues' pairing of column c with c + 64
+// holds) for all M rows.  K is walked in slabs through a ring of LDS
+// buffers: every load instruction moves 1 KiB, one or two whole row runs
+// of a slab (the 32 W rows and the MR X rows; rows past M or past a matrix
+// read as zeros through the buffer bounds, and K past a short last slab
+// is never used), each instruction's kilobyte lands after 16 bytes of
+// padding so the fragment reads of 16 rows spread over the banks, and each
+// wave runs the MFMAs of its quarter of a slab's K.  The waves' fp32 partials are summed through LDS in wave
+// order and wave 0 runs the element-wise epilogue.
+template <int MR>
+struct SkinnyShape {
+  using T = GemmTile<MR, 1, 4>;  // one 16 x 32 column pair of MR rows per workgroup
+  static constexpr int SLAB_K = MR == 16 ? 512 : 256;
+  static constexpr int RUN = SLAB_K * 2;          // bytes of one row in a slab
+  static constexpr int RPI = 1024 / RUN;          // rows per load instruction (1 KiB)
+  static constexpr int LINE = 1024 + 16;          // LDS pitch of one instruction's rows
+  static constexpr int SLAB_ROWS = 2 * 16 + MR;   // W rows of the pair, X rows
+  static constexpr int STAGES = 3;
+  static constexpr int WAVES = 4;
+  static constexpr int LOADS = SLAB_ROWS / RPI / WAVES;  // per wave and slab
+  static_assert(SLAB_ROWS % (RPI * WAVES) == 0, "whole instructions per wave");
+  static_assert(16 % RPI == 0, "an instruction's rows stay in one operand");
+};
+// Prompt rows the skinny kernels cover.  A 128-row shape (128-deep slabs,
+// 256-byte runs) measured slower than 64-row tiles at M = 128 (the layer
+// of seven projections 0.460 against 0.311 ms).
+constexpr int kSkinnyRows = 64;
 
-template <int EPI>
-__global__ __launch_bounds__(kSkinnyWaves *kWave) void gemm_skinny_kernel(GemmArgs a) {
-  using T = GemmTileSkinny;
-  __shared__ f32x4 partial[kSkinnyWaves][T::FN][kWave];
+// Slab row r (W rows of fragments 0 and 1, then X rows) sits at LDS byte
+// (r / RPI) * LINE + (r % RPI) * RUN of its buffer.  With 512-byte runs two
+// rows share one 1 KiB line, so a fragment read (16 rows) meets each bank
+// group twice; with 1 KiB runs, once.
+template <int EPI, int MR>
+__global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_kernel(GemmArgs a) {
+  using S = SkinnyShape<MR>;
+  using T = typename S::T;
+  constexpr int kSlabBytes = S::SLAB_ROWS / S::RPI * S::LINE;
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S::STAGES * kSlabBytes];
+  static_assert(S::WAVES * T::FM * T::FN * kWave * sizeof(f32x4) <= sizeof(ring),
+                "the reduction fits in the ring");
   const int tn = static_cast<int>(blockIdx.x) / T::WN;
   const int wn = static_cast<int>(blockIdx.x) % T::WN;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lr = lane & 15;
   const int g4 = lane >> 4;
+  const int64_t row_bytes = a.k * 2;
 
-  // W row of fragment j for this lane's column (tile column gemm_col).
-  // Rows past the matrix (and X rows past M) are clamped to row 0 instead
-  // of predicated: they only feed output columns (rows) the epilogue never
-  // stores, and every load stays unconditional.
-  const uint16_t *wrow[T::FN];
-#pragma unroll
-  for (int j = 0; j < T::FN; ++j) {
-    const int tc = gemm_col<T>(wn, j, lr);
-    const uint16_t *base;
-    int64_t rows, row;
+  // the matrix, and the row in it, of W slab row r (r < 32: fragment r / 16,
+  // tile column gemm_col(wn, r / 16, r % 16)); rows past a matrix read as
+  // zeros through its buffer bounds
+  auto w_row = [&](int r, const uint16_t *&base, int64_t &rows) -> int64_t {
+    const int j = r / 16;
+    const int tc = gemm_col<T>(wn, j, r % 16);
     if constexpr (EPI == kGemmSwiglu) {
       base = tc < kGemmHalfHead ? a.w0 : a.w1;
       rows = a.n0;
-      row = static_cast<int64_t>(tn) * kGemmHalfHead + (tc % kGemmHalfHead);
+      return static_cast<int64_t>(tn) * kGemmHalfHead + (tc % kGemmHalfHead);
     } else if constexpr (EPI == kGemmQkvRope) {
       const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
       if (tn < hq) {
-        base = a.w0; rows = a.n0; row = static_cast<int64_t>(tn) * kGemmHead + tc;
-      } else if (tn < hq + hk) {
-        base = a.w1; rows = a.n1; row = (tn - hq) * kGemmHead + tc;
-      } else {
-        base = a.w2; rows = a.n2; row = (tn - hq - hk) * kGemmHead + tc;
+        base = a.w0; rows = a.n0; return static_cast<int64_t>(tn) * kGemmHead + tc;
       }
+      if (tn < hq + hk) {
+        base = a.w1; rows = a.n1; return (tn - hq) * kGemmHead + tc;
+      }
+      base = a.w2; rows = a.n2; return (tn - hq - hk) * kGemmHead + tc;
     } else {
-      base = a.w0; rows = a.n0; row = static_cast<int64_t>(tn) * kTileN + tc;
+      base = a.w0; rows = a.n0; return static_cast<int64_t>(tn) * kTileN + tc;
     }
-    wrow[j] = base + (row < rows ? row : 0) * a.k;
+  };
+  // this wave's load instructions: a buffer over the operand's matrix and
+  // the lane's byte offset of slab 0 (its row of the instruction, then
+  // 16 bytes a lane along that row)
+  constexpr int kLanesPerRow = kWave / S::RPI;
+  u32x4 rsrc[S::LOADS];
+  int voff[S::LOADS];
+#pragma unroll
+  for (int t = 0; t < S::LOADS; ++t) {
+    const int r0 = (wave * S::LOADS + t) * S::RPI;
+    const uint16_t *base;
+    int64_t rows, row;
+    if (r0 < 32) {
+      row = w_row(r0, base, rows);
+    } else {
+      base = a.x; rows = a.m; row = r0 - 32;
+    }
+    rsrc[t] = buffer_rsrc_words(base, rows * row_bytes);
+    voff[t] = static_cast<int>((row + lane / kLanesPerRow) * row_bytes) +
+              16 * (lane % kLanesPerRow);
   }
-  const uint16_t *xrow = a.x + (lr < a.m ? lr : 0) * a.k;
+  const uint32_t ring_lds = lds_address(ring);
+  const int slabs = static_cast<int>((a.k + S::SLAB_K - 1) / S::SLAB_K);
+  auto load_slab = [&](int slab, int buf) {
+    const uint32_t dst = ring_lds + static_cast<uint32_t>(buf * kSlabBytes);
+#pragma unroll
+    for (int t = 0; t < S::LOADS; ++t)
+      dma_lds16(rsrc[t], voff[t] + slab * S::RUN, dst + (wave * S::LOADS + t) * S::LINE);
+  };
 
-  // wave w takes 32-deep K chunks [c_begin, c_end); a batch of
-  // kSkinnyUnroll chunks is loaded before its MFMAs, chunks past c_end
-  // load chunk c_end - 1 and enter the MFMAs as zeros
-  const int chunks = static_cast<int>(a.k / 32);
-  const int per = (chunks + kSkinnyWaves - 1) / kSkinnyWaves;
-  const int c_begin = min(wave * per, chunks);
-  const int c_end = min(c_begin + per, chunks);
-  f32x4 acc[1][T::FN];
+  // fragment reads: lane (lr, g4) of 32-deep chunk q reads row lr of the
+  // operand's 16-row group, bytes 64 q + 16 g4 of its run
+  auto row_at = [&](int r) { return (r / S::RPI) * S::LINE + (r % S::RPI) * S::RUN; };
+  f32x4 acc[T::FM][T::FN];
 #pragma unroll
-  for (int j = 0; j < T::FN; ++j) acc[0][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c = c_begin; c < c_end; c += kSkinnyUnroll) {
-    u32x4 xa[kSkinnyUnroll], wb[kSkinnyUnroll][T::FN];
+  for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int u = 0; u < kSkinnyUnroll; ++u) {
-      const int64_t k0 = static_cast<int64_t>(min(c + u, c_end - 1)) * 32 + 8 * g4;
-      xa[u] = *reinterpret_cast<const u32x4 *>(xrow + k0);
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int kChunks = S::SLAB_K / 32 / S::WAVES;  // per wave and slab
+  auto compute = [&](int slab, int buf) {
+    const unsigned char *b0 = ring + buf * kSlabBytes + 16 * g4;
+    const int valid = static_cast<int>(
+        min<int64_t>(S::SLAB_K, a.k - static_cast<int64_t>(slab) * S::SLAB_K) / 32);
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) {
+      const int chunk = wave * kChunks + q;
+      if (chunk >= valid) break;  // wave-uniform: the last slab of a short K
+      u32x4 xa[T::FM], wb[T::FN];
+#pragma unroll
+      for (int i = 0; i < T::FM; ++i)
+        xa[i] = *reinterpret_cast<const u32x4 *>(b0 + row_at(32 + 16 * i + lr) + 64 * chunk);
 #pragma unroll
       for (int j = 0; j < T::FN; ++j)
-        wb[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow[j] + k0));
-    }
-    // every load of the batch is in flight before the first MFMA waits
-    __builtin_amdgcn_sched_barrier(0);
+        wb[j] = *reinterpret_cast<const u32x4 *>(b0 + row_at(16 * j + lr) + 64 * chunk);
 #pragma unroll
-    for (int u = 0; u < kSkinnyUnroll; ++u) {
-      if (c + u >= c_end) xa[u] = u32x4{0u, 0u, 0u, 0u};  // wave-uniform
+      for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-      for (int j = 0; j < T::FN; ++j) acc[0][j] = mfma_16x16x32_bf16(xa[u], wb[u][j], acc[0][j]);
+        for (int j = 0; j < T::FN; ++j) acc[i][j] = mfma_16x16x32_bf16(xa[i], wb[j], acc[i][j]);
     }
+  };
+  // slab s in buffer s % STAGES; step s waits for this wave's loads of
+  // slab s (the later slabs' loads may stay in flight), one barrier
+  // publishes it and frees slab s - 1's buffer, which takes slab
+  // s + STAGES - 1 (past the end: the last slab again, never read)
+  constexpr int kWaitStep = waitcnt_imm((S::STAGES - 2) * S::LOADS, 0);
+#pragma unroll
+  for (int p = 0; p < S::STAGES - 1; ++p) load_slab(min(p, slabs - 1), p);
+  int buf = 0;
+  for (int slab = 0; slab < slabs; ++slab) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitStep);
+    __builtin_amdgcn_s_barrier();
+    const int refill = buf == 0 ? S::STAGES - 1 : buf - 1;
+    load_slab(min(slab + S::STAGES - 1, slabs - 1), refill);
+    compute(slab, buf);
+    buf = buf + 1 == S::STAGES ? 0 : buf + 1;
   }
+  // every load landed and every LDS read done before the ring holds the
+  // partials
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  __syncthreads();
+  f32x4(*partial)[T::FM * T::FN][kWave] =
+      reinterpret_cast<f32x4(*)[T::FM * T::FN][kWave]>(ring);
 #pragma unroll
-  for (int j = 0; j < T::FN; ++j) partial[wave][j][lane] = acc[0][j];
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) partial[wave][i * T::FN + j][lane] = acc[i][j];
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int j = 0; j < T::FN; ++j) {
-    f32x4 sum = partial[0][j][lane];
-    for (int w = 1; w < kSkinnyWaves; ++w) sum += partial[w][j][lane];
-    acc[0][j] = sum;
-  }
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) {
+      f32x4 sum = partial[0][i * T::FN + j][lane];
+      for (int w = 1; w < S::WAVES; ++w) sum += partial[w][i * T::FN + j][lane];
+      acc[i][j] = sum;
+    }
   gemm_epilogue<EPI, T>(a, 0, tn, 0, wn, lane, acc);
 }
 
 template <int EPI>
 static hipError_t launch_skinny(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
-  const int64_t grid = tiles_n * GemmTileSkinny::WN;
+  const int64_t grid = tiles_n * 4;  // one workgroup per column pair
   if (grid > (int64_t{1} << 30)) return static_cast<hipError_t>(CASCADE_ESHAPE);
-  return launch_kernel(gemm_skinny_kernel<EPI>, dim3(static_cast<unsigned>(grid)),
-                       dim3(kSkinnyWaves * kWave), 0, s, a);
+  if (a.m <= 16)
+    return launch_kernel(gemm_skinny_kernel<EPI, 16>, dim3(static_cast<unsigned>(grid)),
+                         dim3(SkinnyShape<16>::WAVES * kWave), 0, s, a);
+  return launch_kernel(gemm_skinny_kernel<EPI, 64>, dim3(static_cast<unsigned>(grid)),
+                       dim3(SkinnyShape<64>::WAVES * kWave), 0, s, a);
 }
 
-// At most 16 rows of X: the skinny kernel.  Else 256-row tiles when there
+// At most 64 rows of X: the skinny kernels.  Else 256-row tiles when there
 // are at least as many as CUs (a partial last round runs as 128-row half
 // tiles); else 128-row tiles (a partial last round as 64-row half tiles),
 // unless there are fewer of those than CUs or at most 64 rows of X: then

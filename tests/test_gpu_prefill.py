@@ -46,9 +46,9 @@ def linear_bound_report(actual, x, w):
     (5, 1000, 4096), (129, 200, 128), (7, 1001, 128),
     (2048, 4096, 192), (2048, 4096, 320), (2048, 1024, 384),
     (2048, 1024, 448), (40, 512, 1088), (16, 4096, 4096), (11, 1024, 14336),
-    (17, 384, 4096)])
+    (17, 384, 4096), (64, 4096, 4096), (65, 1024, 4096), (128, 4096, 14336)])
 def test_gemm_matches_oracle(gpu_device, m, n, k):
-    # m <= 16: the skinny kernel (K split over a workgroup's waves);
+    # m <= 16 and m <= 64: the two skinny kernels; m >= 65: tiles;
     # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs.
     # Slab counts (K / 64): odd and even counts (1, 2, 3, 5, 6, 7, 17, 64,
     # 224) below and above the ring depth of each tile shape (256-row
@@ -71,9 +71,11 @@ def test_gemm_matches_oracle(gpu_device, m, n, k):
     assert r["ok"], r
 
 
-def test_gemm_f32out_matches_float64(gpu_device):
+@pytest.mark.parametrize("m", [5, 37])
+def test_gemm_f32out_matches_float64(gpu_device, m):
+    # m = 5: the skinny kernel's fp32 epilogue; m = 37: 64-row tiles
     dev = gpu_device
-    m, n, k = 37, 128256 // 8, 4096
+    n, k = 128256 // 8, 4096
     x = cases.normal_bf16((m, k), 103)
     w = cases.normal_bf16((n, k), 104, 0.02)
     y = torch.empty((m, n), dtype=torch.float32, device=dev)
