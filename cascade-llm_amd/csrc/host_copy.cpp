@@ -5,23 +5,30 @@
 // (layer_streaming/weight_store.py:258-268; vocab.py:143-147 on the main
 // thread), which its own measurements put at ~14.8 GB/s single-threaded
 // (IMPLEMENTATION_REPORT.md:61-67) -- below the H2D link it feeds.  Here one
-// call splits the copy into 2 MiB pieces that a persistent pool of threads
-// and the caller take from a shared counter; each piece is copied with
-// 32-byte loads and non-temporal 32-byte stores (the staging slot is read
-// next by the DMA engine, not by this CPU, so caching it only evicts the
-// arena stream), then the call returns once every piece is written.
+// copy is split into 2 MiB pieces that several threads take from a shared
+// counter; each piece is copied with 32-byte loads and non-temporal 32-byte
+// stores (the staging slot is read next by the DMA engine, not by this CPU,
+// so caching it only evicts the arena stream), and the call returns once
+// every piece is written.
 //
-// Concurrent callers are serialised: each call already uses every pool
-// thread.  Pure host code; no HIP call is made.
+// The library keeps no thread or state of its own between calls:
+// cascade_host_copy starts its helper threads for the one call, and a
+// caller that copies often (the staging store, once per transfer unit)
+// creates a pool with cascade_copy_pool_create, owns it, and destroys it.
+// Pure host code; no HIP call is made.
 #include <immintrin.h>
+#include <pthread.h>
+#include <sched.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
 #include <atomic>
 #include <condition_variable>
 #include <mutex>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -67,46 +74,115 @@ void copy_piece(char *dst, const char *src, size_t bytes, bool avx2) {
     memcpy(dst, src, bytes);
 }
 
+// One copy split into pieces that several threads take from a counter.
+struct CopyJob {
+  char *dst;
+  const char *src;
+  size_t bytes;
+  size_t pieces;
+  bool avx2;
+  std::atomic<size_t> next{0};
+
+  CopyJob(void *d, const void *s, size_t n, bool use_avx2)
+      : dst(static_cast<char *>(d)),
+        src(static_cast<const char *>(s)),
+        bytes(n),
+        pieces((n + kPiece - 1) / kPiece),
+        avx2(use_avx2) {}
+
+  void run() {
+    for (;;) {
+      const size_t p = next.fetch_add(1, std::memory_order_relaxed);
+      if (p >= pieces) return;
+      const size_t off = p * kPiece;
+      copy_piece(dst + off, src + off, std::min(kPiece, bytes - off), avx2);
+    }
+  }
+};
+
+bool cpu_has_avx2() {
+  static const bool avx2 = __builtin_cpu_supports("avx2");
+  return avx2;
+}
+
+// CPUs of NUMA node `node` that this process may run on, from sysfs
+// ("0-15,32-47").  Returns false when the node does not exist.
+bool node_cpus(int node, std::vector<int> *cpus) {
+  char path[96];
+  snprintf(path, sizeof path, "/sys/devices/system/node/node%d/cpulist", node);
+  FILE *f = fopen(path, "r");
+  if (f == nullptr) return false;
+  char line[4096] = {0};
+  const bool read = fgets(line, sizeof line, f) != nullptr;
+  fclose(f);
+  if (!read) return false;
+  cpu_set_t allowed;
+  CPU_ZERO(&allowed);
+  if (sched_getaffinity(0, sizeof allowed, &allowed) != 0) return false;
+  for (char *tok = strtok(line, ",\n"); tok; tok = strtok(nullptr, ",\n")) {
+    int lo = 0, hi = 0;
+    const int got = sscanf(tok, "%d-%d", &lo, &hi);
+    if (got < 1) continue;
+    if (got == 1) hi = lo;
+    for (int c = lo; c <= hi && c < CPU_SETSIZE; ++c)
+      if (CPU_ISSET(c, &allowed)) cpus->push_back(c);
+  }
+  return true;
+}
+
+// A pool of helper threads owned by whoever created it (the staging store
+// holds one for its lifetime).  A copy is split between the helpers and
+// the calling thread; concurrent copies on one pool run one after another,
+// since each already uses every helper.  Helpers may be bound to the CPUs
+// of one NUMA node (the GPU's, so the copies read and write memory near
+// the PCIe root the DMA engine reads the staging slots through).
 class CopyPool {
  public:
-  static CopyPool &instance() {
-    static CopyPool pool;
-    return pool;
+  CopyPool(int helpers, const std::vector<int> &cpus) : bound_cpus_(0) {
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    for (int c : cpus) CPU_SET(c, &set);
+    try {
+      for (int id = 0; id < helpers; ++id) {
+        workers_.emplace_back([this, id] { worker(id); });
+        if (!cpus.empty() &&
+            pthread_setaffinity_np(workers_.back().native_handle(), sizeof set,
+                                   &set) == 0)
+          bound_cpus_ = static_cast<int>(cpus.size());
+      }
+    } catch (...) {
+      stop_workers();  // the threads already started end before the throw
+      throw;
+    }
   }
 
-  int copy(void *dst, const void *src, size_t bytes, int threads) {
+  ~CopyPool() { stop_workers(); }
+
+  int copy(void *dst, const void *src, size_t bytes) {
     std::lock_guard<std::mutex> call(call_mutex_);
-    const size_t pieces = (bytes + kPiece - 1) / kPiece;
-    const int helpers = static_cast<int>(
-        std::min<size_t>(std::max(threads, 1) - 1, pieces ? pieces - 1 : 0));
-    ensure_threads(helpers);
+    CopyJob job(dst, src, bytes, cpu_has_avx2());
+    const int helpers = static_cast<int>(std::min<size_t>(
+        workers_.size(), job.pieces ? job.pieces - 1 : 0));
     {
       std::lock_guard<std::mutex> lock(mutex_);
-      dst_ = static_cast<char *>(dst);
-      src_ = static_cast<const char *>(src);
-      bytes_ = bytes;
-      pieces_ = pieces;
-      next_.store(0, std::memory_order_relaxed);
+      job_ = &job;
       active_ = helpers;
       pending_ = helpers;
       ++generation_;
     }
     wake_.notify_all();
-    run_pieces();
+    job.run();
     std::unique_lock<std::mutex> lock(mutex_);
     done_.wait(lock, [this] { return pending_ == 0; });
+    job_ = nullptr;
     return 0;
   }
 
-  int thread_count() {
-    std::lock_guard<std::mutex> lock(mutex_);
-    return static_cast<int>(workers_.size());
-  }
+  int threads() const { return static_cast<int>(workers_.size()) + 1; }
+  int bound_cpus() const { return bound_cpus_; }
 
  private:
-  CopyPool() : avx2_(__builtin_cpu_supports("avx2")) {}
-
-  ~CopyPool() {
+  void stop_workers() {
     {
       std::lock_guard<std::mutex> lock(mutex_);
       stop_ = true;
@@ -115,64 +191,105 @@ class CopyPool {
     for (auto &t : workers_) t.join();
   }
 
-  void ensure_threads(int n) {
-    std::lock_guard<std::mutex> lock(mutex_);
-    while (static_cast<int>(workers_.size()) < n) {
-      const int id = static_cast<int>(workers_.size());
-      workers_.emplace_back([this, id] { worker(id); });
-    }
-  }
-
-  void run_pieces() {
-    for (;;) {
-      const size_t p = next_.fetch_add(1, std::memory_order_relaxed);
-      if (p >= pieces_) return;
-      const size_t off = p * kPiece;
-      copy_piece(dst_ + off, src_ + off, std::min(kPiece, bytes_ - off), avx2_);
-    }
-  }
-
   void worker(int id) {
     uint64_t seen = 0;
     for (;;) {
+      CopyJob *job = nullptr;
       {
         std::unique_lock<std::mutex> lock(mutex_);
-        wake_.wait(lock, [&] { return stop_ || (generation_ != seen && id < active_); });
+        wake_.wait(lock, [&] {
+          return stop_ || (generation_ != seen && id < active_);
+        });
         if (stop_) return;
         seen = generation_;
+        job = job_;
       }
-      run_pieces();
+      job->run();
       std::lock_guard<std::mutex> lock(mutex_);
       if (--pending_ == 0) done_.notify_all();
     }
   }
 
-  const bool avx2_;
+  int bound_cpus_;
   std::mutex call_mutex_;
   std::mutex mutex_;
   std::condition_variable wake_;
   std::condition_variable done_;
   std::vector<std::thread> workers_;
+  CopyJob *job_ = nullptr;
   uint64_t generation_ = 0;
   bool stop_ = false;
   int active_ = 0;
   int pending_ = 0;
-  char *dst_ = nullptr;
-  const char *src_ = nullptr;
-  size_t bytes_ = 0;
-  size_t pieces_ = 0;
-  std::atomic<size_t> next_{0};
 };
+
+int check_copy(const void *dst, const void *src, size_t bytes) {
+  if (dst == nullptr || src == nullptr) return CASCADE_EINVAL;
+  const char *d = static_cast<const char *>(dst);
+  const char *s = static_cast<const char *>(src);
+  if (d < s + bytes && s < d + bytes) return CASCADE_EINVAL;  // overlap
+  return 0;
+}
 
 }  // namespace
 
 extern "C" int cascade_host_copy(void *dst, const void *src, size_t bytes,
                                  int threads) {
   if (bytes == 0) return 0;
-  if (dst == nullptr || src == nullptr) return CASCADE_EINVAL;
   if (threads < 1 || threads > kMaxThreads) return CASCADE_EINVAL;
-  const char *d = static_cast<const char *>(dst);
-  const char *s = static_cast<const char *>(src);
-  if (d < s + bytes && s < d + bytes) return CASCADE_EINVAL;  // overlap
-  return CopyPool::instance().copy(dst, src, bytes, threads);
+  if (const int e = check_copy(dst, src, bytes)) return e;
+  // helper threads live for this call only
+  CopyJob job(dst, src, bytes, cpu_has_avx2());
+  const size_t helpers =
+      std::min<size_t>(static_cast<size_t>(threads) - 1, job.pieces - 1);
+  std::vector<std::thread> workers;
+  try {
+    for (size_t i = 0; i < helpers; ++i) workers.emplace_back([&job] { job.run(); });
+  } catch (const std::system_error &) {
+    // fewer helpers than asked: the threads started so far and the caller
+    // still finish every piece
+  }
+  job.run();
+  for (auto &t : workers) t.join();
+  return 0;
+}
+
+extern "C" int cascade_copy_pool_create(int threads, int numa_node,
+                                        uint64_t *pool) {
+  if (pool == nullptr) return CASCADE_EINVAL;
+  *pool = 0;
+  if (threads < 1 || threads > kMaxThreads || numa_node < -1)
+    return CASCADE_EINVAL;
+  std::vector<int> cpus;
+  if (numa_node >= 0 && !node_cpus(numa_node, &cpus)) return CASCADE_EINVAL;
+  try {
+    *pool = reinterpret_cast<uint64_t>(new CopyPool(threads - 1, cpus));
+  } catch (const std::exception &) {
+    return CASCADE_EINVAL;
+  }
+  return 0;
+}
+
+extern "C" int cascade_copy_pool_copy(uint64_t pool, void *dst,
+                                      const void *src, size_t bytes) {
+  if (pool == 0) return CASCADE_EINVAL;
+  if (bytes == 0) return 0;
+  if (const int e = check_copy(dst, src, bytes)) return e;
+  return reinterpret_cast<CopyPool *>(pool)->copy(dst, src, bytes);
+}
+
+extern "C" int cascade_copy_pool_info(uint64_t pool, int *threads,
+                                      int *bound_cpus) {
+  if (pool == 0 || threads == nullptr || bound_cpus == nullptr)
+    return CASCADE_EINVAL;
+  const CopyPool *p = reinterpret_cast<CopyPool *>(pool);
+  *threads = p->threads();
+  *bound_cpus = p->bound_cpus();
+  return 0;
+}
+
+extern "C" int cascade_copy_pool_destroy(uint64_t pool) {
+  if (pool == 0) return CASCADE_EINVAL;
+  delete reinterpret_cast<CopyPool *>(pool);
+  return 0;
 }

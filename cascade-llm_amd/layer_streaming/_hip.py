@@ -104,6 +104,11 @@ _SIGNATURES = {
     "cascade_event_query": (_INT, [_U64]),
     "cascade_event_elapsed_ms": (_INT, [_U64, _U64, ctypes.POINTER(_F)]),
     "cascade_host_copy": (_INT, [_P, _P, _SZ, _INT]),
+    "cascade_copy_pool_create": (_INT, [_INT, _INT, ctypes.POINTER(_U64)]),
+    "cascade_copy_pool_copy": (_INT, [_U64, _P, _P, _SZ]),
+    "cascade_copy_pool_info": (
+        _INT, [_U64, ctypes.POINTER(_INT), ctypes.POINTER(_INT)]),
+    "cascade_copy_pool_destroy": (_INT, [_U64]),
     "cascade_hbm_read": (_INT, [_P, _SZ, _P, _I64, _P]),
     "cascade_device_copy": (_INT, [_P, _P, _SZ, _P]),
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
@@ -766,11 +771,7 @@ def default_copy_threads():
     return max(1, min(8, cpus))
 
 
-def host_copy(dst, src, threads=None):
-    """dst.copy_(src) for contiguous host tensors of equal byte size, with
-    the library's multi-threaded non-temporal memcpy (the GIL is released
-    for the duration of the copy)."""
-
+def _host_copy_bytes(dst, src):
     for name, t in (("dst", dst), ("src", src)):
         if not isinstance(t, torch.Tensor) or t.device.type != "cpu":
             raise ValueError("{} must be a host tensor".format(name))
@@ -779,9 +780,73 @@ def host_copy(dst, src, threads=None):
     nbytes = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() != nbytes:
         raise ValueError("host_copy needs equal byte sizes")
+    return nbytes
+
+
+def host_copy(dst, src, threads=None):
+    """dst.copy_(src) for contiguous host tensors of equal byte size, with
+    the library's multi-threaded non-temporal memcpy (threads started for
+    this call only; the GIL is released for the duration of the copy)."""
+
+    nbytes = _host_copy_bytes(dst, src)
     call("cascade_host_copy", dst.data_ptr(), src.data_ptr(), nbytes,
          int(threads or default_copy_threads()))
     return dst
+
+
+def device_numa_node(device=None):
+    """NUMA node of the host bridge a GPU sits behind, from the PCI
+    device's sysfs entry; -1 when there is no GPU, the platform reports
+    none (a one-node host writes -1 there too) or the entry is missing."""
+
+    if not torch.cuda.is_available():
+        return -1
+    props = torch.cuda.get_device_properties(
+        torch.cuda.current_device() if device is None else device)
+    path = "/sys/bus/pci/devices/{:04x}:{:02x}:{:02x}.0/numa_node".format(
+        props.pci_domain_id, props.pci_bus_id, props.pci_device_id)
+    try:
+        with open(path) as f:
+            return int(f.read().strip())
+    except (OSError, ValueError):
+        return -1
+
+
+class CopyPool:
+    """A caller-owned pool for the multi-threaded host copy: ``threads``
+    threads in all (the caller and threads - 1 helpers), the helpers bound
+    to the CPUs of ``numa_node`` when it is >= 0.  ``close`` joins them."""
+
+    def __init__(self, threads=None, numa_node=-1):
+        handle = _U64(0)
+        call("cascade_copy_pool_create", int(threads or default_copy_threads()),
+             int(numa_node), ctypes.byref(handle))
+        self.handle = handle.value
+        threads_out, bound = _INT(0), _INT(0)
+        call("cascade_copy_pool_info", self.handle, ctypes.byref(threads_out),
+             ctypes.byref(bound))
+        self.threads = threads_out.value
+        self.bound_cpus = bound.value
+        self.numa_node = int(numa_node)
+
+    def copy(self, dst, src):
+        if not self.handle:
+            raise RuntimeError("the copy pool is closed")
+        nbytes = _host_copy_bytes(dst, src)
+        call("cascade_copy_pool_copy", self.handle, dst.data_ptr(),
+             src.data_ptr(), nbytes)
+        return dst
+
+    def close(self):
+        if self.handle:
+            handle, self.handle = self.handle, 0
+            call("cascade_copy_pool_destroy", handle)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 class HipEvent:

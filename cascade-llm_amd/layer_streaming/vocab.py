@@ -171,7 +171,7 @@ class VocabStreamingRuntime:
         if reader is not None:
             reader.synchronize()  # the copy that read this half is done
         target = self.head_staging_slots[half][: rows.numel()]
-        _hip.host_copy(target, rows, getattr(self.store, "copy_threads", None))
+        self.store.copy_to_pinned(target, rows)
         self._staging_read[half] = self._ready[chunk]
         return target
 

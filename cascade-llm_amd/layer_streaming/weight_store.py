@@ -12,10 +12,11 @@ constructor arguments, ``tensor`` / ``unit_source`` / ``prepare_unit`` /
   (``prepare_unit`` hands back a completed future).
 * pinned_staging keeps the arena pageable and moves units through pinned
   staging buffers.  A ``_Stager`` owns those buffers, their byte ring
-  (``StagingRing``) and its own worker threads; each job waits for the copies
-  that last read its bytes, then copies with the library's multi-threaded
-  non-temporal memcpy (``cascade_host_copy``), where the reference makes one
-  tensor copy per unit (:258-268).
+  (``StagingRing``), its own worker threads and a copy pool of the library
+  (``cascade_copy_pool_*``, helpers bound to the GPU's NUMA node when the
+  host has several); each job waits for the copies that last read its
+  bytes, then copies with that pool's multi-threaded non-temporal memcpy,
+  where the reference makes one tensor copy per unit (:258-268).
 * ``load_checkpoint`` parses safetensors headers and reads every tensor
   straight into its arena bytes (``checkpoint.load_into``).
 * ``fill_random`` writes the seeded synthetic weights of the benchmark
@@ -293,10 +294,10 @@ class _Stager:
     the copies that last read those bytes; a worker waits for the events,
     copies, and resolves the job's future with the pinned view."""
 
-    def __init__(self, buffers, workers, copy_threads):
+    def __init__(self, buffers, workers, copy_threads, numa_node):
         self.buffers = buffers
         self.ring = StagingRing(buffers)
-        self.copy_threads = copy_threads
+        self.pool = _hip.CopyPool(copy_threads, numa_node)
         self._jobs = queue.SimpleQueue()
         self._lock = threading.Lock()
         self._durations_ms = []
@@ -334,7 +335,7 @@ class _Stager:
         buffer = self.buffers[buffer_index]
         first = byte_start // buffer.element_size()
         target = buffer[first:first + source.numel()]
-        _hip.host_copy(target, source, self.copy_threads)
+        self.pool.copy(target, source)
         with self._lock:
             self._durations_ms.append((time.perf_counter() - started) * 1000.0)
         return target
@@ -351,6 +352,7 @@ class _Stager:
             self._jobs.put(None)
         for thread in self._threads:
             thread.join()
+        self.pool.close()
 
 
 class PinnedStagingWeightStore(BaseWeightStore):
@@ -359,9 +361,11 @@ class PinnedStagingWeightStore(BaseWeightStore):
     mode = WeightStoreMode.PINNED_STAGING
 
     def __init__(self, plan, allocate=True, tensor_factory=None, worker_count=2,
-                 copy_threads=None):
+                 copy_threads=None, numa_node=None):
         self.worker_count = int(worker_count)
         self.copy_threads = int(copy_threads or _hip.default_copy_threads())
+        # None: the current GPU's node, looked up when the slots are made
+        self.numa_node = numa_node
         self._stager = None
         super().__init__(plan, False, allocate=allocate,
                          tensor_factory=tensor_factory)
@@ -383,7 +387,10 @@ class PinnedStagingWeightStore(BaseWeightStore):
         if self._stager is None:
             buffers = [self._host_buffer(self.plan.slot_elements, True)
                        for _ in range(self.plan.slot_count)]
-            self._stager = _Stager(buffers, self.worker_count, self.copy_threads)
+            if self.numa_node is None:
+                self.numa_node = _hip.device_numa_node()
+            self._stager = _Stager(buffers, self.worker_count, self.copy_threads,
+                                   self.numa_node)
         return arena
 
     def _running_stager(self):
@@ -407,6 +414,12 @@ class PinnedStagingWeightStore(BaseWeightStore):
 
         return self._running_stager().submit(self.unit_source(unit), slot_index,
                                              start, waits)
+
+    def copy_to_pinned(self, target, source):
+        """``target.copy_(source)`` on the staging copy pool (the streamed
+        LM head stages its chunks through it, vocab.py)."""
+
+        return self._running_stager().pool.copy(target, source)
 
     def close(self):
         if self._stager is not None:

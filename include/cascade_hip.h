@@ -312,13 +312,29 @@ int cascade_event_query(uint64_t event);
 int cascade_event_elapsed_ms(uint64_t start, uint64_t end, float *ms);
 
 /* Host memcpy of `bytes` from src to dst (non-overlapping host memory)
- * with `threads` threads (1..64: the caller plus a persistent pool), 2 MiB
- * pieces, non-temporal stores; returns when the copy is complete.  Calls
- * from several threads are serialised.  No HIP call is made.
+ * with `threads` threads (1..64: the caller plus threads started for this
+ * call and joined before it returns), 2 MiB pieces, non-temporal stores;
+ * returns when the copy is complete.  No HIP call is made and nothing
+ * outlives the call.
  * Replaces the pageable -> pinned staging copy of PinnedStagingWeightStore
  * (layer_streaming/weight_store.py:258-268) and of the streamed LM head
  * (layer_streaming/vocab.py:143-147).                                      */
 int cascade_host_copy(void *dst, const void *src, size_t bytes, int threads);
+
+/* The same copy through a caller-owned pool of threads - 1 helper threads,
+ * for a caller that stages many units (the reference's staging store makes
+ * one copy per transfer unit, weight_store.py:258-268).  numa_node >= 0
+ * binds the helpers to that node's CPUs (those this process may use; none
+ * left -> unbound); -1 leaves them unbound; a node that does not exist is
+ * CASCADE_EINVAL.  Copies on one pool from several threads run one after
+ * another.  Destroy joins the helpers; no copy may be running on it.
+ * cascade_copy_pool_info reports the thread count (helpers + caller) and
+ * how many CPUs the helpers are bound to (0 = unbound).                    */
+int cascade_copy_pool_create(int threads, int numa_node, uint64_t *pool);
+int cascade_copy_pool_copy(uint64_t pool, void *dst, const void *src,
+                           size_t bytes);
+int cascade_copy_pool_info(uint64_t pool, int *threads, int *bound_cpus);
+int cascade_copy_pool_destroy(uint64_t pool);
 
 /* ----------------------------------------------------------- measurement
  * Streaming-read kernel: reads `bytes` of device memory (nontemporal 16-byte

@@ -1,8 +1,10 @@
-"""The library's multi-threaded staging memcpy (cascade_host_copy), on the
-CPU: it replaces the pageable -> pinned tensor copy of the pinned-staging
-store (reference layer_streaming/weight_store.py:258-268) and must equal
-that copy byte for byte for any size and alignment."""
+"""The library's multi-threaded staging memcpy (cascade_host_copy and the
+caller-owned cascade_copy_pool_*), on the CPU: it replaces the pageable ->
+pinned tensor copy of the pinned-staging store (reference
+layer_streaming/weight_store.py:258-268) and must equal that copy byte for
+byte for any size and alignment."""
 
+import os
 import threading
 
 import pytest
@@ -33,16 +35,77 @@ def test_host_copy_thread_counts(threads):
     assert torch.equal(dst, src)
 
 
-def test_host_copy_concurrent_callers():
+@pytest.mark.parametrize("nbytes", [1, (2 << 20) + 17, (9 << 20) + 5])
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_copy_pool_equals_tensor_copy(nbytes, threads):
+    gen = torch.Generator().manual_seed(nbytes * threads)
+    src = torch.randint(0, 256, (nbytes + 7,), dtype=torch.uint8, generator=gen)
+    dst = torch.zeros(nbytes + 64, dtype=torch.uint8)
+    with _hip.CopyPool(threads) as pool:
+        assert pool.threads == threads and pool.bound_cpus == 0
+        for _ in range(2):  # the helpers serve one copy after another
+            dst.zero_()
+            pool.copy(dst[5:5 + nbytes], src[7:7 + nbytes])
+            assert torch.equal(dst[5:5 + nbytes], src[7:7 + nbytes])
+            assert int(dst[:5].sum()) == 0 and int(dst[5 + nbytes:].sum()) == 0
+
+
+def _node_cpus(node):
+    with open("/sys/devices/system/node/node{}/cpulist".format(node)) as f:
+        cpus = set()
+        for part in f.read().strip().split(","):
+            lo, _, hi = part.partition("-")
+            cpus.update(range(int(lo), int(hi or lo) + 1))
+    return cpus & os.sched_getaffinity(0)
+
+
+@pytest.mark.skipif(not os.path.exists("/sys/devices/system/node/node0/cpulist"),
+                    reason="no NUMA topology in sysfs")
+def test_copy_pool_binds_helpers_to_a_node():
+    src = torch.arange(5 << 20, dtype=torch.int32)
+    dst = torch.empty_like(src)
+    with _hip.CopyPool(4, numa_node=0) as pool:
+        assert pool.bound_cpus == len(_node_cpus(0))
+        pool.copy(dst, src)
+    assert torch.equal(dst, src)
+
+
+def test_copy_pool_rejects_bad_arguments():
+    with pytest.raises(_hip.HipCallError):  # no such NUMA node
+        _hip.CopyPool(2, numa_node=4095)
+    with pytest.raises(_hip.HipCallError):
+        _hip.CopyPool(2, numa_node=-2)
+    with pytest.raises(_hip.HipCallError):  # thread count out of range
+        _hip.CopyPool(65)
+    buf = torch.zeros(1024, dtype=torch.uint8)
+    pool = _hip.CopyPool(2)
+    with pytest.raises(_hip.HipCallError):  # overlapping ranges
+        _hip.call("cascade_copy_pool_copy", pool.handle, buf.data_ptr(),
+                  buf.data_ptr() + 16, 512)
+    pool.close()
+    pool.close()  # idempotent
+    with pytest.raises(RuntimeError):
+        pool.copy(buf[:10], buf[100:110])
+    with pytest.raises(_hip.HipCallError):
+        _hip.call("cascade_copy_pool_copy", 0, buf.data_ptr(),
+                  buf.data_ptr() + 512, 256)
+
+
+@pytest.mark.parametrize("pooled", [False, True])
+def test_host_copy_concurrent_callers(pooled):
     # the staging store calls from two worker threads at once
     srcs = [torch.full((5 << 20,), i, dtype=torch.int16) for i in range(6)]
     dsts = [torch.empty_like(s) for s in srcs]
     errors = []
+    pool = _hip.CopyPool(4) if pooled else None
 
     def run(i):
         try:
             for _ in range(3):
-                _hip.host_copy(dsts[i], srcs[i], 4)
+                if pool is None:
+                    _hip.host_copy(dsts[i], srcs[i], 4)
+                else:
+                    pool.copy(dsts[i], srcs[i])
         except Exception as e:  # pragma: no cover - reported below
             errors.append(e)
 
@@ -51,6 +114,8 @@ def test_host_copy_concurrent_callers():
         t.start()
     for t in threads:
         t.join()
+    if pool is not None:
+        pool.close()
     assert not errors
     for s, d in zip(srcs, dsts):
         assert torch.equal(s, d)
