@@ -3,9 +3,12 @@
 // One wavefront owns a tile of R weight rows and the whole reduction
 // dimension K.  Lane l reads 16-byte pieces l, l+64, l+128, ... of each row,
 // so every load instruction of a wave covers 1 KiB of one row, fully
-// coalesced.  All loads of a tile are issued before the workgroup builds its
-// copy of the (optionally RMS-normalised) input vector in LDS, so the
-// prologue hides under HBM latency.  Products use v_dot2_f32_bf16 (two bf16
+// coalesced.  A wave issues its loads of the input vector (and of the norm
+// weight), then those of the epilogue's operands (residual, gate, RoPE
+// cos / sin), then every weight load of its tile; loads complete in issue
+// order, so the workgroup builds its copy of the (optionally
+// RMS-normalised) input vector in LDS while the weights stream in, and the
+// epilogue finds its operands in registers.  Products use v_dot2_f32_bf16 (two bf16
 // products accumulated into fp32 per instruction); the row sums are reduced
 // across the wave and finished by an epilogue that reproduces the reference's
 // bf16 rounding points:
@@ -117,6 +120,95 @@ __device__ void stage_input(const GemvArgs &a, u32x4 *xs) {
   }
 }
 
+// The same input vector built in two phases, for K = KC * 512 with NV =
+// ceil(KC / WAVES) 16-byte pieces per thread: load_input issues the loads of
+// x (and of the norm weight) before the weight loads, so that, loads
+// completing in issue order, the vector can be normalised and staged while
+// the weights stream in (store_input) instead of after they have landed.
+template <int NV>
+struct InputRegs {
+  u32x4 x[NV];
+  u32x4 w[NV];  // loaded only with a norm weight
+};
+
+template <int NV, int THREADS, bool EARLY_W>
+__device__ __forceinline__ void load_input(const GemvArgs &a, InputRegs<NV> &in) {
+  // unconditional loads at a clamped index (a load under a per-lane
+  // predicate is waited for on the spot, to merge it with the other path)
+  const int64_t nvec = a.k >> 3;
+  const u32x4 *xg = reinterpret_cast<const u32x4 *>(a.x);
+  const u32x4 *wg = reinterpret_cast<const u32x4 *>(a.norm_w);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t j = min(threadIdx.x + static_cast<int64_t>(i) * THREADS, nvec - 1);
+    in.x[i] = xg[j];
+  }
+  if (EARLY_W && wg != nullptr) {  // workgroup-uniform; in.w is read only on this path
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t j = min(threadIdx.x + static_cast<int64_t>(i) * THREADS, nvec - 1);
+      in.w[i] = wg[j];
+    }
+  }
+}
+
+template <int NV, int THREADS, bool EARLY_W>
+__device__ __forceinline__ void store_input(const GemvArgs &a, InputRegs<NV> &in,
+                                            u32x4 *xs) {
+  const int64_t nvec = a.k >> 3;
+  if (a.norm_w == nullptr) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t j = threadIdx.x + static_cast<int64_t>(i) * THREADS;
+      if (j < nvec) xs[j] = in.x[i];
+    }
+    return;
+  }
+  if constexpr (!EARLY_W) {
+    const u32x4 *wg = reinterpret_cast<const u32x4 *>(a.norm_w);
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      in.w[i] = wg[min(threadIdx.x + static_cast<int64_t>(i) * THREADS, nvec - 1)];
+  }
+  __shared__ float red[THREADS / kWave];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    // a clamped index repeats the last piece: it counts once
+    if (threadIdx.x + static_cast<int64_t>(i) * THREADS >= nvec) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = lo_bf16(in.x[i][e]);
+      const float hi = hi_bf16(in.x[i][e]);
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < THREADS / kWave; ++i) total += red[i];
+  const float variance = total * (1.0f / static_cast<float>(a.k));
+  const float r = 1.0f / __builtin_sqrtf(variance + a.eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t j = threadIdx.x + static_cast<int64_t>(i) * THREADS;
+    if (j >= nvec) continue;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float nlo = round_bf16(lo_bf16(in.x[i][e]) * r);
+      const float nhi = round_bf16(hi_bf16(in.x[i][e]) * r);
+      const uint32_t olo = f32_to_bf16(lo_bf16(in.w[i][e]) * nlo);
+      const uint32_t ohi = f32_to_bf16(hi_bf16(in.w[i][e]) * nhi);
+      o[e] = olo | (ohi << 16);
+    }
+    xs[j] = o;
+  }
+}
+
 __device__ __forceinline__ float silu_f32(float g) {
   return g / (1.0f + expf(-g));
 }
@@ -146,11 +238,13 @@ __device__ __forceinline__ void tile_rows(const GemvArgs &a, int64_t tile,
       base = a.w2;
       lh = head - hq - hk;
     }
+    // a padding tile reads row 0 of a matrix the launch has (unused)
+    const uint16_t *any = a.w0 != nullptr ? a.w0 : (a.w1 != nullptr ? a.w1 : a.w2);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int d = d0 + (r % P) + (r >= P ? kHalfHead : 0);
       ok[r] = tile_ok;
-      wrow[r] = tile_ok ? base + (lh * kHeadDim + d) * a.k : a.w0;
+      wrow[r] = tile_ok ? base + (lh * kHeadDim + d) * a.k : any;
     }
   } else if constexpr (EPI == kSwiglu) {
     constexpr int P = R / 2;
@@ -170,24 +264,60 @@ __device__ __forceinline__ void tile_rows(const GemvArgs &a, int64_t tile,
   }
 }
 
+// The memory operands of the epilogue (the residual or gate element of
+// each row; RoPE's cos / sin at the token's position), loaded right after
+// the weights so that their latency hides under the weight stream instead
+// of following the reduction.
+template <int EPI, int R>
+__device__ __forceinline__ void epilogue_operands(const GemvArgs &a, int64_t tile,
+                                                  const bool (&ok)[R],
+                                                  int64_t length_word,
+                                                  float (&pre0)[R], float (&pre1)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) pre0[r] = pre1[r] = 0.0f;
+  if constexpr (EPI == kResidual || EPI == kMul) {
+    // rows past the matrix read its last row (unused)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      pre0[r] = bf16_to_f32(a.aux[min(tile * R + r, a.n0 - 1)]);
+  } else if constexpr (EPI == kQkvRope) {
+    constexpr int P = R / 2;
+    constexpr int kTilesPerHead = kHalfHead / P;
+    const int d0 = static_cast<int>(tile % kTilesPerHead) * P;
+    // a launch of v rows only may pass no tables (kernel-uniform test)
+    if (a.rope_cos != nullptr && a.rope_sin != nullptr) {
+      const uint16_t *rope_cos = a.rope_cos, *rope_sin = a.rope_sin;
+      if (a.length != nullptr) {
+        const int64_t pos = min(max(length_word - 1, int64_t{0}), a.capacity - 1);
+        rope_cos += pos * kHalfHead;
+        rope_sin += pos * kHalfHead;
+      }
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        pre0[p] = bf16_to_f32(rope_cos[d0 + p]);
+        pre1[p] = bf16_to_f32(rope_sin[d0 + p]);
+      }
+    }
+  }
+}
+
 template <int EPI, int R>
 __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
                                          const float (&acc)[R],
                                          const bool (&ok)[R],
-                                         int64_t length_word) {
+                                         int64_t length_word,
+                                         const float (&pre0)[R],
+                                         const float (&pre1)[R]) {
   if constexpr (EPI == kQkvRope) {
     constexpr int P = R / 2;
     constexpr int kTilesPerHead = kHalfHead / P;
     const int64_t head = tile / kTilesPerHead;
     const int d0 = static_cast<int>(tile % kTilesPerHead) * P;
     const int64_t hq = a.n0 / kHeadDim, hk = a.n1 / kHeadDim;
-    const uint16_t *rope_cos = a.rope_cos, *rope_sin = a.rope_sin;
     uint16_t *k_out = a.k_out, *v_out = a.v_out;
     if (a.length != nullptr) {
       const int64_t pos =
           min(max(length_word - 1, int64_t{0}), a.capacity - 1);
-      rope_cos += pos * kHalfHead;
-      rope_sin += pos * kHalfHead;
       k_out += pos * kHeadDim;
       v_out += pos * kHeadDim;
     }
@@ -201,8 +331,8 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
         // apply_rotary_pos_emb: x*cos + rotate_half(x)*sin, every product
         // and the sum rounded to bf16; cos/sin are bf16 and identical for
         // d and d + 64 (emb = cat(freqs, freqs)).
-        const float c = bf16_to_f32(rope_cos[d]);
-        const float s = bf16_to_f32(rope_sin[d]);
+        const float c = pre0[p];
+        const float s = pre1[p];
         oa = f32_to_bf16(round_bf16(xa * c) + round_bf16(-xb * s));
         ob = f32_to_bf16(round_bf16(xb * c) + round_bf16(xa * s));
       } else {
@@ -246,11 +376,11 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int64_t tile,
       if constexpr (EPI == kPlain) {
         out = v;
       } else if constexpr (EPI == kResidual) {
-        out = bf16_to_f32(a.aux[row]) + v;
+        out = pre0[r] + v;
       } else if constexpr (EPI == kSilu) {
         out = silu_f32(v);
       } else {  // kMul
-        out = bf16_to_f32(a.aux[row]) * v;
+        out = pre0[r] * v;
       }
       a.y[row] = f32_to_bf16(out);
     }
@@ -281,18 +411,35 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
   bool ok[R];
   tile_rows<EPI, R>(a, tile, tile_ok, wrow, ok);
 
-  float acc[R];
+  float acc[R], pre0[R], pre1[R];
   if constexpr (KC > 0) {
+    constexpr int NV = (KC + WAVES - 1) / WAVES;
+    // the input (and the norm weight, K = 4096) ahead of the weights where
+    // the registers allow; down_proj's 56 loads per lane leave no room
+    constexpr bool kEarly = R * KC <= 32;
+    constexpr bool kEarlyW = kEarly && KC <= 8;
+    InputRegs<NV> in;
+    if constexpr (kEarly) {
+      load_input<NV, WAVES * kWave, kEarlyW>(a, in);
+      epilogue_operands<EPI, R>(a, tile, ok, length_word, pre0, pre1);
+    }
+    // unconditional: a row past the matrix reads row 0 of w0 (tile_rows)
+    // and its sum is never stored
     u32x4 wv[R][KC];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        wv[r][c] = ok[r] ? load16<NT>(wrow[r] + (c * kWave + lane) * 8)
-                         : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int c = 0; c < KC; ++c) wv[r][c] = load16<NT>(wrow[r] + (c * kWave + lane) * 8);
     }
-    stage_input<WAVES * kWave>(a, xs);
+    // every load above is issued before any use of the input (the waits
+    // for the input then leave the weight loads in flight)
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kEarly) {
+      store_input<NV, WAVES * kWave, kEarlyW>(a, in, xs);
+    } else {
+      epilogue_operands<EPI, R>(a, tile, ok, length_word, pre0, pre1);
+      stage_input<WAVES * kWave>(a, xs);
+    }
     __syncthreads();
     float acc2[R];
 #pragma unroll
@@ -314,6 +461,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] += acc2[r];
   } else {
+    epilogue_operands<EPI, R>(a, tile, ok, length_word, pre0, pre1);
     stage_input<WAVES * kWave>(a, xs);
     __syncthreads();
     const int64_t nvec = a.k >> 3;
@@ -329,7 +477,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-  if (lane == 0 && tile_ok) epilogue<EPI, R>(a, tile, acc, ok, length_word);
+  if (lane == 0 && tile_ok) epilogue<EPI, R>(a, tile, acc, ok, length_word, pre0, pre1);
 }
 
 template <int KC, int R, int WAVES, int EPI, bool NT>
