@@ -747,13 +747,15 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_
                        dim3(static_cast<unsigned>(grid)), dim3(T::WAVES * kWave), 0, s, a);
 }
 
-// Short prompts (M <= 64 rows).  The weights are nearly all the traffic, so
+// Short prompts (M <= 64 rows, or up to 256 over few columns).  The weights are nearly all the traffic, so
 // they must stream at HBM rate, which needs long runs of one row per load
 // (64-byte pieces of 16 rows per instruction, the layout of an MFMA operand,
 // stream at only 2-3 TB/s).  A workgroup computes one pair of 16-column
 // fragments of a 128-column tile (the columns of wave column wn of a
 // GemmTile<MR, 1, 4>, so the epilogues' pairing of column c with c + 64
-// holds) for all M rows.  K is walked in slabs through a ring of LDS
+// holds) for a block of MR rows (grid.y: the row block; M > 64 runs
+// blocks of 64 rows side by side, each reading the column pair's W
+// again, from the XCD's L2 when the blocks share an XCD).  K is walked in slabs through a ring of LDS
 // buffers: every load instruction moves 1 KiB, one or two whole row runs
 // of a slab (the 32 W rows and the MR X rows; rows past M or past a matrix
 // read as zeros through the buffer bounds, and K past a short last slab
@@ -794,6 +796,7 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
                 "the reduction fits in the ring");
   const int tn = static_cast<int>(blockIdx.x) / T::WN;
   const int wn = static_cast<int>(blockIdx.x) % T::WN;
+  const int rb = static_cast<int>(blockIdx.y);  // block of MR rows of X
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lr = lane & 15;
@@ -837,7 +840,7 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
     if (r0 < 32) {
       row = w_row(r0, base, rows);
     } else {
-      base = a.x; rows = a.m; row = r0 - 32;
+      base = a.x; rows = a.m; row = static_cast<int64_t>(rb) * MR + r0 - 32;
     }
     rsrc[t] = buffer_rsrc_words(base, rows * row_bytes);
     voff[t] = static_cast<int>((row + lane / kLanesPerRow) * row_bytes) +
@@ -920,7 +923,7 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
       for (int w = 1; w < S::WAVES; ++w) sum += partial[w][i * T::FN + j][lane];
       acc[i][j] = sum;
     }
-  gemm_epilogue<EPI, T>(a, 0, tn, 0, wn, lane, acc);
+  gemm_epilogue<EPI, T>(a, rb, tn, 0, wn, lane, acc);
 }
 
 template <int EPI>
@@ -930,11 +933,16 @@ static hipError_t launch_skinny(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   if (a.m <= 16)
     return launch_kernel(gemm_skinny_kernel<EPI, 16>, dim3(static_cast<unsigned>(grid)),
                          dim3(SkinnyShape<16>::WAVES * kWave), 0, s, a);
-  return launch_kernel(gemm_skinny_kernel<EPI, 64>, dim3(static_cast<unsigned>(grid)),
+  // blocks of 64 rows side by side (grid.y); with an even pair count the
+  // blocks of one column pair run on one XCD (linear index mod 8) and share
+  // its W slabs through that XCD's L2
+  const unsigned blocks = static_cast<unsigned>((a.m + 63) / 64);
+  return launch_kernel(gemm_skinny_kernel<EPI, 64>, dim3(static_cast<unsigned>(grid), blocks),
                        dim3(SkinnyShape<64>::WAVES * kWave), 0, s, a);
 }
 
-// At most 64 rows of X: the skinny kernels.  Else 256-row tiles when there
+// At most 64 rows of X, or at most 256 over few columns: the skinny
+// kernels.  Else 256-row tiles when there
 // are at least as many as CUs (a partial last round runs as 128-row half
 // tiles); else 128-row tiles (a partial last round as 64-row half tiles),
 // unless there are fewer of those than CUs or at most 64 rows of X: then
@@ -944,6 +952,15 @@ template <int EPI>
 static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   if (a.m <= kSkinnyRows) return launch_skinny<EPI>(a, tiles_n, s);
   const int cus = gemm_device_cus(s);
+  // up to 256 rows over few columns: blocks of 64 rows through the skinny
+  // kernel while that stays within one workgroup per CU (M = 128: q / o /
+  // down_proj 30 -> 21, 32 -> 22, 103 -> 56 us; k / v up to M = 256 29 ->
+  // 18 us); past that, tiles (M = 192, q_proj: 35 us skinny, 30 tiled).
+  // Not for q|k|v, so that its per-matrix launches (matrix granularity)
+  // sum in the same order as the fused one and match it bit for bit.
+  if (EPI != kGemmQkvRope && a.m <= 4 * kSkinnyRows &&
+      (a.m + kSkinnyRows - 1) / kSkinnyRows * tiles_n * 4 <= cus)
+    return launch_skinny<EPI>(a, tiles_n, s);
   const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
   if (a.m > 128 && tiles256 >= cus)
     return launch_tiles<EPI, kTileK, GemmTile256, 3, GemmTile128x8, 4>(a, tiles_n, cus, s);

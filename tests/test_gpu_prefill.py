@@ -48,7 +48,9 @@ def linear_bound_report(actual, x, w):
     (2048, 1024, 448), (40, 512, 1088), (16, 4096, 4096), (11, 1024, 14336),
     (17, 384, 4096), (64, 4096, 4096), (65, 1024, 4096), (128, 4096, 14336)])
 def test_gemm_matches_oracle(gpu_device, m, n, k):
-    # m <= 16 and m <= 64: the two skinny kernels; m >= 65: tiles;
+    # m <= 16 and m <= 64: the two skinny kernels; m <= 256 over at most 64
+    # column pairs per 64-row block: blocks of the 64-row skinny kernel
+    # (130 x 1024, 128 x 4096, 65 x 1024, 129 x 200); else tiles;
     # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs.
     # Slab counts (K / 64): odd and even counts (1, 2, 3, 5, 6, 7, 17, 64,
     # 224) below and above the ring depth of each tile shape (256-row
@@ -86,7 +88,8 @@ def test_gemm_f32out_matches_float64(gpu_device, m):
 
 
 @pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (6, 4096, 14336),
-                                   (129, 4096, 14336)])
+                                   (129, 4096, 14336), (100, 1024, 4096),
+                                   (256, 1024, 4096)])
 def test_gemm_residual_matches_oracle(gpu_device, m, n, k):
     dev = gpu_device
     x = cases.normal_bf16((m, k), 111)
