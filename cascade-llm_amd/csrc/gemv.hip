@@ -265,12 +265,12 @@ __device__ __forceinline__ void tile_rows(const GemvArgs &a, int64_t tile,
 }
 
 // The memory operands of the epilogue (the residual or gate element of
-// each row; RoPE's cos / sin at the token's position), loaded right after
-// the weights so that their latency hides under the weight stream instead
-// of following the reduction.
+// each row; RoPE's cos / sin at the token's position), loaded with the
+// input vector ahead of the weights (right after them where registers are
+// short), so that their latency hides under the weight stream instead of
+// following the reduction.
 template <int EPI, int R>
 __device__ __forceinline__ void epilogue_operands(const GemvArgs &a, int64_t tile,
-                                                  const bool (&ok)[R],
                                                   int64_t length_word,
                                                   float (&pre0)[R], float (&pre1)[R]) {
 #pragma unroll
@@ -421,10 +421,10 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
     InputRegs<NV> in;
     if constexpr (kEarly) {
       load_input<NV, WAVES * kWave, kEarlyW>(a, in);
-      epilogue_operands<EPI, R>(a, tile, ok, length_word, pre0, pre1);
+      epilogue_operands<EPI, R>(a, tile, length_word, pre0, pre1);
     }
-    // unconditional: a row past the matrix reads row 0 of w0 (tile_rows)
-    // and its sum is never stored
+    // unconditional: a row past the matrix reads row 0 of a matrix the
+    // launch has (tile_rows) and its sum is never stored
     u32x4 wv[R][KC];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
     if constexpr (kEarly) {
       store_input<NV, WAVES * kWave, kEarlyW>(a, in, xs);
     } else {
-      epilogue_operands<EPI, R>(a, tile, ok, length_word, pre0, pre1);
+      epilogue_operands<EPI, R>(a, tile, length_word, pre0, pre1);
       stage_input<WAVES * kWave>(a, xs);
     }
     __syncthreads();
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(WAVES *kWave) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] += acc2[r];
   } else {
-    epilogue_operands<EPI, R>(a, tile, ok, length_word, pre0, pre1);
+    epilogue_operands<EPI, R>(a, tile, length_word, pre0, pre1);
     stage_input<WAVES * kWave>(a, xs);
     __syncthreads();
     const int64_t nvec = a.k >> 3;
