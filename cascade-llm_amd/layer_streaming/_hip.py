@@ -15,6 +15,7 @@ entry point raises :class:`HipLibraryError`.
 import ctypes
 import os
 import threading
+import weakref
 
 import torch
 
@@ -812,16 +813,23 @@ def device_numa_node(device=None):
         return -1
 
 
+def _destroy_copy_pool(handle):
+    call("cascade_copy_pool_destroy", handle)
+
+
 class CopyPool:
     """A caller-owned pool for the multi-threaded host copy: ``threads``
     threads in all (the caller and threads - 1 helpers), the helpers bound
-    to the CPUs of ``numa_node`` when it is >= 0.  ``close`` joins them."""
+    to the CPUs of ``numa_node`` when it is >= 0.  ``close`` joins them (as
+    does garbage collection, or interpreter exit, of an unclosed pool); no
+    copy may be running on the pool then."""
 
     def __init__(self, threads=None, numa_node=-1):
         handle = _U64(0)
         call("cascade_copy_pool_create", int(threads or default_copy_threads()),
              int(numa_node), ctypes.byref(handle))
         self.handle = handle.value
+        self._finalizer = weakref.finalize(self, _destroy_copy_pool, self.handle)
         threads_out, bound = _INT(0), _INT(0)
         call("cascade_copy_pool_info", self.handle, ctypes.byref(threads_out),
              ctypes.byref(bound))
@@ -839,8 +847,8 @@ class CopyPool:
 
     def close(self):
         if self.handle:
-            handle, self.handle = self.handle, 0
-            call("cascade_copy_pool_destroy", handle)
+            self.handle = 0
+            self._finalizer()  # destroys the native pool, once
 
     def __enter__(self):
         return self

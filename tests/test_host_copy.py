@@ -91,6 +91,18 @@ def test_copy_pool_rejects_bad_arguments():
                   buf.data_ptr() + 512, 256)
 
 
+def test_copy_pool_is_destroyed_when_collected():
+    import gc
+    import weakref
+
+    pool = _hip.CopyPool(3)
+    finalizer = pool._finalizer
+    ref = weakref.ref(pool)
+    del pool
+    gc.collect()
+    assert ref() is None and not finalizer.alive  # native pool destroyed
+
+
 @pytest.mark.parametrize("pooled", [False, True])
 def test_host_copy_concurrent_callers(pooled):
     # the staging store calls from two worker threads at once
