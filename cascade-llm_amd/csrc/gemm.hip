@@ -945,9 +945,9 @@ static hipError_t launch_skinny(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
 // kernels.  Else 256-row tiles when there
 // are at least as many as CUs (a partial last round runs as 128-row half
 // tiles); else 128-row tiles (a partial last round as 64-row half tiles),
-// unless there are fewer of those than CUs or at most 64 rows of X: then
-// 64-row tiles (the K / V projections, N = 1024, at M = 2048, and short
-// prompts).
+// unless there are fewer of those than CUs and 64-row tiles need no more
+// than twice their rounds: then 64-row tiles (the K / V projections,
+// N = 1024, at M = 2048, and short prompts).
 template <int EPI>
 static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   if (a.m <= kSkinnyRows) return launch_skinny<EPI>(a, tiles_n, s);
@@ -965,7 +965,13 @@ static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
   if (a.m > 128 && tiles256 >= cus)
     return launch_tiles<EPI, kTileK, GemmTile256, 3, GemmTile128x8, 4>(a, tiles_n, cus, s);
   const int64_t tiles128 = (a.m + 127) / 128 * tiles_n;
-  if (a.m <= 64 || tiles128 < cus) return launch_tiles<EPI, kTileK, GemmTile64, 6>(a, tiles_n, cus, s);
+  // fewer than one round of 128-row tiles still wins where it takes half
+  // the rounds of 64-row tiles (M = 192 / 256, N = 14336: 61.8 -> 39.1 /
+  // 62.6 -> 45.1 us)
+  const int64_t rounds64 = ((a.m + 63) / 64 * tiles_n + cus - 1) / cus;
+  const int64_t rounds128 = (tiles128 + cus - 1) / cus;
+  if (a.m <= 64 || (tiles128 < cus && 2 * rounds128 > rounds64))
+    return launch_tiles<EPI, kTileK, GemmTile64, 6>(a, tiles_n, cus, s);
   return launch_tiles<EPI, kTileK, GemmTile128, 4, GemmTile64, 6>(a, tiles_n, cus, s);
 }
 

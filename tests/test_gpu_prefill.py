@@ -46,11 +46,14 @@ def linear_bound_report(actual, x, w):
     (5, 1000, 4096), (129, 200, 128), (7, 1001, 128),
     (2048, 4096, 192), (2048, 4096, 320), (2048, 1024, 384),
     (2048, 1024, 448), (40, 512, 1088), (16, 4096, 4096), (11, 1024, 14336),
-    (17, 384, 4096), (64, 4096, 4096), (65, 1024, 4096), (128, 4096, 14336)])
+    (17, 384, 4096), (64, 4096, 4096), (65, 1024, 4096), (128, 4096, 14336),
+    (192, 14336, 256), (256, 14336, 192)])
 def test_gemm_matches_oracle(gpu_device, m, n, k):
     # m <= 16 and m <= 64: the two skinny kernels; m <= 256 over at most 64
     # column pairs per 64-row block: blocks of the 64-row skinny kernel
-    # (130 x 1024, 128 x 4096, 65 x 1024, 129 x 200); else tiles;
+    # (130 x 1024, 128 x 4096, 65 x 1024, 129 x 200); else tiles (128-row
+    # tiles short of a round where 64-row ones would take two: 192 / 256 x
+    # 14336);
     # n = 1001: rows not 16-byte aligned, the element-wise epilogue runs.
     # Slab counts (K / 64): odd and even counts (1, 2, 3, 5, 6, 7, 17, 64,
     # 224) below and above the ring depth of each tile shape (256-row
@@ -108,7 +111,7 @@ def test_gemm_residual_matches_oracle(gpu_device, m, n, k):
     assert torch.equal(out.cpu(), res + xs)
 
 
-@pytest.mark.parametrize("m", [2, 6, 16, 200, 700])
+@pytest.mark.parametrize("m", [2, 6, 16, 192, 200, 700])
 def test_swiglu_gemm_fused_and_split_match_oracle(gpu_device, m):
     dev = gpu_device
     inter, hidden = 14336, 4096
