@@ -342,12 +342,12 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
 //   O += V_blk^T P (eight 16-dim tiles; P rounded to bf16 for the MFMA)
 // and positions past a column's own limit score -inf.
 //
-// Balance.  Tokens are cut into units of 4 waves x 4 NB tokens; unit u needs
-// blocks [0, len(u)), len growing along the causal triangle.  Workgroup
-// (pair p, KV head g) has 8 waves in two halves: half 0 walks unit A = p and
-// then the first `split` blocks of unit B = U - 1 - p, half 1 walks B's
-// blocks [split, len(B)); `split` evens the two walks, so all workgroups do
-// about the same work.  B's two partial softmax states are merged through
+// Balance.  Tokens are cut into units of HW waves x 4 NB tokens; unit u
+// needs blocks [0, len(u)), len growing along the causal triangle.
+// Workgroup (pair p, KV head g) has 2 HW waves in two halves: half 0 walks
+// unit A = p and then the first `split` blocks of unit B = U - 1 - p, half
+// 1 walks B's blocks [split, len(B)); `split` evens the two walks, so all
+// workgroups do about the same work.  B's two partial softmax states are merged through
 // LDS at the end (m, l, o of half 0 rescaled onto half 1's).
 //
 // Staging.  A half walks its blocks in lockstep; each block is moved once
@@ -368,10 +368,13 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
 // by more than kLazyRescale (log2 units); o and l share the stale maximum,
 // so the result is unchanged and most rescales are skipped.
 //
-// MI355X, S = 2048 (config 5, one layer): 55 us, against 150 us for one wave
-// per (4 NB tokens) reading K / V from L2 with no balancing.
-constexpr int kPrefillBlocks = 2;                         // MFMA column blocks per wave
-constexpr int kPrefillUnit = kAttnWaves * 4 * kPrefillBlocks;  // query tokens per unit
+// MI355X, S = 2048 (config 5, one layer): 55 us with NB = 2, HW = 4 (two
+// waves per SIMD), against 150 us for one wave per (4 NB tokens) reading
+// K / V from L2 with no balancing, 74 us for NB = 4, HW = 2 (one wave per
+// SIMD) and 96 us for NB = 1, HW = 8 (registers spilled).
+constexpr int kPrefillBlocks = 2;     // MFMA column blocks per wave
+constexpr int kPrefillHalfWaves = 4;  // waves per half of a workgroup
+constexpr int kPrefillUnit = kPrefillHalfWaves * 4 * kPrefillBlocks;  // query tokens per unit
 constexpr float kLazyRescale = 8.0f;
 
 struct PrefillArgs {
@@ -399,25 +402,27 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
   return __builtin_bit_cast(uint2, r);
 }
 
-template <int NB>
-__global__ __launch_bounds__(2 * kAttnWaves * kWave)
-__attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
+template <int NB, int HW>
+__global__ __launch_bounds__(2 * HW * kWave)
+__attribute__((amdgpu_waves_per_eu(HW / 2))) void prefill_attention_kernel(
     PrefillArgs a) {
   constexpr int G = kAttnG, D = kAttnD, TOK = 4 * NB;
-  constexpr int UNIT = kAttnWaves * TOK;
+  constexpr int UNIT = HW * TOK;
+  constexpr int LPW = 8 / HW;  // block load instructions per wave
+  static_assert(8 % HW == 0, "whole load instructions per wave");
   constexpr int BUF = kAttnBlock * D;
   __shared__ __attribute__((aligned(16))) uint16_t kbuf0[2][BUF];  // [half]
   __shared__ __attribute__((aligned(16))) uint16_t kbuf1[2][BUF];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf0[2][BUF];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf1[2][BUF];
-  __shared__ f32x4 mo[kAttnWaves][NB * 8][kWave];  // half 0's partial o of B
-  __shared__ float2 mml[kAttnWaves][NB][kWave];    // and its m, l
+  __shared__ f32x4 mo[HW][NB * 8][kWave];  // half 0's partial o of B
+  __shared__ float2 mml[HW][NB][kWave];    // and its m, l
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int half = wave / kAttnWaves;
-  const int w4 = wave % kAttnWaves;
+  const int half = wave / HW;
+  const int w4 = wave % HW;
   const int g = static_cast<int>(blockIdx.x) % a.kv_heads;
   const int pair = static_cast<int>(blockIdx.x) / a.kv_heads;
   const int c16 = lane & 15;
@@ -442,7 +447,8 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
 
   // block loads: instruction i (0..7) of a block fills slots 64 i .. 64 i + 63,
   // i.e. chunks 2 i, 2 i + 1 of all 32 rows; lane L takes chunk
-  // 2 i + L / 32 of row (L % 32) ^ (8 (L / 32)).  Wave w4 issues i = 2 w4, 2 w4 + 1.
+  // 2 i + L / 32 of row (L % 32) ^ (8 (L / 32)).  Wave w4 issues i = LPW w4 ..
+  // LPW w4 + LPW - 1.
   const int last_row = a.past + a.tokens - 1;
   const int ld_row = (lane & 31) ^ (8 * (lane >> 5));
   const int ld_chunk_bytes = 16 * (lane >> 5);
@@ -450,11 +456,11 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
       const_cast<uint16_t *>(a.k + g * a.head_stride), 0, (last_row + 1) * D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(a.v + g * a.head_stride), 0, (last_row + 1) * D * 2, 0x00020000);
-  auto load_block = [&](__amdgpu_buffer_rsrc_t rsrc, uint16_t *dst, int blk) {
+  auto load_block = [&](__amdgpu_buffer_rsrc_t rsrc, uint16_t *dst, int blk) __attribute__((always_inline)) {
     const int voff = min(blk * kAttnBlock + ld_row, last_row) * (D * 2) + ld_chunk_bytes;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = 2 * w4 + h;
+    for (int h = 0; h < LPW; ++h) {
+      const int i = LPW * w4 + h;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rsrc, (__attribute__((address_space(3))) void *)(dst + 64 * 8 * i), 16,
           voff, 32 * i, 0, 0);
@@ -475,7 +481,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
   u32x4 qop[NB][4];
   float m[NB], l[NB];
   f32x4 o[NB][8];
-  auto begin_unit = [&](int u) {
+  auto begin_unit = [&](int u) __attribute__((always_inline)) {
     const int t0 = u * UNIT + w4 * TOK;
     lim_min = a.past + t0;
 #pragma unroll
@@ -494,7 +500,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
       for (int e = 0; e < 8; ++e) o[b][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   };
-  auto write_out = [&]() {
+  auto write_out = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const float lb = xor32_sum(xor16_sum(l[b]));
@@ -511,7 +517,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
       }
     }
   };
-  auto read_k = [&](const uint16_t *buf, u32x4 (&kt)[2][4]) {
+  auto read_k = [&](const uint16_t *buf, u32x4 (&kt)[2][4]) __attribute__((always_inline)) {
     const char *base = reinterpret_cast<const char *>(buf) + k_base;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
@@ -519,7 +525,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
       for (int cc = 0; cc < 4; ++cc)
         kt[hf][cc] = *reinterpret_cast<const u32x4 *>(base + 2048 * cc + 256 * hf);
   };
-  auto read_v = [&](const uint16_t *buf, u32x4 (&vf)[8]) {
+  auto read_v = [&](const uint16_t *buf, u32x4 (&vf)[8]) __attribute__((always_inline)) {
     const char *base = reinterpret_cast<const char *>(buf) + v_base;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -549,7 +555,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void prefill_attention_kernel(
   // step j, parity P = j & 1: K_{j+2} -> kbuf[P], V_{j+1} -> vbuf[1-P];
   // reads V_j from vbuf[P] and K_{j+1} from kbuf[1-P]
   auto step = [&](int j, uint16_t *k_here, const uint16_t *k_next,
-                  const uint16_t *v_here, uint16_t *v_next) {
+                  const uint16_t *v_here, uint16_t *v_next) __attribute__((always_inline)) {
     const int blk = block_at(j);
     const int nb1 = block_at(j + 1);
     const int nb2 = block_at(j + 2);
@@ -880,8 +886,8 @@ extern "C" int cascade_prefill_attention_bf16(
   // consecutive KV heads
   const int64_t workgroups = (a.units + 1) / 2 * n_kv_heads;
   if (workgroups > 0x7fffffff) return CASCADE_EINVAL;
-  return launch_kernel(prefill_attention_kernel<kPrefillBlocks>,
+  return launch_kernel(prefill_attention_kernel<kPrefillBlocks, kPrefillHalfWaves>,
                        dim3(static_cast<unsigned>(workgroups)),
-                       dim3(2 * kAttnWaves * kWave), 0,
+                       dim3(2 * kPrefillHalfWaves * kWave), 0,
                        static_cast<hipStream_t>(stream), a);
 }
