@@ -12,6 +12,10 @@
 // slabs; each wave owns 64 rows x 64 (or 32) columns of
 // v_mfma_f32_16x16x32_bf16 fragments and reads its A and B fragments (16
 // bytes a lane) from LDS.  Shapes (launch_gemm picks one):
+//   GemmTileWide 256 x 256 (two 128-column sub-tiles), 8 waves of 128 x 64,
+//                32-deep slabs on a ring of 4: where its schedule of rounds
+//                is shorter than GemmTile256's (the fused gate|up at
+//                M = 2048: 3 rounds, then a round of 128 x 256 half tiles);
 //   GemmTile256  256 x 128, 8 waves, a ring of 3 slab buffers: the large
 //                GEMMs (at least as many 256-row tiles as CUs: q, o, gate,
 //                up, down at M = 2048);
@@ -138,18 +142,22 @@ __device__ __forceinline__ bool gemm_tile(int t, int tiles, int tiles_m, int til
   return true;
 }
 
-// Tile shapes.  Every tile is 128 columns wide (one head of q|k|v, or 64
-// gate + 64 up rows); BM rows of X are split over WM x WN waves, each
-// owning FM x FN fragments of 16 x 16.
-template <int BM_, int WM_, int WN_>
+// Tile shapes.  A tile is NSUB sub-tiles of 128 columns side by side (a
+// sub-tile is one head of q|k|v, or 64 gate + 64 up rows); the BM rows of a
+// sub-tile are split over WM x WN waves, each owning FM x FN fragments of
+// 16 x 16.
+template <int BM_, int WM_, int WN_, int NSUB_ = 1>
 struct GemmTile {
   static constexpr int BM = BM_;
   static constexpr int WM = WM_;
   static constexpr int WN = WN_;
-  static constexpr int WAVES = WM * WN;
+  static constexpr int NSUB = NSUB_;
+  static constexpr int BN = kTileN * NSUB;
+  static constexpr int SUBWAVES = WM * WN;  // waves of one sub-tile
+  static constexpr int WAVES = SUBWAVES * NSUB;
   static constexpr int FM = BM / WM / 16;
   static constexpr int FN = kTileN / WN / 16;
-  static constexpr int H = FN / 2;  // fragments per half tile
+  static constexpr int H = FN / 2;  // fragments per half sub-tile
   // staged epilogue: bf16 per staged column (BM rows + 8 pad; the column
   // stride is 4 banks mod 64, so 16 lanes writing 16 columns hit 16
   // distinct 4-bank groups)
@@ -160,6 +168,8 @@ using GemmTile256 = GemmTile<256, 4, 2>;  // 8 waves of 64 x 64
 using GemmTile128 = GemmTile<128, 2, 2>;  // 4 waves of 64 x 64
 using GemmTile64 = GemmTile<64, 1, 4>;    // 4 waves of 64 x 32
 using GemmTile128x8 = GemmTile<128, 2, 4>;  // 8 waves of 64 x 32 (half of GemmTile256)
+using GemmTileWide = GemmTile<256, 2, 2, 2>;      // 8 waves of 128 x 64, 256 columns
+using GemmTileWideHalf = GemmTile<128, 2, 2, 2>;  // 8 waves of 64 x 64, 256 columns
 
 // Tile column of fragment j of wave column wn for lane row lr.  A wave's
 // first-half fragments (j < H) and second-half fragments (j >= H) sit 64
@@ -283,16 +293,16 @@ __device__ __forceinline__ void gemm_epilogue_staged(
   const int lr = lane & 15;
   const int lq = lane >> 4;
   const int arow = (T::BM / T::WM) * wm;
-  // items: 16 rows x 32 columns of the output tile; lane (g, i) of a wave
-  // takes row i, columns 8 g .. 8 g + 7 of the item.  Wave w takes items
-  // w, w + 4, ...
+  // items: 16 rows x 32 columns of the output sub-tile; lane (g, i) of a
+  // wave takes row i, columns 8 g .. 8 g + 7 of the item.  Wave w of the
+  // sub-tile takes items w, w + SUBWAVES, ...
   constexpr int TW = EPI == kGemmSwiglu || EPI == kGemmQkvRope ? 64 : kTileN;
   constexpr int kItems = (T::BM / 16) * (TW / 32);
-  constexpr int kPer = kItems / T::WAVES;
-  static_assert(kItems % T::WAVES == 0, "whole items per wave");
+  constexpr int kPer = kItems / T::SUBWAVES;
+  static_assert(kItems % T::SUBWAVES == 0, "whole items per wave");
   const int g = lq, li = lr;
-  auto item_r0 = [&](int n) { return 16 * ((wave + T::WAVES * n) / (TW / 32)); };
-  auto item_c0 = [&](int n) { return 32 * ((wave + T::WAVES * n) % (TW / 32)) + 8 * g; };
+  auto item_r0 = [&](int n) { return 16 * ((wave + T::SUBWAVES * n) / (TW / 32)); };
+  auto item_c0 = [&](int n) { return 32 * ((wave + T::SUBWAVES * n) % (TW / 32)) + 8 * g; };
   const int64_t ncols = a.n0;  // output width (SwiGLU: n_half)
 
   // ---- inputs the epilogue reads from memory, issued first so their
@@ -456,30 +466,34 @@ struct DmaSlab {
 template <class T, int STAGES, int BK = kTileK>
 struct GemmRing {
   static constexpr int XB = T::BM * BK;
-  static constexpr int WB = kTileN * BK;
+  static constexpr int WB = T::BN * BK;
   static constexpr int SLAB = XB + WB;
-  static constexpr int STAGE = kTileN * T::STAGE_COL;
+  static constexpr int STAGE = T::NSUB * kTileN * T::STAGE_COL;
   static constexpr int LDS = STAGES * SLAB > STAGE ? STAGES * SLAB : STAGE;
 };
 
-// Output tile (tm, tn) of shape T: rows tm * BM .., columns tn * 128 ..
-// (q|k|v: head tn; SwiGLU: gate / up rows tn * 64 ..).  sb0 holds the ring.
+// Output tile (tm, tn) of shape T: rows tm * BM .., 128-column sub-tiles
+// tn * NSUB .. (q|k|v: head tn; SwiGLU: gate / up rows 64 per sub-tile).
+// sb0 holds the ring.
 template <int EPI, class T, int STAGES, int BK = kTileK>
 __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
                                               uint16_t *sb0) {
   static_assert(STAGES >= 3, "a ring of at least 3 slab buffers");
+  static_assert(T::NSUB == 1 || EPI != kGemmQkvRope, "q|k|v: one head per tile");
   using L = DmaSlab<BK>;
   using R = GemmRing<T, STAGES, BK>;
   constexpr int XI = T::BM * L::ROWB / 1024;  // load instructions per X slab
-  constexpr int WI = kTileN * L::ROWB / 1024;
+  constexpr int WI = T::BN * L::ROWB / 1024;
   constexpr int XW = XI / T::WAVES, WW = WI / T::WAVES;  // per wave
   static_assert(XI % T::WAVES == 0 && WI % T::WAVES == 0, "whole loads per wave");
   constexpr int XB = R::XB, kSlab = R::SLAB;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int wm = wave / T::WN;
-  const int wn = wave % T::WN;
+  const int sub = wave / T::SUBWAVES;  // sub-tile of the wave
+  const int sw = wave % T::SUBWAVES;
+  const int wm = sw / T::WN;
+  const int wn = sw % T::WN;
   const int lr = lane & 15;
   const int g4 = lane >> 4;
   const int64_t k_bytes = a.k * 2;
@@ -488,7 +502,7 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   const uint16_t *wbase0, *wbase1;
   int64_t wrows0, wrows1, wrow0, wrow1;  // rows of each matrix, first tile row in it
   if constexpr (EPI == kGemmSwiglu) {
-    wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kGemmHalfHead;
+    wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * T::NSUB * kGemmHalfHead;
     wbase1 = a.w1; wrows1 = a.n0; wrow1 = wrow0;
   } else if constexpr (EPI == kGemmQkvRope) {
     const int64_t hq = a.n0 / kGemmHead, hk = a.n1 / kGemmHead;
@@ -501,7 +515,7 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
     }
     wbase1 = wbase0; wrows1 = wrows0; wrow1 = wrow0;
   } else {
-    wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * kTileN;
+    wbase0 = a.w0; wrows0 = a.n0; wrow0 = static_cast<int64_t>(tn) * T::BN;
     wbase1 = wbase0; wrows1 = wrows0; wrow1 = wrow0;
   }
   const u32x4 xw = buffer_rsrc_words(a.x, a.m * k_bytes);
@@ -553,8 +567,13 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
     for (int h = 0; h < WW; ++h) {
       const int i = wave * WW + h;
       const int trow = L::RPI * i;  // tile row of the instruction
-      const bool second = EPI == kGemmSwiglu && trow >= kGemmHalfHead;
-      const int64_t row = (second ? wrow1 : wrow0) + (second ? trow - kGemmHalfHead : trow);
+      // SwiGLU: sub-tile trow / 128 holds 64 gate rows, then their 64 up rows
+      const int tt = trow % kTileN;
+      const bool second = EPI == kGemmSwiglu && tt >= kGemmHalfHead;
+      const int64_t row =
+          EPI == kGemmSwiglu
+              ? (second ? wrow1 : wrow0) + (trow / kTileN) * kGemmHalfHead + tt % kGemmHalfHead
+              : wrow0 + trow;
       dma_lds16(second ? ww1 : ww0,
                 ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
                 dw + i * 1024);
@@ -597,7 +616,7 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
 #pragma unroll
       for (int j = 0; j < T::FN; ++j)
         fb[ks][j] = *reinterpret_cast<const u32x4 *>(
-            aw + off + (gemm_col<T>(wn, j, lr) - lr) * L::ROWB);
+            aw + off + (kTileN * sub + gemm_col<T>(wn, j, lr) - lr) * L::ROWB);
     }
   };
   // publish: every LDS read issued so far stays above the wait (the empty
@@ -650,9 +669,10 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   __builtin_amdgcn_s_waitcnt(kWaitAll);
   if (EPI != kGemmF32 && a.vec_out) {
     __builtin_amdgcn_s_barrier();  // every wave's loads landed, ring read
-    gemm_epilogue_staged<EPI, T>(a, tm, tn, wm, wn, lane, wave, acc, sb0);
+    gemm_epilogue_staged<EPI, T>(a, tm, tn * T::NSUB + sub, wm, wn, lane, sw, acc,
+                                 sb0 + sub * (kTileN * T::STAGE_COL));
   } else {
-    gemm_epilogue<EPI, T>(a, tm, tn, wm, wn, lane, acc);
+    gemm_epilogue<EPI, T>(a, tm, tn * T::NSUB + sub, wm, wn, lane, acc);
   }
 }
 
@@ -941,10 +961,29 @@ static hipError_t launch_skinny(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
                        dim3(SkinnyShape<64>::WAVES * kWave), 0, s, a);
 }
 
+// Schedule of launch_tiles in rounds: whole rounds of full tiles, then a
+// round of half-height tiles (tail 1), a partial round of full tiles
+// (tail 2) or nothing (tail 0).
+struct TileRounds {
+  int64_t full;
+  int tail;
+};
+static TileRounds tile_rounds(int64_t tiles_m, int64_t tiles_n, int64_t htiles_m, int cus) {
+  const int64_t tiles = tiles_m * tiles_n;
+  const int64_t rem = tiles % cus;
+  if (rem == 0) return {tiles / cus, 0};
+  if (tiles > cus && 2 * rem <= cus) {
+    const int64_t cols = (rem + tiles_m - 1) / tiles_m;
+    if (cols < tiles_n && cols * htiles_m <= cus) return {tiles / cus, 1};
+  }
+  return {tiles / cus, 2};
+}
+
 // At most 64 rows of X, or at most 256 over few columns: the skinny
-// kernels.  Else 256-row tiles when there
-// are at least as many as CUs (a partial last round runs as 128-row half
-// tiles); else 128-row tiles (a partial last round as 64-row half tiles),
+// kernels.  Else 256-row tiles when there are at least as many as CUs: 256
+// columns wide where their schedule is shorter (below), else 128 wide (a
+// partial last round runs as 128-row half tiles); else 128-row tiles (a
+// partial last round as 64-row half tiles),
 // unless there are fewer of those than CUs and 64-row tiles need no more
 // than twice their rounds: then 64-row tiles (the K / V projections,
 // N = 1024, at M = 2048, and short prompts).
@@ -962,8 +1001,29 @@ static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
       (a.m + kSkinnyRows - 1) / kSkinnyRows * tiles_n * 4 <= cus)
     return launch_skinny<EPI>(a, tiles_n, s);
   const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
-  if (a.m > 128 && tiles256 >= cus)
+  if (a.m > 128 && tiles256 >= cus) {
+    // 256 x 256 tiles read a quarter less X and W per MFMA: a round of them
+    // takes 0.91 of two rounds of 256 x 128 tiles (M = 2048, N = 8192:
+    // 137.6 -> 125.5 us), and their half-height tail tiles (128 x 256) as
+    // long as one round of 256 x 128.  They need 32-deep slabs (a ring of
+    // four 32 KiB slabs; 64-deep ones would not fit three in the LDS), and
+    // SwiGLU whole pairs of 128-column gate / up groups.  q|k|v keeps one
+    // head per tile.  M = 2048, gate|up (N = 2 x 14336): 7 rounds of 256 x
+    // 128 tiles against 3 rounds + a half-height round of 256 x 256.
+    if constexpr (EPI != kGemmQkvRope) {
+      const int64_t tm256 = (a.m + 255) / 256, tm128 = (a.m + 127) / 128;
+      const int64_t wide_n = (tiles_n + 1) / 2;
+      const TileRounds std_r = tile_rounds(tm256, tiles_n, tm128, cus);
+      const TileRounds wide_r = tile_rounds(tm256, wide_n, tm128, cus);
+      constexpr double kWideRound = 1.82;  // in rounds of 256 x 128 tiles
+      const double std_t = static_cast<double>(std_r.full) + 0.5 * std_r.tail;
+      const double wide_t = kWideRound * static_cast<double>(wide_r.full) +
+                            (wide_r.tail == 1 ? 1.0 : wide_r.tail == 2 ? kWideRound : 0.0);
+      if (wide_t < std_t && (EPI != kGemmSwiglu || tiles_n % 2 == 0))
+        return launch_tiles<EPI, 32, GemmTileWide, 4, GemmTileWideHalf, 4>(a, wide_n, cus, s);
+    }
     return launch_tiles<EPI, kTileK, GemmTile256, 3, GemmTile128x8, 4>(a, tiles_n, cus, s);
+  }
   const int64_t tiles128 = (a.m + 127) / 128 * tiles_n;
   // fewer than one round of 128-row tiles still wins where it takes half
   // the rounds of 64-row tiles (M = 192 / 256, N = 14336: 61.8 -> 39.1 /

@@ -176,6 +176,55 @@ def test_gemm_half_tile_tail_matches_oracle(gpu_device, m, n, k):
     assert torch.equal(fused.cpu(), split.cpu())
 
 
+# Outputs whose schedule of 256 x 256 tiles (two 128-column sub-tiles per
+# workgroup, 32-deep slabs) is shorter than that of 256 x 128 tiles run on
+# them: 8000 columns (63 128-column tiles, the last one partial, so the last
+# workgroup's second sub-tile lies past the output; k = 64: fewer slabs
+# than the ring holds), 8192 (one whole round), 600 x 28672 and 2048 x
+# 28672 (a last round of 128 x 256 half-height tiles; SwiGLU over 2 x 28672
+# rows: whole rounds, and at m = 600 a partial last round).  The split
+# SwiGLU halves of 8192 / 28672 run on 256 x 128 or 256 x 256 tiles by the
+# same rule, and the fused result equals the split one bit for bit either
+# way (the K order of the MFMAs does not depend on the slab depth).
+@pytest.mark.parametrize("m,n,k", [(2048, 8000, 64), (2048, 8192, 128),
+                                   (600, 28672, 320), (2048, 28672, 64)])
+def test_gemm_wide_tiles_match_oracle(gpu_device, m, n, k):
+    print("wide tiles m={} n={} k={}".format(m, n, k), flush=True)
+    dev = gpu_device
+    x = cases.normal_bf16((m, k), 181)
+    w = cases.normal_bf16((n, k), 182, 0.05)
+    w2 = cases.normal_bf16((n, k), 183, 0.05)
+    res = cases.normal_bf16((m, n), 184)
+    xd, wd, w2d = x.to(dev), w.to(dev), w2.to(dev)
+    lin = ref.linear(x, w)
+    y = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm(xd, wd, y)
+    assert linear_bound_report(y, x, w) <= 1.0
+    r = cases.compare(y, lin)
+    assert r["ok"], r
+    yf = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _hip.gemm_f32out(xd, wd, yf)
+    r = cases.compare(yf, ref.linear_exact(x, w).float(), atol=1e-4, rtol=1e-4)
+    assert r["ok"], r
+    out = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm_residual(xd, wd, res.to(dev), out)
+    r = cases.compare(out, res + lin)
+    assert r["ok"], r
+    if n % 128:
+        return  # fused SwiGLU pairs whole 128-column gate / up groups
+    g = torch.empty((m, n), dtype=BF16, device=dev)
+    split = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gate_silu_gemm(xd, wd, g)
+    _hip.up_mul_gemm(xd, w2d, g, split)
+    r = cases.compare(g, F.silu(lin))
+    assert r["ok"], r
+    r = cases.compare(split, F.silu(lin) * ref.linear(x, w2))
+    assert r["ok"], r
+    fused = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gate_up_swiglu_gemm(xd, wd, w2d, fused)
+    assert torch.equal(fused.cpu(), split.cpu())
+
+
 def _rope_tables(positions):
     inv = ref.llama3_inv_freq(DIM)
     cos, sin = ref.rope_cos_sin(inv, list(range(positions)))
