@@ -8,8 +8,9 @@
 // input (layer_streaming/llama31.py:241-279 during the prefill call, and the
 // resident LM head, llama31.py:330-334).
 //
-// Tiling.  A workgroup computes a BM x 128 output tile, K walked in 64-deep
-// slabs; each wave owns 64 rows x 64 (or 32) columns of
+// Tiling.  A workgroup computes a BM x 128 output tile (or two side by
+// side), K walked in 64-deep slabs (32-deep for the 256-column tiles); each
+// wave owns 64 (or 128) rows x 64 (or 32) columns of
 // v_mfma_f32_16x16x32_bf16 fragments and reads its A and B fragments (16
 // bytes a lane) from LDS.  Shapes (launch_gemm picks one):
 //   GemmTileWide 256 x 256 (two 128-column sub-tiles), 8 waves of 128 x 64,
@@ -25,7 +26,8 @@
 //                prompts of at most 64 tokens).
 // When the last round of tiles would leave at least half of the CUs idle,
 // the last tile columns run as tiles of half the height in the same launch
-// (GemmTile128x8 for GemmTile256, GemmTile64 for GemmTile128): M = 2048,
+// (GemmTileWideHalf, 128 x 256, for GemmTileWide; GemmTile128x8 for
+// GemmTile256; GemmTile64 for GemmTile128): M = 2048,
 // N = 14336 runs 768 full tiles in three rounds, then 256 half tiles,
 // instead of three and a half rounds of full tiles.
 //
@@ -41,7 +43,8 @@
 // on an LDS read.
 //
 // LDS layout of a slab: 128-byte rows (64 bf16) back to back; 16-byte
-// chunk c of row r sits at chunk c ^ ((r / 2) % 8).  A fragment read (16
+// chunk c of row r sits at chunk c ^ ((r / 2) % 8) (32-deep slabs: 64-byte
+// rows, chunk c ^ ((r / 4) % 4)).  A fragment read (16
 // lanes: 16 consecutive rows, one chunk) then hits 16 distinct 16-byte bank
 // groups, each read is a per-lane base plus an immediate offset, and a load
 // instruction (64 lanes x 16 bytes) fills 8 whole rows, so its lanes read
