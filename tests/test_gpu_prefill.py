@@ -225,6 +225,55 @@ def test_gemm_wide_tiles_match_oracle(gpu_device, m, n, k):
     assert torch.equal(fused.cpu(), split.cpu())
 
 
+# Seeded random shapes across the tile-shape rule (256 x 128 or 256 x 256
+# tiles by their schedule of rounds, half-height tails, 128- and 64-row
+# tiles): every epilogue output stays within the float64 product bound and
+# the fused SwiGLU equals the split one.
+def _random_gemm_shapes(count, seed):
+    import random
+    rng = random.Random(seed)
+    shapes = []
+    for _ in range(count):
+        m = rng.choice([rng.randint(129, 700), rng.randint(700, 3100)])
+        n = rng.choice([8 * rng.randint(32, 5000), 128 * rng.randint(2, 300)])
+        n = min(n, (24_000_000 // m) // 128 * 128)  # keeps the oracle quick
+        shapes.append((m, n, 64 * rng.randint(1, 3)))
+    return shapes
+
+
+# seed 11: 256 x 256 tiles with and without a half-height round, 256 x 128
+# tiles, 128- and 64-row tiles, and SwiGLU on 256 x 256 and 128-row tiles
+@pytest.mark.parametrize("m,n,k", _random_gemm_shapes(8, 11))
+def test_gemm_random_shapes_match_oracle(gpu_device, m, n, k):
+    print("random shape m={} n={} k={}".format(m, n, k), flush=True)
+    dev = gpu_device
+    x = cases.normal_bf16((m, k), 191)
+    w = cases.normal_bf16((n, k), 192, 0.05)
+    res = cases.normal_bf16((m, n), 193)
+    xd, wd = x.to(dev), w.to(dev)
+    y = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm(xd, wd, y)
+    assert linear_bound_report(y, x, w) <= 1.0
+    out = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm_residual(xd, wd, res.to(dev), out)
+    r = cases.compare(out, res + ref.linear(x, w))
+    assert r["ok"], r
+    yf = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _hip.gemm_f32out(xd, wd, yf)
+    r = cases.compare(yf, ref.linear_exact(x, w).float(), atol=1e-4, rtol=1e-4)
+    assert r["ok"], r
+    if n % 128:
+        return
+    w2d = cases.normal_bf16((n, k), 194, 0.05).to(dev)
+    g = torch.empty((m, n), dtype=BF16, device=dev)
+    split = torch.empty_like(g)
+    fused = torch.empty_like(g)
+    _hip.gate_silu_gemm(xd, wd, g)
+    _hip.up_mul_gemm(xd, w2d, g, split)
+    _hip.gate_up_swiglu_gemm(xd, wd, w2d, fused)
+    assert torch.equal(fused.cpu(), split.cpu())
+
+
 def _rope_tables(positions):
     inv = ref.llama3_inv_freq(DIM)
     cos, sin = ref.rope_cos_sin(inv, list(range(positions)))
