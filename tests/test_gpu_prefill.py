@@ -314,10 +314,13 @@ def test_qkv_rope_gemm_matches_oracle(gpu_device, m, pos0):
         assert int(buf[:, slot0 + m:].abs().sum()) == 0
 
 
-def test_qkv_rope_gemm_split_matrices_equal_fused(gpu_device):
-    # matrix granularity: q, k, v in three launches == one fused launch
+# matrix granularity: q, k, v in three launches == one fused launch; at
+# m = 2048 the fused launch takes three heads per tile (32-deep slabs) and
+# the split ones 256 x 128 / 64 x 128 tiles (64-deep), in the same K order
+@pytest.mark.parametrize("m", [70, 2048])
+def test_qkv_rope_gemm_split_matrices_equal_fused(gpu_device, m):
     dev = gpu_device
-    m, hidden, kv = 70, 4096, 1024
+    hidden, kv = 4096, 1024
     x = cases.normal_bf16((m, hidden), 141).to(dev)
     wq = cases.normal_bf16((hidden, hidden), 142, 0.02).to(dev)
     wk = cases.normal_bf16((kv, hidden), 143, 0.02).to(dev)
@@ -325,19 +328,20 @@ def test_qkv_rope_gemm_split_matrices_equal_fused(gpu_device):
     c, s = (t.to(dev) for t in _rope_tables(m + 10))
     outs = []
     for split in (False, True):
-        kc = torch.zeros((8, 128, DIM), dtype=BF16, device=dev)
+        cap = m + 58
+        kc = torch.zeros((8, cap, DIM), dtype=BF16, device=dev)
         vc = torch.zeros_like(kc)
         q = torch.zeros((m, hidden), dtype=BF16, device=dev)
         args = (c, s, 10)
         if split:
-            _hip.qkv_rope_gemm(x, wq, None, None, *args, q, None, None, 128 * DIM, 5)
+            _hip.qkv_rope_gemm(x, wq, None, None, *args, q, None, None, cap * DIM, 5)
             _hip.qkv_rope_gemm(x, None, wk, None, *args, None, kc.view(-1), None,
-                               128 * DIM, 5)
+                               cap * DIM, 5)
             _hip.qkv_rope_gemm(x, None, None, wv, *args, None, None, vc.view(-1),
-                               128 * DIM, 5)
+                               cap * DIM, 5)
         else:
             _hip.qkv_rope_gemm(x, wq, wk, wv, *args, q, kc.view(-1), vc.view(-1),
-                               128 * DIM, 5)
+                               cap * DIM, 5)
         outs.append((q.cpu(), kc.cpu(), vc.cpu()))
     for a, b in zip(*outs):
         assert torch.equal(a, b)
