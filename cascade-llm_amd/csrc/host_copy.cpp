@@ -22,6 +22,7 @@
 #include <stddef.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -119,13 +120,24 @@ bool node_cpus(int node, std::vector<int> *cpus) {
   cpu_set_t allowed;
   CPU_ZERO(&allowed);
   if (sched_getaffinity(0, sizeof allowed, &allowed) != 0) return false;
-  for (char *tok = strtok(line, ",\n"); tok; tok = strtok(nullptr, ",\n")) {
-    int lo = 0, hi = 0;
-    const int got = sscanf(tok, "%d-%d", &lo, &hi);
-    if (got < 1) continue;
-    if (got == 1) hi = lo;
-    for (int c = lo; c <= hi && c < CPU_SETSIZE; ++c)
-      if (CPU_ISSET(c, &allowed)) cpus->push_back(c);
+  // "a" or "a-b" ranges separated by commas, parsed with strtol over a
+  // local cursor (no hidden parser state: pools may be created from
+  // several threads at once)
+  const char *p = line;
+  while (*p != '\0' && *p != '\n') {
+    char *end = nullptr;
+    const long lo = strtol(p, &end, 10);
+    if (end == p) break;  // not a number: malformed list, keep what we have
+    long hi = lo;
+    p = end;
+    if (*p == '-') {
+      hi = strtol(p + 1, &end, 10);
+      if (end == p + 1) break;
+      p = end;
+    }
+    for (long c = lo < 0 ? 0 : lo; c <= hi && c < CPU_SETSIZE; ++c)
+      if (CPU_ISSET(static_cast<int>(c), &allowed)) cpus->push_back(static_cast<int>(c));
+    if (*p == ',') ++p;
   }
   return true;
 }

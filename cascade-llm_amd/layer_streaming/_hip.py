@@ -115,7 +115,7 @@ _SIGNATURES = {
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 ESHAPE = 1003  # CASCADE_ESHAPE
 
 
@@ -813,7 +813,28 @@ def device_numa_node(device=None):
         return -1
 
 
-def _destroy_copy_pool(handle):
+class _PoolState:
+    """The native pool handle and the count of copies running on it, shared
+    by a CopyPool and its finalizer."""
+
+    __slots__ = ("handle", "busy", "lock")
+
+    def __init__(self, handle):
+        self.handle = handle
+        self.busy = 0
+        self.lock = threading.Lock()
+
+
+def _destroy_copy_pool(state):
+    with state.lock:
+        handle, state.handle = state.handle, 0
+        if not handle or state.busy:
+            # A copy is still running on the pool: only a daemon staging
+            # thread at interpreter exit can be inside one when the pool is
+            # finalized.  New copies are refused from here on, and the
+            # native pool, whose helpers that copy is using, is left to the
+            # process exit.
+            return
     call("cascade_copy_pool_destroy", handle)
 
 
@@ -821,34 +842,45 @@ class CopyPool:
     """A caller-owned pool for the multi-threaded host copy: ``threads``
     threads in all (the caller and threads - 1 helpers), the helpers bound
     to the CPUs of ``numa_node`` when it is >= 0.  ``close`` joins them (as
-    does garbage collection, or interpreter exit, of an unclosed pool); no
-    copy may be running on the pool then."""
+    does garbage collection, or interpreter exit, of an unclosed pool).  A
+    pool closed or finalized while a copy runs on it refuses new copies and
+    leaves the native pool alive for that copy (it is not destroyed then)."""
 
     def __init__(self, threads=None, numa_node=-1):
         handle = _U64(0)
         call("cascade_copy_pool_create", int(threads or default_copy_threads()),
              int(numa_node), ctypes.byref(handle))
-        self.handle = handle.value
-        self._finalizer = weakref.finalize(self, _destroy_copy_pool, self.handle)
+        self._state = _PoolState(handle.value)
+        self._finalizer = weakref.finalize(self, _destroy_copy_pool, self._state)
         threads_out, bound = _INT(0), _INT(0)
-        call("cascade_copy_pool_info", self.handle, ctypes.byref(threads_out),
+        call("cascade_copy_pool_info", handle.value, ctypes.byref(threads_out),
              ctypes.byref(bound))
         self.threads = threads_out.value
         self.bound_cpus = bound.value
         self.numa_node = int(numa_node)
 
+    @property
+    def handle(self):
+        return self._state.handle
+
     def copy(self, dst, src):
-        if not self.handle:
-            raise RuntimeError("the copy pool is closed")
         nbytes = _host_copy_bytes(dst, src)
-        call("cascade_copy_pool_copy", self.handle, dst.data_ptr(),
-             src.data_ptr(), nbytes)
+        state = self._state
+        with state.lock:
+            handle = state.handle
+            if not handle:
+                raise RuntimeError("the copy pool is closed")
+            state.busy += 1
+        try:
+            call("cascade_copy_pool_copy", handle, dst.data_ptr(),
+                 src.data_ptr(), nbytes)
+        finally:
+            with state.lock:
+                state.busy -= 1
         return dst
 
     def close(self):
-        if self.handle:
-            self.handle = 0
-            self._finalizer()  # destroys the native pool, once
+        self._finalizer()  # destroys the native pool, once
 
     def __enter__(self):
         return self

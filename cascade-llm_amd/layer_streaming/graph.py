@@ -69,9 +69,8 @@ class DecodeGraph:
     replays it.  ``tokens()`` returns the ids generated so far, in order.
 
     Requires an executor without a streamed vocabulary (the LM head is
-    resident), per-stage layer launches (``layer_mode="stages"``), and a
-    ResidentTransformerRuntime: streamed weights would put host copies and
-    cross-stream events in the step.
+    resident) and a ResidentTransformerRuntime: streamed weights would put
+    host copies and cross-stream events in the step.
     """
 
     def __init__(self, executor, runtime, token, max_new_tokens):

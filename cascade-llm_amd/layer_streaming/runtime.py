@@ -16,7 +16,9 @@
       them fired.
   Slots remember what they hold, so copies run ahead across calls (the LM
   head's first chunks behind the last units, the next call's first units
-  behind the last chunks).
+  behind the last chunks); they also remember the store generation the
+  bytes came from, and the store drains the runtime's copies (``quiesce``)
+  before it reloads, refills or frees its arena.
 * ``ResidentTransformerRuntime`` -- same ``run`` contract with every transfer
   unit resident in HBM (no streaming); the configuration used to measure
   the decode kernels against the HBM roofline.
@@ -203,7 +205,8 @@ class DoubleBufferRuntime:
         # that slot has been enqueued (VocabStreamingRuntime copies its
         # first chunks from here)
         self.release_hook = None
-        self._owner = [None] * self.slot_count      # (kind, index, ready event)
+        # (kind, index, ready event, store generation of the bytes)
+        self._owner = [None] * self.slot_count
         self._last_free = [None] * self.slot_count  # event of the last reader
         self._failed = False
         self._staging_left = {}
@@ -213,6 +216,9 @@ class DoubleBufferRuntime:
         self._free = [_hip.HipEvent() for _ in range(count)]
         self._start = _hip.HipEvent()
         self._timing = None
+        add_reader = getattr(store, "add_reader", None)
+        if add_reader is not None:
+            add_reader(self)  # the store drains our copies before its bytes change
 
     @property
     def stats(self):
@@ -262,16 +268,32 @@ class DoubleBufferRuntime:
         if timing is not None:
             timing[1].record(stream)
         ready.record(stream)
-        self._owner[slot] = (kind, index, ready)
+        self._owner[slot] = (kind, index, ready, self._store_generation())
+
+    def _store_generation(self):
+        return getattr(self.store, "generation", 0)
 
     def slot_holding(self, slot, kind, index):
         """Ready event of the copy that put (kind, index) in ``slot``, or
-        None when the slot holds something else."""
+        None when the slot holds something else, or bytes the store has
+        replaced since (load_checkpoint, fill_random, close)."""
 
         owner = self._owner[slot]
-        if owner is not None and owner[0] == kind and owner[1] == index:
+        if (owner is not None and owner[0] == kind and owner[1] == index
+                and owner[3] == self._store_generation()):
             return owner[2]
         return None
+
+    def quiesce(self):
+        """Wait until no copy or staging job of this runtime reads the
+        store's arena (called by the store before its bytes change)."""
+
+        for future in list(self._staging_left.values()):
+            try:
+                future.result()
+            except Exception:  # the run that made it already raised
+                pass
+        self.copy_stream.synchronize()
 
     def slot_released(self, slot, free):
         """``free`` (a compute-stream event) marks the end of the last
@@ -280,7 +302,9 @@ class DoubleBufferRuntime:
         self._last_free[slot] = free
 
     def discard_slots(self):
-        """Forget what the slots hold (after the host weights changed)."""
+        """Forget what the slots hold.  Not needed after the store's own
+        load_checkpoint / fill_random / close, which the slots notice by the
+        store's generation."""
 
         self._owner = [None] * self.slot_count
 

@@ -21,6 +21,12 @@ constructor arguments, ``tensor`` / ``unit_source`` / ``prepare_unit`` /
   straight into its arena bytes (``checkpoint.load_into``).
 * ``fill_random`` writes the seeded synthetic weights of the benchmark
   configurations (there is no checkpoint on the GPU hosts).
+* ``generation`` counts the times the arena's bytes changed (a load, a
+  fill, ``close``).  Runtimes that copy out of the arena asynchronously
+  register with ``add_reader``; before the bytes change, the store calls
+  each reader's ``quiesce()`` (which waits for its copies in flight), and
+  a runtime's device slots remember the generation they were filled from,
+  so a slot filled before a reload is never taken for the new weights.
 * ``tensor_factory`` stays injectable for tests, called as
   ``factory(elements, dtype=torch.bfloat16, device="cpu", pin_memory=...)``.
 """
@@ -30,6 +36,7 @@ from enum import Enum
 import queue
 import threading
 import time
+import weakref
 
 import torch
 
@@ -90,6 +97,8 @@ class BaseWeightStore:
         self.arena = None
         self._loaded = False
         self._layout = _layout_table(plan)
+        self.generation = 0
+        self._readers = weakref.WeakSet()
         if allocate:
             self.allocate()
 
@@ -109,12 +118,26 @@ class BaseWeightStore:
     def loaded(self):
         return self._loaded
 
+    def add_reader(self, reader):
+        """Register an object whose ``quiesce()`` waits for its reads of the
+        arena in flight (held weakly)."""
+
+        self._readers.add(reader)
+
+    def _bytes_changing(self):
+        # every asynchronous reader of the old bytes is done before they
+        # change, and the generation tells cached copies of them apart
+        for reader in list(self._readers):
+            reader.quiesce()
+        self.generation += 1
+
     def _host_buffer(self, elements, pinned):
         return self.tensor_factory(elements, dtype=torch.bfloat16, device="cpu",
                                    pin_memory=bool(pinned))
 
     def allocate(self):
         if self.arena is None:
+            self._bytes_changing()
             self.arena = self._host_buffer(self.plan.host_arena_elements,
                                            self.pin_full_arena)
         return self.arena
@@ -144,6 +167,7 @@ class BaseWeightStore:
         """Load a local safetensors checkpoint into the packed CPU arena."""
 
         self.allocate()
+        self._bytes_changing()
         _checkpoint.load_into(self, checkpoint)
         self._loaded = True
         return self
@@ -160,6 +184,7 @@ class BaseWeightStore:
         """
 
         self.allocate()
+        self._bytes_changing()
         draw_on = torch.device(device) if device is not None else torch.device("cpu")
         with torch.inference_mode():
             for index, (key, spec) in enumerate(self.plan.tensors.items()):
@@ -185,6 +210,8 @@ class BaseWeightStore:
         return self
 
     def close(self):
+        if self.arena is not None:
+            self._bytes_changing()
         self.arena = None
         self._loaded = False
 
@@ -423,6 +450,8 @@ class PinnedStagingWeightStore(BaseWeightStore):
 
     def close(self):
         if self._stager is not None:
+            if self.arena is not None:
+                self._bytes_changing()  # before the staging buffers go
             self._stager.close()
             self._stager = None
         super().close()

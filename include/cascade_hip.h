@@ -32,7 +32,9 @@
 extern "C" {
 #endif
 
-#define CASCADE_ABI_VERSION 1
+/* 2: cascade_hbm_read takes a workgroup count; the one-launch decoder layer
+   exports are gone. */
+#define CASCADE_ABI_VERSION 2
 
 /* Argument errors (no work enqueued). */
 #define CASCADE_EINVAL 1001     /* null pointer, bad size or count */

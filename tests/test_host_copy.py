@@ -70,6 +70,33 @@ def test_copy_pool_binds_helpers_to_a_node():
     assert torch.equal(dst, src)
 
 
+@pytest.mark.skipif(not os.path.exists("/sys/devices/system/node/node0/cpulist"),
+                    reason="no NUMA topology in sysfs")
+def test_copy_pools_created_concurrently_bind_the_same_cpus():
+    # the node's CPU list is parsed without shared parser state, so pools
+    # made from several threads at once all see the whole list
+    expected = len(_node_cpus(0))
+    counts, errors = [], []
+    start = threading.Barrier(8)
+
+    def make():
+        try:
+            start.wait()
+            for _ in range(20):
+                with _hip.CopyPool(2, numa_node=0) as pool:
+                    counts.append(pool.bound_cpus)
+        except Exception as error:  # reported below
+            errors.append(error)
+
+    threads = [threading.Thread(target=make) for _ in range(8)]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join()
+    assert not errors
+    assert counts == [expected] * 160
+
+
 def test_copy_pool_rejects_bad_arguments():
     with pytest.raises(_hip.HipCallError):  # no such NUMA node
         _hip.CopyPool(2, numa_node=4095)
@@ -143,3 +170,34 @@ def test_host_copy_rejects_bad_arguments():
         _hip.host_copy(buf[:10], buf[100:120])
     with pytest.raises(ValueError):  # not contiguous
         _hip.host_copy(buf[:10], buf[100:120:2])
+
+
+def test_pool_finalized_during_a_copy_leaves_that_copy_alone():
+    # what interpreter exit does to a daemon staging thread's pool: the
+    # finalizer runs while a copy is in progress; the copy completes, the
+    # native pool is not destroyed under it, and later copies are refused
+    src = torch.arange(96 << 20, dtype=torch.int32)  # 384 MiB, ~0.1 s on one thread
+    dst = torch.zeros_like(src)
+    pool = _hip.CopyPool(1)
+    started, outcome = threading.Event(), []
+
+    def copy():
+        started.set()
+        try:
+            pool.copy(dst, src)
+            outcome.append("done")
+        except Exception as error:  # reported below
+            outcome.append(error)
+
+    thread = threading.Thread(target=copy)
+    thread.start()
+    started.wait()
+    while pool._state.busy == 0 and thread.is_alive():
+        pass  # until the copy is inside the native call (or already over)
+    pool._finalizer()
+    thread.join()
+    assert outcome == ["done"]
+    assert torch.equal(dst, src)
+    assert pool.handle == 0
+    with pytest.raises(RuntimeError, match="closed"):
+        pool.copy(dst[:8], src[:8])

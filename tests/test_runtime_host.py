@@ -4,10 +4,13 @@ once, so a compute that runs before its copy sees stale slot bytes).
 
 Checked: every unit computes on its own weights; the host waits for copy i
 before it enqueues compute i; a copy into a slot waits for the event of the
-slot's last reader; the next call's first units are copied ahead (full_pinned)
-and reused, not copied again; a run that raises part-way is drained (staging
-jobs, both streams) before the next run reuses the slots, which then compute
-on the right weights (reference ordering: runtime.py:185-236).
+slot's last reader (with one slot: copy i + 1 waits for compute i); the next
+call's first units are copied ahead (full_pinned) and reused, not copied
+again, unless the store reloaded, refilled or freed its arena since (its
+generation), in which case the store first drains the copy stream; a run
+that raises part-way is drained (staging jobs, both streams) before the next
+run reuses the slots, which then compute on the right weights (reference
+ordering: runtime.py:93-106, :185-236).
 """
 
 import contextlib
@@ -120,13 +123,13 @@ class UnitChecker:
         return state
 
 
-def mark_units(store):
+def mark_units(store, base=0):
     # distinct values at both ends of every tensor (the rest stays as is)
     for index, (key, spec) in enumerate(store.plan.tensors.items()):
         if spec.alias_of is None:
             flat = store.tensor(key).reshape(-1)
-            flat[:4] = float(index + 1)
-            flat[-4:] = -float(index + 1)
+            flat[:4] = float(base + index + 1)
+            flat[-4:] = -float(base + index + 1)
 
 
 def events_of(log, kind):
@@ -204,3 +207,96 @@ def test_run_that_raised_is_drained_before_reuse(doubles):
     runtime.run(UnitChecker(store, doubles), state=None)
     assert ("stream_sync", "copy") not in doubles
     store.close()
+
+
+@pytest.mark.parametrize("mode", ["full_pinned", "pinned_staging"])
+def test_single_slot_copy_waits_for_previous_compute(doubles, mode):
+    # reference runtime.py:93-106 accepts one slot: unit i + 1 then reuses
+    # unit i's slot, so its copy must wait for compute i
+    plan = build_llama31_8b_plan("matrix_group", num_layers=1, stream_vocab=False)
+    store_cls = FullPinnedWeightStore if mode == "full_pinned" else PinnedStagingWeightStore
+    store = store_cls(plan, tensor_factory=cpu_factory)
+    mark_units(store)
+    runtime = rt.DoubleBufferRuntime(plan, store, resident=None, device="cpu",
+                                     slot_count=1)
+    assert len(runtime.device_slots) == 1 and runtime.stats.device_slot_count == 1
+    for call in range(2):
+        del doubles[:]
+        check = UnitChecker(store, doubles)
+        runtime.run(check, state=None)
+        assert check.seen == [u.unit_id for u in plan.units]
+        # every copy-stream wait names the free event of a unit whose
+        # compute is already recorded: earlier in this call, or (the first
+        # copy of a call) the previous call's last unit
+        free_ids = {ev.id: i for i, ev in enumerate(runtime._free)}
+        waits = [(index, entry) for index, entry in enumerate(doubles)
+                 if entry[0] == "wait" and entry[2] == "copy"]
+        copies = [index for index, entry in enumerate(doubles) if entry[0] == "copy"]
+        # one slot: every copy waits, except the very first copy into the
+        # fresh slot
+        if call == 0:
+            assert copies[0] < waits[0][0]
+            copies = copies[1:]
+        assert len(waits) == len(copies)
+        for (index, entry), copy_at in zip(waits, copies):
+            assert index < copy_at
+            unit = free_ids[entry[1]]
+            record = ("record", entry[1], "compute")
+            if record in doubles[:index]:
+                computed = doubles.index(("compute", plan.units[unit].unit_id))
+                assert computed < doubles.index(record) < index
+            else:
+                assert index == waits[0][0] and unit == len(plan.units) - 1
+    store.close()
+
+
+def _loading(monkeypatch, log, base):
+    # a checkpoint "load" that writes new bytes at the marked positions
+    from layer_streaming import weight_store as ws
+
+    def load_into(store, checkpoint):
+        log.append(("load", checkpoint))
+        mark_units(store, base=base)
+
+    monkeypatch.setattr(ws._checkpoint, "load_into", load_into)
+
+
+def test_reloaded_store_is_not_served_from_prefetched_slots(doubles, monkeypatch):
+    # units 0 and 1 sit in the slots after a run; a checkpoint load (no
+    # discard_slots) must drain the copy stream first and make the next run
+    # copy them again, computing on the new bytes
+    plan = tiny_plan()
+    store = FullPinnedWeightStore(plan, tensor_factory=cpu_factory)
+    mark_units(store)
+    runtime = rt.DoubleBufferRuntime(plan, store, resident=None, device="cpu")
+    runtime.run(UnitChecker(store, doubles), state=None)
+    assert runtime.slot_holding(0, "unit", 0) is not None
+    generation = store.generation
+    del doubles[:]
+    _loading(monkeypatch, doubles, base=1000)
+    store.load_checkpoint("weights.safetensors")
+    assert store.generation > generation
+    # the runtime's prefetch reading the arena finished before the new bytes
+    assert doubles.index(("stream_sync", "copy")) < doubles.index(
+        ("load", "weights.safetensors"))
+    assert runtime.slot_holding(0, "unit", 0) is None
+    del doubles[:]
+    check = UnitChecker(store, doubles)
+    runtime.run(check, state=None)
+    assert check.seen == [u.unit_id for u in plan.units]
+    assert len(events_of(doubles, "copy")) == len(plan.units) + 2
+    store.close()
+
+
+def test_store_close_drains_the_runtime_copies(doubles):
+    plan = tiny_plan()
+    store = FullPinnedWeightStore(plan, tensor_factory=cpu_factory)
+    mark_units(store)
+    runtime = rt.DoubleBufferRuntime(plan, store, resident=None, device="cpu")
+    runtime.run(UnitChecker(store, doubles), state=None)
+    del doubles[:]
+    store.close()
+    # the copies of the next call's first units (still reading the arena)
+    # were waited for before the arena was dropped
+    assert doubles == [("stream_sync", "copy")]
+    assert store.arena is None and runtime.slot_holding(0, "unit", 0) is None
