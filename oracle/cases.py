@@ -76,6 +76,120 @@ def within_noise_floor(actual, expected, alternative, factor=2.0):
             "ratio_to_floor": diff / floor}
 
 
+def blocked_attention(q, k, v, past, block=32):
+    """A second valid restatement of bf16 SDPA: an online softmax over
+    ``block``-row blocks of keys, each block's numerator exp(s - m) rounded
+    to bf16 against the running maximum m, the accumulator and the
+    denominator rescaled in fp32 when m grows (the flash-attention order of
+    the reference's CUDA SDPA, and of this build's kernels)."""
+
+    heads, seq, dim = q.shape
+    groups = heads // k.shape[0]
+    kf = k.float().repeat_interleave(groups, dim=0)
+    vf = v.float().repeat_interleave(groups, dim=0)
+    scores = (q.float() @ kf.transpose(1, 2)) / math.sqrt(dim)
+    length = k.shape[1]
+    allowed = torch.arange(length)[None, :] <= (past + torch.arange(seq))[:, None]
+    scores = scores.masked_fill(~allowed[None], float("-inf"))
+    m = torch.full((heads, seq, 1), float("-inf"))
+    den = torch.zeros(heads, seq, 1)
+    acc = torch.zeros(heads, seq, dim)
+    for start in range(0, length, block):
+        part = scores[..., start:start + block]
+        m_new = torch.maximum(m, part.amax(dim=-1, keepdim=True))
+        # rows whose keys so far are all masked keep m = -inf: weight 0
+        safe = torch.where(torch.isinf(m_new), torch.zeros_like(m_new), m_new)
+        alpha = torch.exp(m - safe)
+        p = torch.exp(part - safe)
+        den = den * alpha + p.sum(dim=-1, keepdim=True)
+        acc = acc * alpha + p.to(q.dtype).float() @ vf[:, start:start + block]
+        m = m_new
+    out = acc / den
+    return out.transpose(0, 1).reshape(seq, heads * dim).to(q.dtype)
+
+
+def alternative_layer(inp, weights, cache, past, cos, sin, eps, n_heads=32,
+                      n_kv_heads=8, trace=None):
+    """The decoder layer through the second valid restatements of its two
+    accumulating ops (sgemm_linear, blocked_attention): the reference's own
+    implementation-order noise, against which a GPU result is judged."""
+
+    return ref.decoder_layer(inp, weights, cache, past, cos, sin, eps, n_heads,
+                             n_kv_heads, linear_fn=sgemm_linear,
+                             attention_fn=blocked_attention, trace=trace)
+
+
+def alternative_model(tensor, num_layers, eps=1e-5):
+    """OracleLlama through the second valid restatements (sgemm_linear,
+    blocked_attention): the free-running noise floor of a whole model."""
+
+    return ref.OracleLlama(tensor, num_layers, eps, linear_fn=sgemm_linear,
+                           attention_fn=blocked_attention)
+
+
+def _row_scale(weight, x):
+    """Per output row, sqrt(sum_j (W_ij x_j)^2): the magnitude at which a
+    fp32-accumulated dot product's summation order moves its result."""
+
+    w2 = weight.float().square()
+    x2 = x.float().reshape(-1, weight.shape[1]).square()
+    return (x2 @ w2.t()).sqrt()
+
+
+def layer_rounding_scales(inp, trace, weights):
+    """Per element of a decoder layer's two bf16 residual sums, the largest
+    magnitude whose bf16 granularity the element passed through.
+
+    h_attn = inp + o:   |inp|, |o|, |h_attn| and the accumulation scale of
+                        o_proj over the attention output (_row_scale);
+    out = h_attn + down: those, |down|, |out| and the accumulation scale of
+                        down_proj over silu(gate) * up.
+    """
+
+    def largest(*parts):
+        return torch.stack([t.float().reshape(-1).abs() for t in parts]).amax(0)
+
+    kappa_o = _row_scale(weights["o"], trace["attn"]).reshape(-1)
+    kappa_d = _row_scale(weights["down"], trace["inter"]).reshape(-1)
+    attn_scale = largest(inp, trace["o"], trace["h_attn"], kappa_o)
+    out = trace["h_attn"] + trace["down"]
+    out_scale = torch.maximum(largest(trace["down"], out, kappa_d), attn_scale)
+    return {"h_attn": attn_scale, "out": out_scale}
+
+
+def bf16_ulps(magnitude):
+    """Elementwise bf16 spacing at |magnitude| (8 significant bits)."""
+
+    m = magnitude.float().abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(m)) - 7)
+
+
+# Per-element bound of a decoder layer's bf16 residual sums, in bf16 ulps of
+# layer_rounding_scales.  Calibrated on the CPU against the alternative
+# restatement (alternative_layer): over 96 seeded single-token layers (24
+# seeds x positions 31, 544, 2048, 4100) it deviates from the oracle by at
+# most 3 such ulps (mostly 2, mean 0.3), and over 16 prefills (8 seeds x
+# 512 and 2048 tokens) by at most 4 (mean 0.41-0.45): at most 0.5 of this
+# bound, so a correct GPU result passes with a factor of 2 to spare.
+# tests/test_oracle.py re-checks cases of both kinds and shows that
+# plausible mistakes exceed the bound.
+LAYER_ULPS = 8.0
+
+
+def within_rounding_bound(actual, expected, scale, ulps=LAYER_ULPS):
+    """|actual_i - expected_i| <= ulps * bf16_ulp(scale_i) for every element;
+    ``worst_ratio`` is the largest |difference| / bound."""
+
+    a = actual.detach().float().cpu().reshape(-1)
+    e = expected.detach().float().cpu().reshape(-1)
+    bound = ulps * bf16_ulps(scale.reshape(-1))
+    ratio = (a - e).abs() / bound
+    worst = float(ratio.max()) if ratio.numel() else 0.0
+    return {"ok": bool(worst <= 1.0), "worst_ratio": worst,
+            "max_abs": float((a - e).abs().max()) if a.numel() else 0.0,
+            "mean_ratio": float(ratio.mean()) if ratio.numel() else 0.0}
+
+
 def layer_case(seed, past, hidden=4096, intermediate=14336, n_heads=32,
                n_kv_heads=8, head_dim=128):
     """One decoder layer (BASELINE config 2 at past = 2048)."""
@@ -103,11 +217,13 @@ def layer_case(seed, past, hidden=4096, intermediate=14336, n_heads=32,
     }
 
 
-def layer_expected(case, linear=None):
+def layer_expected(case, linear=None, attention=None):
     """Oracle intermediates of one decode step at position ``past``
-    (``linear``: the GEMV restatement, default oracle.linear)."""
+    (``linear`` / ``attention``: the GEMV and attention restatements,
+    default oracle.linear / oracle.attention)."""
 
     linear = ref.linear if linear is None else linear
+    attention = ref.attention if attention is None else attention
     n_heads, n_kv, dim = case["n_heads"], case["n_kv_heads"], case["head_dim"]
     past = case["past"]
     eps = case["eps"]
@@ -122,13 +238,17 @@ def layer_expected(case, linear=None):
     k = ref.apply_rope(k, cos, sin)
     keys = torch.cat((case["k_cache"], k), dim=1)
     values = torch.cat((case["v_cache"], v), dim=1)
-    attn = ref.attention(q, keys, values, past)
-    h1 = x + linear(attn, case["o"])
+    attn = attention(q, keys, values, past)
+    o = linear(attn, case["o"])
+    h1 = x + o
     n2 = ref.rms_norm(h1, case["ln2"], eps)
     inter = torch.nn.functional.silu(linear(n2, case["gate"])) * linear(
         n2, case["up"])
-    out = h1 + linear(inter, case["down"])
+    down = linear(inter, case["down"])
+    out = h1 + down
     return {
+        "o": o.reshape(-1),
+        "down": down.reshape(-1),
         "q": q.transpose(0, 1).reshape(-1),
         "k_new": k[:, 0],
         "v_new": v[:, 0],
@@ -243,17 +363,25 @@ def layer_teacher_forced(inp, out, weights, k_full, v_full, past, cos, sin,
     cache [Hkv, past + S, D] after the call (positions < past are the
     inputs, the rest are the GPU's new K / V rows).  The oracle recomputes
     the layer from ``inp`` and the cache prefix (decoder_layer,
-    llama31.py:169-283); the output must lie within twice the summation-
-    order noise floor (within_noise_floor) and each new K / V row within
-    the north-star tolerance or that floor.
+    llama31.py:169-283).  Every element of the output must lie within
+    LAYER_ULPS bf16 ulps of its rounding scale (within_rounding_bound,
+    layer_rounding_scales); each new K / V row within the north-star
+    tolerance or twice the deviation of the alternative restatement
+    (alternative_layer: sgemm_linear and blocked_attention).
     """
 
     prefix = {"k": k_full[:, :past], "v": v_full[:, :past]} if past else {}
     alt_prefix = dict(prefix)
-    expected = ref.decoder_layer(inp, weights, prefix, past, cos, sin, eps)
-    alternative = ref.decoder_layer(inp, weights, alt_prefix, past, cos, sin,
-                                    eps, linear_fn=sgemm_linear)
-    report = {"out": within_noise_floor(out, expected, alternative)}
+    trace = {}
+    expected = ref.decoder_layer(inp, weights, prefix, past, cos, sin, eps,
+                                 trace=trace)
+    alternative = alternative_layer(inp, weights, alt_prefix, past, cos, sin, eps)
+    scale = layer_rounding_scales(inp, trace, weights)["out"]
+    report = {"out": within_rounding_bound(out, expected, scale)}
+    report["out"]["alternative_worst_ratio"] = within_rounding_bound(
+        alternative, expected, scale)["worst_ratio"]
+    report["out"]["ratio_to_floor"] = within_noise_floor(
+        out, expected, alternative)["ratio_to_floor"]
     ok = report["out"]["ok"]
     for name, gpu in (("k", k_full), ("v", v_full)):
         r = compare(gpu[:, past:], prefix[name][:, past:])

@@ -17,7 +17,9 @@ TF = transformers, the library the reference calls for RoPE):
   apply_rope          TF models/llama/modeling_llama.py:130-160,
                       called at llama31.py:206-212
   attention           _repeat_kv + F.scaled_dot_product_attention,
-                      llama31.py:28-31,213-234 (fp32 softmax, bf16 output)
+                      llama31.py:28-31,213-234 (fp32 scores, softmax
+                      numerator rounded to bf16 as bf16 SDPA does, bf16
+                      output)
   decoder_layer       llama31.py:169-283 (one whole layer, all S tokens)
   lm_head_logits      llama31.py:330-334, vocab.py:247 (fp32 logits; the
                       reference's bf16 rounding is optional)
@@ -128,10 +130,20 @@ def apply_rope(x, cos, sin):
     return (x * cos[None]) + (rotate_half(x) * sin[None])
 
 
-def attention(q, k, v, past):
+def attention(q, k, v, past, round_numerator=True):
     """q [H, S, D]; k / v [Hkv, past + S, D] (all bf16).  Query token t sees
     positions <= past + t (no mask at decode, causal at prefill, as
-    llama31.py:221-229).  fp32 scores and softmax, bf16 output [S, H*D]."""
+    llama31.py:221-229).  fp32 scores; output [S, H*D] in q's dtype.
+
+    The softmax numerator p = exp(s - rowmax) is rounded to q's dtype
+    before the product with V, and the denominator sums the unrounded p:
+    the rounding point of F.scaled_dot_product_attention on bf16 operands
+    (llama31.py:223-229; the reference's CPU path reaches it through
+    transformers' sdpa attention, benchmarks/real_llama31_correctness.py:
+    87-129).  Bit-exact against bf16 SDPA on the CPU for a prompt whose keys
+    fit one block of that kernel (tests/golden/tiny_llama_bf16.json); no-op
+    for fp32 operands.  ``round_numerator=False`` keeps p in fp32 (fp32
+    SDPA)."""
 
     heads, seq, dim = q.shape
     groups = heads // k.shape[0]
@@ -141,22 +153,29 @@ def attention(q, k, v, past):
     length = k.shape[1]
     allowed = torch.arange(length)[None, :] <= (past + torch.arange(seq))[:, None]
     scores = scores.masked_fill(~allowed[None], float("-inf"))
-    probs = torch.softmax(scores, dim=-1)
-    out = probs @ vf
+    numerator = torch.exp(scores - scores.amax(dim=-1, keepdim=True))
+    denominator = numerator.sum(dim=-1, keepdim=True)
+    if round_numerator:
+        numerator = numerator.to(q.dtype).float()
+    out = (numerator @ vf) / denominator
     return out.transpose(0, 1).reshape(seq, heads * dim).to(q.dtype)
 
 
 def decoder_layer(hidden, w, cache, past, cos, sin, eps, n_heads=32,
-                  n_kv_heads=8, linear_fn=None):
+                  n_kv_heads=8, linear_fn=None, attention_fn=None, trace=None):
     """One decoder layer for S tokens, llama31.py:169-283.
 
     hidden [S, H] bf16; w: dict with q, k, v, o, gate, up, down, ln1, ln2;
     cache: dict with "k" / "v" tensors [Hkv, past, D] (or None), updated in
-    place.  Returns the new hidden [S, H].  ``linear_fn`` replaces the GEMV
-    restatement (default: ``linear``).
+    place.  Returns the new hidden [S, H].  ``linear_fn`` / ``attention_fn``
+    replace the GEMV / attention restatements (default: ``linear``,
+    ``attention``).  A ``trace`` dict receives the intermediates: attn,
+    o (o_proj output), h_attn (after the first residual add), inter
+    (silu(gate) * up) and down (down_proj output).
     """
 
     linear = globals()["linear"] if linear_fn is None else linear_fn
+    attend = globals()["attention"] if attention_fn is None else attention_fn
     seq, width = hidden.shape
     dim = width // n_heads
     residual = hidden
@@ -170,13 +189,18 @@ def decoder_layer(hidden, w, cache, past, cos, sin, eps, n_heads=32,
         k = torch.cat((cache["k"], k), dim=1)
         v = torch.cat((cache["v"], v), dim=1)
     cache["k"], cache["v"] = k, v
-    attn = attention(q, k, v, past)
-    hidden = residual + linear(attn, w["o"])
+    attn = attend(q, k, v, past)
+    o = linear(attn, w["o"])
+    hidden = residual + o
     residual = hidden
     normalized = rms_norm(hidden, w["ln2"], eps)
     gate = F.silu(linear(normalized, w["gate"]))
     up = linear(normalized, w["up"])
-    return residual + linear(gate * up, w["down"])
+    inter = gate * up
+    down = linear(inter, w["down"])
+    if trace is not None:
+        trace.update(attn=attn, o=o, h_attn=hidden, inter=inter, down=down)
+    return residual + down
 
 
 # --------------------------------------------------------------- LM head
@@ -253,16 +277,19 @@ class OracleLlama:
     """Greedy batch=1 decoding of a Llama-3.1-8B-shaped model on the CPU.
 
     ``tensor(key)`` returns the bf16 CPU tensor of a checkpoint key (e.g. a
-    weight store's ``tensor``); ``linear_fn`` replaces the GEMV restatement
-    in every layer (default ``linear``).  Mirrors Llama31DecodeExecutor: begin
+    weight store's ``tensor``); ``linear_fn`` / ``attention_fn`` replace the
+    GEMV / attention restatements in every layer (default ``linear``,
+    ``attention``).  Mirrors Llama31DecodeExecutor: begin
     (embedding row gather), the layers, finish (final norm, fp32 logits of
     the last position, top-k).
     """
 
     def __init__(self, tensor, num_layers=32, eps=1e-5, rope=None,
-                 n_heads=32, n_kv_heads=8, head_dim=128, linear_fn=None):
+                 n_heads=32, n_kv_heads=8, head_dim=128, linear_fn=None,
+                 attention_fn=None):
         self.tensor = tensor
         self.linear_fn = linear_fn
+        self.attention_fn = attention_fn
         self.num_layers = int(num_layers)
         self.eps = float(eps)
         self.n_heads = n_heads
@@ -287,7 +314,7 @@ class OracleLlama:
             hidden = decoder_layer(
                 hidden, layer_weights(self.tensor, layer), self.caches[layer],
                 past, cos, sin, self.eps, self.n_heads, self.n_kv_heads,
-                linear_fn=self.linear_fn,
+                linear_fn=self.linear_fn, attention_fn=self.attention_fn,
             )
         self.length = past + ids.numel()
         normalized = rms_norm(hidden[-1:], self.tensor("model.norm.weight"), self.eps)

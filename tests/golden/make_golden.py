@@ -17,6 +17,21 @@ fixtures hold inputs and outputs only:
                      heads, SwiGLU 128, vocab 97, llama3 RoPE) with seeded
                      fp32 weights; its fp32 logits for a 6-token prompt and
                      a 4-token greedy continuation.
+  tiny_llama_bf16.json
+                     the reference's CPU path itself
+                     (benchmarks/real_llama31_correctness.py:87-129:
+                     AutoModelForCausalLM in bf16, default sdpa attention,
+                     greedy argmax) on a 2-layer model of the 8B's head
+                     geometry (hidden 512, 4 query heads of 128 sharing one
+                     KV head, SwiGLU 1024, vocab 97, llama3 RoPE): every
+                     decoder layer's output, the final norm and the bf16
+                     logits (as bf16 bits) for a 6-token prompt and 3
+                     greedy tokens.  The weights are not stored: the recipe
+                     below regenerates them (checksums included), and the
+                     parameters are cast to bf16 after construction with
+                     the RoPE inverse frequencies left in fp32, as
+                     from_pretrained(torch_dtype=torch.bfloat16) leaves
+                     them.
 """
 
 import json
@@ -119,11 +134,90 @@ def tiny_model_fixture():
     return arrays
 
 
+BF16_CONFIG = {"hidden_size": 512, "intermediate_size": 1024,
+               "num_hidden_layers": 2, "num_attention_heads": 4,
+               "num_key_value_heads": 1, "head_dim": 128, "vocab_size": 97,
+               "rms_norm_eps": 1e-5}
+BF16_PROMPT = [5, 17, 42, 3, 88, 61]
+
+
+def bf16_weight(index, shape):
+    """Weight recipe of the bf16 fixture: parameter ``index`` (in
+    named_parameters order) drawn in fp32 from its own generator, norm
+    vectors 1 + 0.1 N(0, 1), matrices 0.04 N(0, 1), rounded to bf16."""
+
+    gen = torch.Generator().manual_seed(1000 + index)
+    values = torch.randn(tuple(shape), generator=gen)
+    values = 1.0 + 0.1 * values if len(shape) == 1 else 0.04 * values
+    return values.to(torch.bfloat16)
+
+
+def tiny_bf16_fixture():
+    cfg = LlamaConfig(**BF16_CONFIG, rope_parameters=dict(ROPE),
+                      max_position_embeddings=131072, tie_word_embeddings=False,
+                      attn_implementation="sdpa")
+    model = LlamaForCausalLM(cfg).eval()
+    names, shapes, checksums = [], [], []
+    with torch.no_grad():
+        for index, (name, p) in enumerate(model.named_parameters()):
+            # parameters only: the rotary inverse frequencies stay fp32
+            p.data = bf16_weight(index, p.shape)
+            names.append(name)
+            shapes.append(list(p.shape))
+            checksums.append(float(p.data.double().sum()))
+    assert model.model.rotary_emb.inv_freq.dtype == torch.float32
+    layer_out = {}
+    hooks = [layer.register_forward_hook(
+        lambda mod, args, out, i=i: layer_out.__setitem__(i, out[0] if isinstance(out, tuple) else out))
+        for i, layer in enumerate(model.model.layers)]
+    hooks.append(model.model.norm.register_forward_hook(
+        lambda mod, args, out: layer_out.__setitem__("norm", out)))
+    steps, tokens = [], []
+    past = None
+    ids = list(BF16_PROMPT)
+    with torch.inference_mode():
+        for _ in range(4):
+            out = model(input_ids=torch.tensor([ids]), past_key_values=past,
+                        use_cache=True)
+            past = out.past_key_values
+            logits = out.logits[0, -1]
+            assert logits.dtype == torch.bfloat16
+            steps.append({
+                "ids": ids,
+                "layer_out_bf16_bits": [bits(layer_out[i][0])
+                                        for i in range(len(model.model.layers))],
+                "final_norm_bf16_bits": bits(layer_out["norm"][0]),
+                "logits_bf16_bits": bits(logits),
+            })
+            token = int(logits.float().argmax())  # the reference's greedy step
+            tokens.append(token)
+            ids = [token]
+    for hook in hooks:
+        hook.remove()
+    return {
+        "transformers_version": transformers.__version__,
+        "torch_version": torch.__version__,
+        "config": BF16_CONFIG,
+        "rope": ROPE,
+        "attn_implementation": "sdpa",
+        "weight_recipe": "bf16_weight(index, shape) in tests/golden/make_golden.py",
+        "weight_names": names,
+        "weight_shapes": shapes,
+        "weight_checksums": checksums,
+        "prompt": BF16_PROMPT,
+        "tokens": tokens,
+        "steps": steps,
+    }
+
+
 def main():
     (OUT / "rope_llama3.json").write_text(
         json.dumps(rope_fixture(), indent=1) + "\n", encoding="utf-8")
     np.savez_compressed(OUT / "tiny_llama.npz", **tiny_model_fixture())
-    print("wrote", OUT / "rope_llama3.json", OUT / "tiny_llama.npz")
+    (OUT / "tiny_llama_bf16.json").write_text(
+        json.dumps(tiny_bf16_fixture()) + "\n", encoding="utf-8")
+    print("wrote", OUT / "rope_llama3.json", OUT / "tiny_llama.npz",
+          OUT / "tiny_llama_bf16.json")
 
 
 if __name__ == "__main__":

@@ -7,15 +7,17 @@ CPU oracle.
 
 * Per call (prefill and each decode), teacher-forced layer by layer: the
   oracle recomputes each of the 32 layers from the GPU's input hidden rows
-  and cache prefix; outputs within twice the summation-order noise floor,
-  new K / V rows within the tolerance (oracle.cases.layer_teacher_forced).
+  and cache prefix; every output element within cases.LAYER_ULPS bf16 ulps
+  of its rounding scale, new K / V rows within the tolerance
+  (oracle.cases.layer_teacher_forced).
   The final logits (oracle final norm + fp32 LM head on the GPU's last
   hidden row) within |a - b| <= 2e-2 + 1e-2 |b|, the top-10 ids and order
   equal to a stable sort of the GPU's logits and to the oracle's where its
   values are separated.  Embedding rows bit-exact.
 * Free-running: the oracle's own 32-layer model fed the same token sequence
-  (OracleLlama); per step the GPU logits within twice its summation-order
-  noise floor (largest and RMS deviation), the greedy token equal wherever
+  (OracleLlama); per step the GPU logits within twice the deviation of the
+  alternative restatement's chain (cases.alternative_model; largest and RMS
+  deviation), the greedy token equal wherever
   the oracle's top-1 margin exceeds the tolerance, and the reference's
   comparison metrics (benchmarks/compare_real_logits.py:35-73) reported.
 Reference path: layer_streaming/runtime.py:137-268, vocab.py:100-300,
@@ -128,14 +130,14 @@ def test_call_teacher_forced(generation, call):
             kv[layer, 0, :, : past + seq], kv[layer, 1, :, : past + seq],
             past, cos, sin, EPS)
         assert report["ok"], (call, layer, report)
-        worst = max(worst, report["out"]["ratio_to_floor"])
+        worst = max(worst, report["out"]["worst_ratio"])
     final = c["hidden"][LAYERS - 1][-1:]
     normalized = ref.rms_norm(final, store.tensor("model.norm.weight"), EPS)
     expected = ref.lm_head_logits(normalized[0], store.tensor("lm_head.weight"))
     r = cases.compare(c["logits"], expected)
     contract = cases.topk_contract(c["values"], c["indices"], c["logits"],
                                    expected, TOP_K)
-    _say("call", call, "layers: worst out / floor {:.3f}".format(worst),
+    _say("call", call, "layers: worst per-element ratio to the bound {:.3f}".format(worst),
          "logits", r, "top-k", contract)
     assert r["ok"], r
     assert contract["ok"], contract
@@ -145,12 +147,13 @@ def test_free_running_tokens(generation):
     store = generation["store"]
     calls = generation["calls"]
     chains = {}
-    for name, linear in (("oracle", None), ("sgemm", cases.sgemm_linear)):
-        model = ref.OracleLlama(store.tensor, LAYERS, EPS, linear_fn=linear)
+    for name in ("oracle", "alternative"):
+        model = (ref.OracleLlama(store.tensor, LAYERS, EPS) if name == "oracle"
+                 else cases.alternative_model(store.tensor, LAYERS, EPS))
         chains[name] = [model.step(c["ids"], TOP_K)[0] for c in calls]
         _say("free-running chain", name, "done")
     expected = torch.stack(chains["oracle"])
-    alternative = torch.stack(chains["sgemm"])
+    alternative = torch.stack(chains["alternative"])
     floors = (alternative - expected).abs().amax(-1)
     gpu = torch.stack([c["logits"] for c in calls])
     metrics = cases.reference_metrics(expected, gpu)

@@ -1,22 +1,23 @@
 """BASELINE config 5 through the executor: a 2048-token random-ID prompt
 prefilled in pinned_staging mode (pageable arena -> pinned staging slots ->
 two 128 MiB device slots) with matrix granularity (seven units per layer)
-and the streamed vocabulary, on 4 full-width Llama-3.1-8B layers, against
-the CPU oracle.  The MFMA GEMMs, the causal prefill attention and the staged
-copies all run at their config-5 shapes; 4 layers instead of 32 keep the
-CPU oracle (about 1 TFLOP per layer here) within a test's time.
+and the streamed vocabulary, on the full 32-layer Llama-3.1-8B-shaped model,
+against the CPU oracle.  The MFMA GEMMs, the causal prefill attention and
+the staged copies all run at their config-5 shapes.
 
-* Teacher-forced, layer by layer: the oracle recomputes each layer from the
-  GPU's 2048 input hidden rows; outputs within twice the summation-order
-  noise floor, the 2048 new K / V rows of every head within the tolerance
+* Teacher-forced, on 8 of the 32 layers (the first four and layers 8, 16,
+  24 and 31; the CPU oracle spends about 1 TFLOP per layer): the oracle
+  recomputes the layer from the GPU's 2048 input hidden rows; every element
+  of the output within cases.LAYER_ULPS bf16 ulps of its rounding scale,
+  the 2048 new K / V rows of every head within the tolerance
   (oracle.cases.layer_teacher_forced).
 * Final logits of the last position (oracle final norm + fp32 LM head on the
   GPU's last hidden row) within |a - b| <= 2e-2 + 1e-2 |b|; top-10 ids and
   order as a stable sort of the GPU's logits and as the oracle's where
   separated.
-* Free-running: the oracle's own 4-layer prefill; logits within twice its
-  noise floor (max and RMS) and the greedy token equal where the margin
-  permits.
+* Free-running: the oracle's own 32-layer prefill; logits within twice the
+  deviation of the alternative restatement's chain (max and RMS) and the
+  greedy token equal where the margin permits.
 Reference path: llama31.py:128-349 (is_causal SDPA at :221-229),
 weight_store.py:209-298, runtime.py:137-268.
 """
@@ -38,7 +39,8 @@ from oracle import llama_oracle as ref
 
 pytestmark = pytest.mark.gpu
 
-LAYERS = 4
+LAYERS = 32
+CHECKED_LAYERS = (0, 1, 2, 3, 8, 16, 24, 31)
 TOKENS = 2048
 TOP_K = 10
 EPS = 1e-5
@@ -98,7 +100,7 @@ def test_embedding_rows_are_exact(prefill):
     assert torch.equal(prefill["hidden"][-1], table[prefill["ids"]])
 
 
-@pytest.mark.parametrize("layer", range(LAYERS))
+@pytest.mark.parametrize("layer", CHECKED_LAYERS)
 def test_layer_teacher_forced(prefill, layer):
     store = prefill["store"]
     cos, sin = ref.rope_cos_sin(ref.llama3_inv_freq(128), list(range(TOKENS)))
@@ -107,8 +109,8 @@ def test_layer_teacher_forced(prefill, layer):
         prefill["hidden"][layer - 1], prefill["hidden"][layer],
         ref.layer_weights(store.tensor, layer), kv[layer, 0], kv[layer, 1], 0,
         cos, sin, EPS)
-    _say("layer", layer, "out / floor {:.3f}".format(
-        report["out"]["ratio_to_floor"]), "k ratio {:.3f}".format(
+    _say("layer", layer, "out: worst per-element ratio to the bound {:.3f} (alternative {:.3f})".format(
+        report["out"]["worst_ratio"], report["out"]["alternative_worst_ratio"]), "k ratio {:.3f}".format(
         report["k"]["worst_ratio"]), "v ratio {:.3f}".format(
         report["v"]["worst_ratio"]))
     assert report["ok"], (layer, report)
@@ -130,15 +132,16 @@ def test_last_position_logits_and_topk(prefill):
 def test_free_running_prefill(prefill):
     store = prefill["store"]
     chains = {}
-    for name, linear in (("oracle", None), ("sgemm", cases.sgemm_linear)):
-        model = ref.OracleLlama(store.tensor, LAYERS, EPS, linear_fn=linear)
+    for name in ("oracle", "alternative"):
+        model = (ref.OracleLlama(store.tensor, LAYERS, EPS) if name == "oracle"
+                 else cases.alternative_model(store.tensor, LAYERS, EPS))
         chains[name] = model.step(prefill["ids"], TOP_K)[0]
         _say("free-running chain", name, "done")
     expected = chains["oracle"]
-    floor = float((chains["sgemm"] - expected).abs().max())
+    floor = float((chains["alternative"] - expected).abs().max())
     free = cases.compare(prefill["logits"], expected)
     metrics = cases.reference_metrics(expected[None], prefill["logits"][None])
-    second = cases.reference_metrics(expected[None], chains["sgemm"][None])
+    second = cases.reference_metrics(expected[None], chains["alternative"][None])
     _say("free-running", free, "noise floor", floor, metrics,
          "second CPU order", second)
     assert free["max_abs"] <= 2 * max(floor, 0.02), (free, floor)

@@ -7,10 +7,11 @@ Each configuration runs the reference's token loop (tools/run_llama31.py:
 
 1. Teacher-forced parity: the oracle recomputes every decoder layer from
    the GPU's own input hidden state and KV cache (captured through
-   ``executor.capture``).  The GPU's layer output must lie within twice the
-   reference's own summation-order noise floor on those inputs (oracle with
-   F.linear vs oracle with an fp32 sgemm; cases.within_noise_floor) and the
-   K/V it wrote within |a - b| <= 2e-2 + 1e-2 |b| (or that floor); the
+   ``executor.capture``).  Every element of the GPU's layer output must lie
+   within cases.LAYER_ULPS bf16 ulps of its rounding scale
+   (cases.within_rounding_bound) and the K/V it wrote within
+   |a - b| <= 2e-2 + 1e-2 |b| (or twice the alternative restatement's
+   deviation, cases.within_noise_floor); the
    oracle's final norm + fp32 LM head on the GPU's final hidden state must
    match the GPU's logits within the north-star tolerance
    |a - b| <= 2e-2 + 1e-2 |b|; the embedding rows are bit-exact.
@@ -64,32 +65,20 @@ def source_store():
     return store
 
 
-def _sgemm_linear(x, w):
-    return (x.float() @ w.float().t()).to(torch.bfloat16)
-
-
 @pytest.fixture(scope="module")
-def oracle_run(source_store, monkeypatch_module):
+def oracle_run(source_store):
     print("oracle greedy decode", flush=True)
     tokens, steps = ref.OracleLlama(source_store.tensor, LAYERS).generate(
         PROMPT, NEW_TOKENS, TOP_K)
-    # the same decode with another valid fp32 summation order
-    monkeypatch_module.setattr(ref, "linear", _sgemm_linear)
-    alt = ref.OracleLlama(source_store.tensor, LAYERS)
+    # the same decode through the second valid restatements (an fp32 sgemm,
+    # blocked attention)
+    alt = cases.alternative_model(source_store.tensor, LAYERS)
     floors = []
     for step in range(NEW_TOKENS):
         logits, _, _ = alt.step(PROMPT if step == 0 else [tokens[step - 1]], TOP_K)
         floors.append(float((logits - steps[step][0]).abs().max()))
-    monkeypatch_module.undo()
     print("oracle noise floor per step", floors, flush=True)
     return tokens, steps, floors
-
-
-@pytest.fixture(scope="module")
-def monkeypatch_module():
-    mp = pytest.MonkeyPatch()
-    yield mp
-    mp.undo()
 
 
 def copy_weights(src, dst):
@@ -98,7 +87,8 @@ def copy_weights(src, dst):
             dst.tensor(key).copy_(src.tensor(key))
 
 
-def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
+def build(store_mode, granularity, vocab_mode, runtime_kind, source, device,
+          slots=None):
     plan = build_llama31_8b_plan(granularity, stream_vocab=(vocab_mode == "streamed"),
                                  num_layers=LAYERS)
     store = create_weight_store(plan, store_mode)
@@ -107,7 +97,9 @@ def build(store_mode, granularity, vocab_mode, runtime_kind, source, device):
     if runtime_kind == "resident":
         runtime = ResidentTransformerRuntime(plan, store, resident, device)
     else:
-        runtime = DoubleBufferRuntime(plan, store, resident, device, profile=True)
+        runtime = DoubleBufferRuntime(plan, store, resident, device, profile=True,
+                                      slot_count=slots)
+        assert len(runtime.device_slots) == (slots or plan.slot_count)
     vocab = None
     if plan.vocab is not None:
         vocab = VocabStreamingRuntime(plan, store, runtime, profile=True)
@@ -134,13 +126,16 @@ def teacher_forced(source, executor, captured, ids, past, gpu_logits):
         v_gpu = cache.buffer[layer, 1, :, : past + seq].cpu()
         kv = {"k": k_gpu[:, :past], "v": v_gpu[:, :past]} if past else {}
         weights = ref.layer_weights(source.tensor, layer)
-        expected = ref.decoder_layer(inp, weights, kv, past, cos, sin, EPS)
+        trace = {}
+        expected = ref.decoder_layer(inp, weights, kv, past, cos, sin, EPS,
+                                     trace=trace)
         alt_kv = {"k": k_gpu[:, :past], "v": v_gpu[:, :past]} if past else {}
-        alternative = ref.decoder_layer(inp, weights, alt_kv, past, cos, sin, EPS,
-                                        linear_fn=cases.sgemm_linear)
-        r = cases.within_noise_floor(out, expected, alternative)
+        alternative = cases.alternative_layer(inp, weights, alt_kv, past, cos,
+                                              sin, EPS)
+        scale = cases.layer_rounding_scales(inp, trace, weights)["out"]
+        r = cases.within_rounding_bound(out, expected, scale)
         assert r["ok"], ("layer", layer, r)
-        worst["layer"] = max(worst["layer"], r["ratio_to_floor"])
+        worst["layer"] = max(worst["layer"], r["worst_ratio"])
         for name, gpu in (("k", k_gpu), ("v", v_gpu)):
             r = cases.compare(gpu[:, past:], kv[name][:, past:])
             f = cases.within_noise_floor(gpu[:, past:], kv[name][:, past:],
@@ -157,23 +152,29 @@ def teacher_forced(source, executor, captured, ids, past, gpu_logits):
 
 
 CONFIGS = [
-    # store, granularity, vocab, runtime
-    ("full_pinned", "matrix_group", "streamed", "double"),
-    ("pinned_staging", "matrix", "streamed", "double"),
-    ("full_pinned", "layer", "resident", "double"),
-    ("pinned_staging", "matrix_group", "resident", "double"),
-    ("full_pinned", "matrix_group", "resident", "resident"),
-    ("full_pinned", "layer", "resident", "resident"),
+    # store, granularity, vocab, runtime, device slots (None: the plan's 2)
+    ("full_pinned", "matrix_group", "streamed", "double", None),
+    ("pinned_staging", "matrix", "streamed", "double", None),
+    ("full_pinned", "layer", "resident", "double", None),
+    ("pinned_staging", "matrix_group", "resident", "double", None),
+    ("full_pinned", "matrix_group", "resident", "resident", None),
+    ("full_pinned", "layer", "resident", "resident", None),
+    # one device slot (reference runtime.py:93-106, the s1 rows of its
+    # published benchmarks); a streamed vocabulary needs two
+    ("full_pinned", "matrix_group", "resident", "double", 1),
+    ("pinned_staging", "matrix", "resident", "double", 1),
 ]
 
 
-@pytest.mark.parametrize("store_mode,granularity,vocab_mode,runtime_kind", CONFIGS)
+@pytest.mark.parametrize("store_mode,granularity,vocab_mode,runtime_kind,slots",
+                         CONFIGS)
 def test_decode_matches_oracle(gpu_device, source_store, oracle_run, store_mode,
-                               granularity, vocab_mode, runtime_kind):
-    print("config", store_mode, granularity, vocab_mode, runtime_kind, flush=True)
+                               granularity, vocab_mode, runtime_kind, slots):
+    print("config", store_mode, granularity, vocab_mode, runtime_kind, slots,
+          flush=True)
     oracle_tokens, oracle_steps, floors = oracle_run
     store, runtime, executor = build(store_mode, granularity, vocab_mode,
-                                     runtime_kind, source_store, gpu_device)
+                                     runtime_kind, source_store, gpu_device, slots)
     ids = list(PROMPT)
     past = 0
     with torch.inference_mode():

@@ -71,3 +71,19 @@ def test_oracle_streamed_lm_head_equals_full_topk():
     fv, fi = ref.topk(ref.lm_head_logits(h, w), 10)
     assert torch.equal(i, fi) and torch.equal(v, fv)
     assert logits.shape == (1000,)
+
+
+def test_streamed_vocabulary_needs_two_device_slots():
+    # reference vocab.py:63-64: the LM-head chunks alternate over two slots,
+    # so a single-slot transformer runtime is refused before any allocation
+    from types import SimpleNamespace
+
+    from layer_streaming.plan import build_llama31_8b_plan
+    from layer_streaming.vocab import VocabStreamingRuntime
+
+    plan = build_llama31_8b_plan("matrix_group", num_layers=1, stream_vocab=True)
+    one_slot = SimpleNamespace(device_slots=[torch.empty(plan.slot_elements,
+                                                         dtype=torch.bfloat16,
+                                                         device="meta")])
+    with pytest.raises(ValueError, match="two device slots"):
+        VocabStreamingRuntime(plan, store=None, transformer_runtime=one_slot)
