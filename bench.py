@@ -287,7 +287,8 @@ def resident_decode(args):
     runtime = ResidentTransformerRuntime(plan, None, resident, dev,
                                          synchronize=False).fill_random(args.seed)
     executor = Llama31DecodeExecutor(Llama31Config(), resident, top_k=10)
-    total = args.context + args.warmup + args.steps + 1
+    head_steps = 8  # config 1 with the head resident, after the timed steps
+    total = args.context + args.warmup + args.steps + head_steps + 1
     graphed = not args.no_decode_graph
     if graphed:
         total += args.warmup + args.steps + 1
@@ -317,8 +318,14 @@ def resident_decode(args):
             token = state.topk_indices.reshape(1, -1)[:, :1]
         torch.cuda.synchronize(dev)
         elapsed = time.perf_counter() - start
+        executor.instrument("lm_head", head_steps)
+        for _ in range(head_steps):
+            state = executor.finish(runtime.run(executor, executor.begin(token)))
+            token = state.topk_indices.reshape(1, -1)[:, :1]
+        torch.cuda.synchronize(dev)
     executor.check_errors()
     timed_ms = executor.kernel_times_ms(group)
+    head_us = 1000.0 * statistics.median(executor.kernel_times_ms("lm_head"))
     ms_per_step = elapsed * 1000.0 / args.steps
     graph = None
     if graphed:
@@ -356,6 +363,16 @@ def resident_decode(args):
         "mean_attended": mean_context + 1,
         "token_hbm_bytes": token_bytes(int(mean_context)),
         "last_token": int(token.reshape(-1)[0]),
+        "config1_lm_head_resident": {
+            "workload": "BASELINE config 1 with the LM head resident in HBM: "
+                        "128256 x 4096 bf16 GEMV to fp32 logits, block top-k "
+                        "and merge (3 launches) on the final hidden state of "
+                        "{} decode steps, between stream events (dispatch "
+                        "included)".format(head_steps),
+            "median_us": round(head_us, 2),
+            "bytes": VOCAB * HIDDEN * 2,
+            "gbps": round(VOCAB * HIDDEN * 2 / (head_us * 1e-6) / 1e9, 1),
+        },
     }
     if graph is not None:
         result["decode_graph"] = graph
@@ -592,6 +609,8 @@ def streamed_decode(args):
     )
 
     dev = torch.device("cuda:0")
+    torch.cuda.synchronize(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
     plan = build_llama31_8b_plan("matrix_group", stream_vocab=True)
     log("config 3: pinning a {:.1f} GB host arena".format(plan.host_arena_bytes / 1e9))
     t0 = time.perf_counter()
@@ -641,6 +660,9 @@ def streamed_decode(args):
                 lm.append(vocab.last_profile)
             else:
                 walls.append(wall)
+    peak_allocated = torch.cuda.max_memory_allocated(dev)
+    peak_reserved = torch.cuda.max_memory_reserved(dev)
+    lm_head = config1_lm_head(executor, vocab, runtime, state, dev)
     bytes_token = plan.stream_bytes_per_token + VOCAB * HIDDEN * 2 + HIDDEN * 2
     spread = percentiles(walls)
     median = spread["median"]
@@ -665,9 +687,173 @@ def streamed_decode(args):
         "lm_head_compute_event_sum_ms": statistics.median(
             p["compute_event_sum_ms"] for p in lm),
         "host_setup_s": setup_s,
+        "memory": {
+            "cuda_peak_allocated_bytes": peak_allocated,
+            "cuda_peak_allocated_gib": round(peak_allocated / 2 ** 30, 4),
+            "cuda_peak_reserved_bytes": peak_reserved,
+            "planned_weight_gpu_bytes": runtime.stats.weight_gpu_bytes,
+            "pinned_host_bytes": store.pinned_cpu_bytes + vocab.extra_pinned_cpu_bytes,
+            "reference_cuda_peak_allocated_bytes": 481369088,
+            "reference_source": "real_results/vocab_streaming_summary.json "
+                                "matrix_group_streamed_vocab (0.448 GiB, RTX 3080 Ti)",
+            "note": "peak since the config-3 objects were built: two 224 MiB "
+                    "slots, resident norms, KV cache, scratch and workspaces",
+        },
+        "config1_lm_head_streamed": lm_head,
     }
     store.close()
     del executor, vocab, runtime, resident, store
+    torch.cuda.empty_cache()
+    return result
+
+
+def config1_lm_head(executor, vocab, runtime, state, dev, repeats=5):
+    """BASELINE config 1 on the GPU: the streamed-vocabulary LM-head step
+    alone (8 chunks of 16384 rows, the last 13568, copied from the pinned
+    arena through the two device slots; one GEMV + top-k launch per chunk),
+    the figures the reference reports for its vocab profile
+    (real_results/vocab_streaming_summary.json "profiles.vocab": H2D event
+    sum, GEMV + top-k event sum, pipeline).  Each step starts with no chunk
+    in the slots (they hold the next call's first units)."""
+
+    import torch
+
+    hidden = torch.randn(1, 1, HIDDEN, device=dev).to(torch.bfloat16)
+    profiles = []
+    with torch.inference_mode():
+        vocab.profile = True
+        for step in range(1 + repeats):
+            torch.cuda.synchronize(dev)
+            runtime.discard_slots()
+            out = vocab.lm_head_topk(hidden, top_k=10)
+            torch.cuda.synchronize(dev)
+            if step:
+                profiles.append(dict(vocab.last_profile))
+        vocab.profile = False
+    del out
+
+    def med(key):
+        return round(statistics.median(p[key] for p in profiles), 4)
+
+    return {
+        "workload": "hidden [1, 4096] bf16 ~ N(0,1); LM head [128256, 4096] bf16 "
+                    "in the pinned arena; 7 x 16384 + 13568 rows; top-10; "
+                    "{} steps after 1 warm-up, medians".format(repeats),
+        "pipeline_ms": med("pipeline_ms"),
+        "h2d_event_sum_ms": med("h2d_event_sum_ms"),
+        "gemv_topk_event_sum_ms": med("compute_event_sum_ms"),
+        "h2d_gbps": med("h2d_effective_gbps"),
+        "h2d_bytes": VOCAB * HIDDEN * 2,
+        "reference_ms": {"pipeline": 44.01, "h2d_event_sum": 43.70,
+                         "gemv_topk_event_sum": 2.18,
+                         "source": "real_results/vocab_streaming_summary.json:68-78 "
+                                   "(RTX 3080 Ti, PCIe Gen4)"},
+    }
+
+
+# ------------------------------------------------- config 2 (one layer)
+
+# Algorithmic bytes of the decode kernels of one layer (weights, the input
+# vector, the norm weight and the epilogue operands they read, and what they
+# write); attention: the K / V rows read for L attended positions, q and the
+# output.
+def layer_kernel_bytes(attended):
+    return {
+        "qkv": (HIDDEN + 2 * 1024) * HIDDEN * 2 + HIDDEN * 2 * 2 + (HIDDEN + 2 * 1024) * 2,
+        "attention": 2 * attended * 8 * 128 * 2 + 32 * 128 * 2 * 2,
+        "o_proj": HIDDEN * HIDDEN * 2 + HIDDEN * 2 + 2 * HIDDEN * 2,
+        "gate_up": 2 * INTER * HIDDEN * 2 + 2 * HIDDEN * 2 + INTER * 2,
+        "down_proj": HIDDEN * INTER * 2 + INTER * 2 + 2 * HIDDEN * 2,
+    }
+
+
+def config2_layer(args, past=2048, repeats=20):
+    """BASELINE config 2 on the GPU: one Llama-3.1-8B-shaped decoder layer,
+    one decode token over a KV cache pre-filled at 2048 positions ~ N(0, 1),
+    weights resident in HBM.  The layer (the runtime's four matrix_group
+    units: q|k|v + RoPE + KV write, attention + o_proj, gate/up, down) is
+    timed with events around runtime.run, the embedding gather and the LM
+    head outside them; then each kernel group with its own events
+    (Llama31DecodeExecutor.instrument)."""
+
+    import torch
+    from layer_streaming import (
+        Llama31Config,
+        Llama31DecodeExecutor,
+        ResidentDeviceArena,
+        ResidentTransformerRuntime,
+        build_llama31_8b_plan,
+    )
+
+    dev = torch.device("cuda:0")
+    plan = build_llama31_8b_plan("matrix_group", stream_vocab=False, num_layers=1)
+    resident = ResidentDeviceArena(plan, None, dev, fill=False).fill_random(args.seed)
+    runtime = ResidentTransformerRuntime(plan, None, resident, dev,
+                                         synchronize=False).fill_random(args.seed)
+    executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=1), resident,
+                                     top_k=10)
+    executor.reserve(past + 2 * repeats + 8)
+    cache = executor.kv_cache
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+    cache.buffer[0, :, :, :past].normal_(generator=gen)
+    cache.set_length(0, past)
+    groups = ("qkv", "attention", "o_proj", "gate_up", "down_proj")
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    token = torch.tensor([[int(args.seed * 7919 % VOCAB)]], device=dev)
+    layer_ms, attended = [], []
+    log("config 2: one layer at KV {}".format(past))
+    with torch.inference_mode():
+        for phase in ("layer", "kernels"):
+            if phase == "kernels":
+                for group in groups:
+                    executor.instrument(group, repeats)
+            for step in range(repeats + (1 if phase == "layer" else 0)):
+                state = executor.begin(token)
+                start.record()
+                state = runtime.run(executor, state)
+                stop.record()
+                state = executor.finish(state)
+                token = state.topk_indices.reshape(1, -1)[:, :1]
+                torch.cuda.synchronize(dev)
+                if phase == "layer" and step:
+                    layer_ms.append(start.elapsed_time(stop))
+                    attended.append(cache.sequence_length())
+    executor.check_errors()
+    mean_attended = statistics.mean(attended)
+    kernel_bytes = layer_kernel_bytes(mean_attended)
+    kernels = {}
+    for group in groups:
+        times = executor.kernel_times_ms(group)
+        avg_us = 1000.0 * statistics.mean(times)
+        kernels[group] = {
+            "avg_us": round(avg_us, 3),
+            "bytes": int(kernel_bytes[group]),
+            "gbps": round(kernel_bytes[group] / (avg_us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(kernel_bytes[group] / (avg_us * 1e-6) / 1e9
+                                  / HBM_PEAK_GBPS, 4),
+        }
+    kernels["attention"]["timing"] = ("main + split-merge launches between "
+                                      "stream events (dispatch included)")
+    layer_bytes = (436207616 + 2 * HIDDEN * 2 + 2 * mean_attended * 8 * 128 * 2
+                   + 8 * 128 * 2 * 2)
+    median = statistics.median(layer_ms)
+    result = {
+        "workload": "BASELINE config 2: one 8B-shaped decoder layer, weights "
+                    "~ N(0,0.02) resident in HBM, KV pre-filled at {} positions "
+                    "~ N(0,1), one decode token per step; 1 warm-up + {} timed "
+                    "steps, then {} steps with per-kernel events".format(
+                        past, repeats, repeats),
+        "layer_us_median": round(1000.0 * median, 2),
+        "layer_us_p10": round(1000.0 * percentiles(layer_ms)["p10"], 2),
+        "layer_bytes": int(layer_bytes),
+        "layer_gbps": round(layer_bytes / (median * 1e-3) / 1e9, 1),
+        "layer_frac_of_peak": round(layer_bytes / (median * 1e-3) / 1e9
+                                    / HBM_PEAK_GBPS, 4),
+        "mean_attended": round(mean_attended, 1),
+        "kernels": kernels,
+    }
+    del executor, runtime, resident, cache
     torch.cuda.empty_cache()
     return result
 
@@ -987,6 +1173,8 @@ def main():
         line["decode_graph"] = resident["decode_graph"]
     if "prefill_resident" in resident:
         line["prefill_resident"] = resident["prefill_resident"]
+    line["config1_lm_head_resident"] = resident["config1_lm_head_resident"]
+    line["config2_layer"] = config2_layer(args)
     if not args.no_streamed:
         s = streamed_decode(args)
         line["streamed"] = {

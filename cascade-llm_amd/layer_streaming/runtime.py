@@ -205,6 +205,10 @@ class DoubleBufferRuntime:
         # that slot has been enqueued (VocabStreamingRuntime copies its
         # first chunks from here)
         self.release_hook = None
+        # pinned_staging: called once per call, when the call's last unit has
+        # gone to the staging workers (VocabStreamingRuntime queues the
+        # staging of its first chunks behind it)
+        self.staging_done_hook = None
         # (kind, index, ready event, store generation of the bytes)
         self._owner = [None] * self.slot_count
         self._last_free = [None] * self.slot_count  # event of the last reader
@@ -383,6 +387,8 @@ class DoubleBufferRuntime:
                 staged[next_stage] = self.store.stage_in_ring(units[next_stage],
                                                               *placed)
                 next_stage += 1
+                if next_stage == count and self.staging_done_hook is not None:
+                    self.staging_done_hook()
 
         source_wait_ms = 0.0
 

@@ -11,10 +11,15 @@ layer_streaming/vocab.py).
   one kernel launch (cascade_lm_head_topk_bf16: fp32 logits GEMV, block
   top-k and the merge with the running list).  Hand-off and slot ownership
   follow DoubleBufferRuntime: the host waits for a chunk's copy, then
-  enqueues its kernel; with a full_pinned store the first two chunks are
-  copied while the transformer's last units still run, and the next call's
-  first units while the last chunks run.  The call returns when the top-k
-  is in HBM (the reference synchronises there too, vocab.py:268-271).
+  enqueues its kernel; the first two chunks are copied while the
+  transformer's last units still run, and (full_pinned) the next call's
+  first units while the last chunks run.  With a pinned_staging store the
+  chunks pass through two pinned halves, staged on the store's staging
+  workers ahead of their copies: the first two queued behind the call's last
+  unit, chunk c + 2 as soon as chunk c's copy is enqueued (the reference
+  stages each chunk on the calling thread, vocab.py:133-147).  The call
+  returns when the top-k is in HBM (the reference synchronises there too,
+  vocab.py:268-271).
 * ``merge_topk`` is the reference's public helper (vocab.py:11-32) with a
   deterministic order on ties (value descending, index ascending).
 
@@ -110,14 +115,21 @@ class VocabStreamingRuntime:
         self._ready = [_hip.HipEvent() for _ in range(chunks)]
         self._free = [_hip.HipEvent() for _ in range(chunks)]
         self._staging_read = [None, None]  # copy that last read a pinned half
+        self._prestaged = {}  # chunk -> future of its staged pinned half
         self._start = _hip.HipEvent()
         self._rows_free = _hip.HipEvent()
         self._timers = None
         self._timed = {}
         self._workspaces = {}
-        if not self._staged:
-            # the first chunks follow the transformer's last units directly
-            runtime.release_hook = self._copy_first_chunk
+        # the first chunks follow the transformer's last units directly; a
+        # pageable store's chunks are staged on its staging workers, the
+        # first two queued behind the call's last unit
+        runtime.release_hook = self._copy_first_chunk
+        if self._staged:
+            runtime.staging_done_hook = self._prestage_first_chunks
+            add_reader = getattr(store, "add_reader", None)
+            if add_reader is not None:
+                add_reader(self)  # staging jobs read the arena
 
     @property
     def gpu_slot_bytes(self):
@@ -156,24 +168,51 @@ class VocabStreamingRuntime:
 
     # ----------------------------------------------------------- LM head
 
+    def _chunk_rows(self, chunk):
+        first, end = self.vocab.chunk_bounds(chunk)
+        return self.store.tensor(self.vocab.lm_head_key)[first:end].reshape(-1)
+
+    def _prestage(self, chunk):
+        """pinned_staging: queue the staging of ``chunk`` into its pinned half
+        on the store's staging workers, behind the copy that last read the
+        half.  Called for chunk c + 2 once chunk c's copy is enqueued, and
+        for the first two chunks behind a call's last unit."""
+
+        if chunk >= self.vocab.chunk_count or chunk in self._prestaged:
+            return
+        rows = self._chunk_rows(chunk)
+        half = chunk % 2
+        reader = self._staging_read[half]
+        target = self.head_staging_slots[half][: rows.numel()]
+        self._prestaged[chunk] = self.store.stage_into(
+            target, rows, () if reader is None else (reader,))
+
+    def _prestage_first_chunks(self):
+        for chunk in range(min(2, self.vocab.chunk_count)):
+            self._prestage(chunk)
+
     def _chunk_source(self, chunk):
         """Pinned host rows of one chunk (staged first for pinned_staging)."""
 
-        first, end = self.vocab.chunk_bounds(chunk)
-        rows = self.store.tensor(self.vocab.lm_head_key)[first:end].reshape(-1)
         if not self._staged:
+            rows = self._chunk_rows(chunk)
             if not rows.is_pinned():
                 raise RuntimeError("a full_pinned store must hold the LM head "
                                    "in page-locked memory")
             return rows
-        half = chunk % 2
-        reader = self._staging_read[half]
-        if reader is not None:
-            reader.synchronize()  # the copy that read this half is done
-        target = self.head_staging_slots[half][: rows.numel()]
-        self.store.copy_to_pinned(target, rows)
-        self._staging_read[half] = self._ready[chunk]
-        return target
+        self._prestage(chunk)  # no-op when already queued
+        return self._prestaged.pop(chunk).result()
+
+    def quiesce(self):
+        """Wait for the staging jobs still reading the store's arena (called
+        by the store before its bytes change)."""
+
+        for future in list(self._prestaged.values()):
+            try:
+                future.result()
+            except Exception:  # the call that queued it already raised
+                pass
+        self._prestaged = {}
 
     def _copy_chunk(self, chunk):
         first, end = self.vocab.chunk_bounds(chunk)
@@ -186,6 +225,11 @@ class VocabStreamingRuntime:
         self.transformer_runtime.slot_copy(chunk % 2, "chunk", chunk,
                                            self._chunk_source(chunk), nbytes,
                                            self._ready[chunk], pair)
+        if self._staged:
+            # this copy reads the chunk's pinned half; the chunk two ahead
+            # is staged there once it is done
+            self._staging_read[chunk % 2] = self._ready[chunk]
+            self._prestage(chunk + 2)
 
     def _copy_first_chunk(self, slot):
         """Release hook of the transformer runtime: its last unit in
@@ -260,29 +304,37 @@ class VocabStreamingRuntime:
         self._start.wait(self.compute_stream)
         if timers:
             timers["pipeline"][0].record(self.coordinator)
-        ready = {c: self._chunk_ready(c) for c in range(min(2, chunks))}
-        for chunk in range(chunks):
-            first, end = self.vocab.chunk_bounds(chunk)
-            slot = chunk % 2
-            ready.pop(chunk).synchronize()  # host hand-off: the chunk is in HBM
-            weight = self.device_slots[slot][: (end - first) * width].view(-1, width)
-            with torch.cuda.stream(self.compute_stream):
-                if timers:
-                    timers["compute_start"][chunk].record(self.compute_stream)
-                _hip.lm_head_topk(
-                    weight, hidden, top_k, first, chunk == 0, workspace, values,
-                    indices,
-                    logits_out=None if flat_logits is None else flat_logits[first:end],
-                    stream=self.compute_stream,
-                )
-                if timers:
-                    timers["compute_end"][chunk].record(self.compute_stream)
-                self._free[chunk].record(self.compute_stream)
-            runtime.slot_released(slot, self._free[chunk])
-            if chunk + 2 < chunks:
-                ready[chunk + 2] = self._chunk_ready(chunk + 2)
-            else:
-                runtime.prefetch_next_call(slot)
+        try:
+            ready = {c: self._chunk_ready(c) for c in range(min(2, chunks))}
+            for chunk in range(chunks):
+                first, end = self.vocab.chunk_bounds(chunk)
+                slot = chunk % 2
+                ready.pop(chunk).synchronize()  # host hand-off: the chunk is in HBM
+                weight = self.device_slots[slot][: (end - first) * width].view(-1, width)
+                with torch.cuda.stream(self.compute_stream):
+                    if timers:
+                        timers["compute_start"][chunk].record(self.compute_stream)
+                    _hip.lm_head_topk(
+                        weight, hidden, top_k, first, chunk == 0, workspace, values,
+                        indices,
+                        logits_out=None if flat_logits is None else flat_logits[first:end],
+                        stream=self.compute_stream,
+                    )
+                    if timers:
+                        timers["compute_end"][chunk].record(self.compute_stream)
+                    self._free[chunk].record(self.compute_stream)
+                runtime.slot_released(slot, self._free[chunk])
+                if chunk + 2 < chunks:
+                    ready[chunk + 2] = self._chunk_ready(chunk + 2)
+                else:
+                    runtime.prefetch_next_call(slot)
+        except BaseException:
+            # staging jobs left in flight must not land in a half that a
+            # later call stages again: wait for them, and for the copies
+            self.quiesce()
+            self.copy_stream.synchronize()
+            self._staging_read = [None, None]
+            raise
 
         last = self._free[chunks - 1]
         last.wait(self.coordinator)

@@ -341,6 +341,14 @@ class _Stager:
         self._jobs.put((result, source, buffer_index, byte_start, tuple(waits)))
         return result
 
+    def submit_into(self, target, source, waits):
+        """A job that copies ``source`` into the pinned ``target`` (a buffer
+        the caller owns) once ``waits`` are done."""
+
+        result = Future()
+        self._jobs.put((result, source, target, None, tuple(waits)))
+        return result
+
     def _serve(self):
         while True:
             job = self._jobs.get()
@@ -359,12 +367,16 @@ class _Stager:
         started = time.perf_counter()
         for event in waits:
             event.synchronize()  # the copies that read these bytes are done
-        buffer = self.buffers[buffer_index]
-        first = byte_start // buffer.element_size()
-        target = buffer[first:first + source.numel()]
+        if byte_start is None:  # submit_into: buffer_index is the target view
+            target = buffer_index
+        else:
+            buffer = self.buffers[buffer_index]
+            first = byte_start // buffer.element_size()
+            target = buffer[first:first + source.numel()]
         self.pool.copy(target, source)
-        with self._lock:
-            self._durations_ms.append((time.perf_counter() - started) * 1000.0)
+        if byte_start is not None:  # the unit staging the profile reports
+            with self._lock:
+                self._durations_ms.append((time.perf_counter() - started) * 1000.0)
         return target
 
     def stats(self, reset=False):
@@ -441,6 +453,14 @@ class PinnedStagingWeightStore(BaseWeightStore):
 
         return self._running_stager().submit(self.unit_source(unit), slot_index,
                                              start, waits)
+
+    def stage_into(self, target, source, waits=()):
+        """Copy ``source`` into the caller's pinned ``target`` on the staging
+        workers once ``waits`` (the copies that last read ``target``) are
+        done; returns a future of ``target``.  The streamed LM head stages
+        its chunks ahead this way (vocab.py)."""
+
+        return self._running_stager().submit_into(target, source, waits)
 
     def copy_to_pinned(self, target, source):
         """``target.copy_(source)`` on the staging copy pool (the streamed

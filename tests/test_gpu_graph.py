@@ -105,7 +105,8 @@ def test_qkv_at_clamps_a_length_past_capacity(gpu_device):
 
 
 @pytest.mark.parametrize("length,capacity", [(1, 1), (7, 12), (33, 40),
-                                             (2101, 2200), (4100, 4100)])
+                                             (2101, 2200), (4100, 4100),
+                                             (32769, 34800)])
 def test_attention_at_equals_attention(gpu_device, length, capacity):
     assert _span(length) == _span(capacity)
     dev = torch.device(gpu_device)
