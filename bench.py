@@ -553,15 +553,43 @@ def prefill_sweep(args):
 # ------------------------------------------------- config 3 (H2D streamed)
 
 
+def copy_rates(samples, stream, slot, reps=5, rounds=2):
+    """H2D GB/s of each (nbytes -> pinned source) copied alone into ``slot``
+    on ``stream``: per round 2 warm-up + ``reps`` timed copies per size, each
+    bracketed by events, median per round; the best round per size (a
+    transient stall of the host link in one round is not the link's rate)."""
+
+    from layer_streaming import _hip
+
+    rates = {}
+    for _ in range(rounds):
+        for nbytes, source in samples.items():
+            pairs = []
+            for rep in range(2 + reps):
+                a = _hip.HipEvent(enable_timing=True)
+                b = _hip.HipEvent(enable_timing=True)
+                a.record(stream)
+                _hip.memcpy_h2d_async(slot, source, nbytes, stream)
+                b.record(stream)
+                if rep >= 2:
+                    pairs.append((a, b))
+            stream.synchronize()
+            ms = statistics.median(x.elapsed_time(y) for x, y in pairs)
+            rates[nbytes] = max(rates.get(nbytes, 0.0), nbytes / 1e9 / (ms / 1e3))
+    return rates
+
+
+def size_label(n):
+    return str(n >> 20) + " MiB" if n % (1 << 20) == 0 else str(n)
+
+
 def h2d_ideal(plan, store, runtime, reps=5):
     """Copy time of one streamed token's transfers when each runs alone:
     every distinct transfer size is copied from the token's own arena rows
-    into a device slot on the copy stream (2 warm-up + ``reps`` timed, each
-    bracketed by events), and the token's transfers are priced at their
-    size's median rate."""
+    into a device slot on the copy stream (copy_rates), and the token's
+    transfers are priced at their size's rate."""
 
     import torch
-    from layer_streaming import _hip
 
     vocab = plan.vocab
     transfers = [(u.nbytes, store.unit_source(u)) for u in plan.units]
@@ -573,27 +601,11 @@ def h2d_ideal(plan, store, runtime, reps=5):
     samples = {}
     for nbytes, source in transfers:
         samples.setdefault(nbytes, source)
-    stream = runtime.copy_stream
-    slot = runtime.device_slots[0]
-    rates = {}
-    for nbytes, source in samples.items():
-        pairs = []
-        for rep in range(2 + reps):
-            a = _hip.HipEvent(enable_timing=True)
-            b = _hip.HipEvent(enable_timing=True)
-            a.record(stream)
-            _hip.memcpy_h2d_async(slot, source, nbytes, stream)
-            b.record(stream)
-            if rep >= 2:
-                pairs.append((a, b))
-        stream.synchronize()
-        ms = statistics.median(x.elapsed_time(y) for x, y in pairs)
-        rates[nbytes] = nbytes / 1e9 / (ms / 1e3)
+    rates = copy_rates(samples, runtime.copy_stream, runtime.device_slots[0], reps)
     ideal_ms = sum(n / 1e9 / rates[n] * 1e3 for n, _ in transfers)
     runtime.discard_slots()  # slot 0 now holds a probe copy
     torch.cuda.synchronize()
-    return ideal_ms, {str(n >> 20) + " MiB" if n % (1 << 20) == 0 else str(n): round(r, 2)
-                      for n, r in sorted(rates.items())}
+    return ideal_ms, {size_label(n): round(r, 2) for n, r in sorted(rates.items())}
 
 
 def streamed_decode(args):
@@ -951,6 +963,18 @@ def prefill_streamed(args):
     attn_tflops = attn_flops / (statistics.mean(attn) * 1e-3) / 1e12
     bytes_prefill = plan.stream_bytes_per_token + VOCAB * HIDDEN * 2
     median = statistics.median(walls)
+    # the H2D roofline of this path: the prefill's transfers (224 matrix
+    # units, 8 LM-head chunks) priced at the rate each size reaches alone,
+    # copied from a pinned staging slot
+    sizes = [u.nbytes for u in plan.units] + [
+        (e - f) * HIDDEN * 2 for f, e in
+        (plan.vocab.chunk_bounds(c) for c in range(plan.vocab.chunk_count))]
+    pinned = store.staging_slots[0].view(-1)
+    rates = copy_rates({n: pinned for n in sorted(set(sizes))},
+                       runtime.copy_stream, runtime.device_slots[0])
+    runtime.discard_slots()
+    torch.cuda.synchronize(dev)
+    ideal_ms = sum(n / 1e9 / rates[n] * 1e3 for n in sizes)
     result = {
         "workload": "BASELINE config 5: {}-token random-ID prompt, pinned_staging "
                     "(pageable arena + pinned staging slots), matrix granularity, "
@@ -963,6 +987,10 @@ def prefill_streamed(args):
         "prompt_tokens_per_s": round(tokens / (median / 1e3), 1),
         "h2d_bytes": bytes_prefill,
         "pcie_inclusive_gbps": round(bytes_prefill / 1e9 / (median / 1e3), 2),
+        "isolated_copy_ms": round(ideal_ms, 2),
+        "frac_of_isolated_copy_time": round(ideal_ms / median, 4),
+        "isolated_copy_gbps_by_size": {size_label(n): round(r, 2)
+                                       for n, r in sorted(rates.items())},
         "transformer_h2d_gbps_median": round(statistics.median(
             p["h2d_effective_gbps"] for p in profiles), 2),
         "transformer_compute_event_sum_ms": round(statistics.median(
