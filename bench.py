@@ -921,6 +921,8 @@ def prefill_streamed(args):
               "prefill_attention": LAYERS}
     repeats = args.prefill_repeats
     profiled = None
+    phases = []  # host ms of begin (embedding), run (the units), finish (LM head)
+    head_profile = {}
     with torch.inference_mode():
         # warm-up, timed prefills without timing events, then one prefill
         # with copy / unit events and every GEMM and attention launch timed
@@ -933,9 +935,16 @@ def prefill_streamed(args):
                     executor.instrument(name, count)
             torch.cuda.synchronize(dev)
             t0 = time.perf_counter()
-            state = executor.finish(runtime.run(executor, executor.begin(prompt)))
+            state = executor.begin(prompt)
+            t1 = time.perf_counter()
+            state = runtime.run(executor, state)
+            t2 = time.perf_counter()
+            state = executor.finish(state)
             torch.cuda.synchronize(dev)
-            wall = (time.perf_counter() - t0) * 1000.0
+            t3 = time.perf_counter()
+            wall = (t3 - t0) * 1000.0
+            if rep and not last:
+                phases.append(((t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3))
             log("config 5: prefill {} {:.1f} ms{}".format(
                 rep, wall, " (profiled)" if last else ""))
             if rep == 0:
@@ -943,6 +952,7 @@ def prefill_streamed(args):
             if last:
                 profiled = wall
                 profiles.append(runtime.last_profile)
+                head_profile = dict(vocab.last_profile)
             else:
                 walls.append(wall)
     times = {name: executor.kernel_times_ms(name) for name in groups}
@@ -997,6 +1007,16 @@ def prefill_streamed(args):
             p["compute_event_sum_ms"] for p in profiles), 2),
         "staging_copy_sum_ms": round(statistics.median(
             p.get("staging_event_sum_ms", 0.0) for p in profiles), 1),
+        "host_phase_ms_median": {
+            name: round(statistics.median(ph[i] for ph in phases), 2)
+            for i, name in enumerate(("begin_embedding", "run_units",
+                                      "finish_lm_head"))},
+        "lm_head_profiled": {k: round(head_profile[k], 3) for k in
+                             ("pipeline_ms", "h2d_event_sum_ms",
+                              "h2d_effective_gbps", "compute_event_sum_ms")
+                             if k in head_profile},
+        "transformer_gpu_pipeline_ms": round(statistics.median(
+            p["gpu_pipeline_ms"] for p in profiles), 2),
         "gemm": gemms,
         "gemm_sum_ms": round(total_ms, 2),
         "gemm_tflops": round(2.0 * tokens * 218103808 * LAYERS / (total_ms * 1e-3)

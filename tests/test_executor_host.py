@@ -463,6 +463,23 @@ def test_begin_rejects_multi_token_after_prefill(monkeypatch, weights, exact_ora
                               HostResident(plan, weights))
 
 
+def test_layer_count_must_match_the_plan(monkeypatch, weights, exact_oracle):
+    # The reference accepts only the 32-layer config (llama31.py:93-109).
+    # Here the config must match the plan the resident arena was built from:
+    # a full 32-layer plan takes only the 32-layer config, as in the
+    # reference; a truncated plan (the tests' full-width 2-layer models, the
+    # CLI's --layers) takes only its own layer count.
+    full = build_llama31_8b_plan("matrix_group")
+    monkeypatch.setattr(_hip, "load", lambda: None)
+    for layers in (31, 33, 2):
+        with pytest.raises(ValueError, match="num_hidden_layers"):
+            Llama31DecodeExecutor(Llama31Config(num_hidden_layers=layers),
+                                  HostResident(full, weights))
+    small = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    with pytest.raises(ValueError, match="num_hidden_layers"):
+        Llama31DecodeExecutor(Llama31Config(), HostResident(small, weights))
+
+
 def test_begin_rejects_token_ids_outside_the_vocabulary(monkeypatch, weights,
                                                         exact_oracle):
     # F.embedding raises on such an id (the reference's resident table,
