@@ -886,6 +886,25 @@ PREFILL_GEMMS = (
 )
 
 
+def unit_copy_gaps(runtime, plan):
+    """Idle time of the copy engine between consecutive unit copies of the
+    profiled call (copy i + 1's start event minus copy i's end event), in
+    total and by the operation of the unit whose copy waited."""
+
+    timing = runtime._timing_events()
+    units = plan.units
+    by_op = {}
+    gaps = []
+    for i in range(len(units) - 1):
+        gap = timing["copy_end"][i].elapsed_time(timing["copy_start"][i + 1])
+        gaps.append(gap)
+        op = units[i + 1].operation
+        by_op[op] = by_op.get(op, 0.0) + gap
+    return {"sum_ms": round(sum(gaps), 3),
+            "max_ms": round(max(gaps), 3),
+            "by_next_unit_ms": {k: round(v, 3) for k, v in sorted(by_op.items())}}
+
+
 def prefill_streamed(args):
     """one 2048-token prefill in pinned_staging mode."""
 
@@ -923,6 +942,7 @@ def prefill_streamed(args):
     profiled = None
     phases = []  # host ms of begin (embedding), run (the units), finish (LM head)
     head_profile = {}
+    copy_gaps = {}
     with torch.inference_mode():
         # warm-up, timed prefills without timing events, then one prefill
         # with copy / unit events and every GEMM and attention launch timed
@@ -953,6 +973,7 @@ def prefill_streamed(args):
                 profiled = wall
                 profiles.append(runtime.last_profile)
                 head_profile = dict(vocab.last_profile)
+                copy_gaps = unit_copy_gaps(runtime, plan)
             else:
                 walls.append(wall)
     times = {name: executor.kernel_times_ms(name) for name in groups}
@@ -1017,6 +1038,7 @@ def prefill_streamed(args):
                              if k in head_profile},
         "transformer_gpu_pipeline_ms": round(statistics.median(
             p["gpu_pipeline_ms"] for p in profiles), 2),
+        "unit_copy_gaps": copy_gaps,
         "gemm": gemms,
         "gemm_sum_ms": round(total_ms, 2),
         "gemm_tflops": round(2.0 * tokens * 218103808 * LAYERS / (total_ms * 1e-3)

@@ -269,3 +269,43 @@ def test_out_of_vocabulary_ids_raise(gpu_device, source_store):
         state = executor.finish(runtime.run(executor, executor.begin(good)))
         executor.check_errors()
     store.close()
+
+
+def test_refilled_store_is_copied_again(gpu_device):
+    # The runtime copies the next call's first units ahead (full_pinned).
+    # Refilling the store between calls, without discard_slots(), must make
+    # the next call compute on the new bytes: its tokens and logits equal
+    # those of a runtime built fresh on the refilled store.
+    def run(store, runtime_plan, runtime=None):
+        resident = ResidentDeviceArena(runtime_plan, store, gpu_device)
+        if runtime is None:
+            runtime = DoubleBufferRuntime(runtime_plan, store, resident, gpu_device)
+        else:
+            runtime.resident = resident
+        executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
+                                         resident, top_k=TOP_K,
+                                         return_full_logits=True)
+        with torch.inference_mode():
+            state = executor.finish(runtime.run(executor, executor.begin(
+                torch.tensor([PROMPT], device=gpu_device))))
+            torch.cuda.synchronize(gpu_device)
+        return runtime, state.logits.reshape(-1, VOCAB_SIZE)[-1].cpu()
+
+    VOCAB_SIZE = 128256
+    plan = build_llama31_8b_plan("matrix_group", stream_vocab=False,
+                                 num_layers=LAYERS)
+    store = create_weight_store(plan, "full_pinned")
+    store.fill_random(seed=5, device=gpu_device)
+    runtime, first = run(store, plan)
+    assert runtime.slot_holding(0, "unit", 0) is not None  # copied ahead
+    print("refilling the store between calls", flush=True)
+    store.fill_random(seed=6, device=gpu_device)
+    assert runtime.slot_holding(0, "unit", 0) is None
+    _, second = run(store, plan, runtime)
+    fresh_store = create_weight_store(plan, "full_pinned")
+    fresh_store.fill_random(seed=6, device=gpu_device)
+    _, expected = run(fresh_store, plan)
+    assert not torch.equal(first, second)
+    assert torch.equal(second, expected)
+    store.close()
+    fresh_store.close()
