@@ -52,20 +52,55 @@ __device__ __forceinline__ float exp2_fast(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// Split plan.  The len positions of a KV head form ceil(len / 32) blocks of
+// 32 rows; split_count(len) = min(kAttnMaxSplits, blocks) splits take
+// consecutive runs of them, as evenly as whole blocks allow: each split gets
+// blocks / used blocks and the last blocks % used splits one more.  The
+// partial last block thus lands in a longer split: at len = 32769 (1025
+// blocks) 63 splits hold 16 blocks and the last 17, the 17th a single row,
+// so no wave of the 4 in a workgroup runs more than 4 full blocks.  (A
+// fixed span of ceil(blocks / 64) blocks would give 61 splits of 17, whose
+// first waves run a fifth full block while the other three idle.)
+__host__ __device__ constexpr int split_count(int len) {
+  return (len + kAttnBlock - 1) / kAttnBlock < kAttnMaxSplits
+             ? (len + kAttnBlock - 1) / kAttnBlock
+             : kAttnMaxSplits;
+}
+
+struct SplitRows {
+  int used;   // split_count(len)
+  int begin;  // rows [begin, end) of split `split` (split < used)
+  int end;
+};
+
+__device__ __forceinline__ SplitRows split_rows(int len, int split) {
+  const int blocks = (len + kAttnBlock - 1) / kAttnBlock;
+  const int used = split_count(len);
+  const int per = blocks / used;
+  const int shorter = used - blocks % used;  // splits of `per` blocks
+  const int first = split * per + max(0, split - shorter);
+  const int count = per + (split >= shorter ? 1 : 0);
+  SplitRows r;
+  r.used = used;
+  r.begin = first * kAttnBlock;
+  r.end = min((first + count) * kAttnBlock, len);
+  return r;
+}
+
 struct AttnArgs {
   const uint16_t *q;
   const uint16_t *k;
   const uint16_t *v;
   int64_t head_stride;
   int32_t len;
-  int32_t span;     // positions per split (a multiple of kAttnBlock)
-  int32_t nsplits;
+  int32_t nsplits;  // grid width and partial layout (split_count(len))
   float scale_log2;  // scale * log2(e)
   uint16_t *out;
   float *part_ml;      // [kv_heads][nsplits][G][2]  (max in log2 units, sum)
   float *part_acc;     // [kv_heads][nsplits][G][D]
   // AT kernels: the length is this device word, clamped to [1, len] (len
-  // then holds the cache capacity, which sets span and nsplits)
+  // then holds the cache capacity, which sets nsplits; the splits follow
+  // the word's length, and those past its plan write empty partials)
   const int64_t *len_word;
 };
 
@@ -89,15 +124,37 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
   const int wave = tid / kWave;
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
+  // AT: the length word is loaded first (the split's rows depend on it)
+  int64_t len_word = a.len;
+  if constexpr (AT) len_word = *a.len_word;
   // q operand of dim chunk c: B[8 g4 + j][c16] = q[head c16][32 c + 8 g4 + j]
-  // (loaded first: under AT its latency overlaps the length's)
+  // (loaded before the length is used, so the two latencies overlap)
   u32x4 qop[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     qop[c] = c16 < G ? *reinterpret_cast<const u32x4 *>(
                            a.q + (g * G + c16) * D + 32 * c + 8 * g4)
                      : u32x4{0u, 0u, 0u, 0u};
-  const int begin = split * a.span;
+  const int len = static_cast<int>(
+      min(max(len_word, int64_t{1}), static_cast<int64_t>(a.len)));
+  const SplitRows rows = split_rows(len, split);
+  if constexpr (AT) {
+    if (split >= rows.used) {
+      // A split past the current length's plan (the grid is sized for the
+      // capacity): an empty partial, m = -inf and l = 0, which the merge
+      // weighs 0.  Split 0 is always used, so nsplits > 1 here.
+      const int64_t slot0 = (static_cast<int64_t>(g) * a.nsplits + split) * G;
+      for (int i = tid; i < G * D; i += WAVES * kWave)
+        a.part_acc[slot0 * D + i] = 0.0f;
+      if (tid < G) {
+        a.part_ml[(slot0 + tid) * 2] = -INFINITY;
+        a.part_ml[(slot0 + tid) * 2 + 1] = 0.0f;
+      }
+      return;
+    }
+  }
+  const int begin = rows.begin;
+  const int end = rows.end;
   const uint16_t *kb = a.k + g * a.head_stride;
   const uint16_t *vb = a.v + g * a.head_stride;
   const int krow = 8 * (c16 >> 2) + (c16 & 3);  // + 4 hf
@@ -119,45 +176,6 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
       vt[j] = kv_load<NT>(vb + static_cast<int64_t>(row) * D + 8 * c16);
     }
   };
-
-  // AT: the wave's first block is loaded before the length is known, its
-  // rows clamped to the capacity (allocated rows, whatever they hold); rows
-  // at or past the length are masked once it is known -- scores -inf as in
-  // any block, and V zeroed, since an unwritten row may hold NaN and 0 NaN
-  // is NaN in the P V product.
-  // The empty asm consumes the block so the compiler cannot sink its loads
-  // below the length test; the length's scalar load is issued first, and
-  // both latencies overlap.
-  int64_t len_word = a.len;
-  if constexpr (AT) len_word = *a.len_word;
-  u32x4 kt0[2][4], vt0[8];
-  if constexpr (AT) {
-    load_block(begin + wave * kAttnBlock, min(begin + a.span, a.len) - 1, kt0,
-               vt0);
-    asm volatile("" ::"v"(kt0[0][0]), "v"(kt0[0][1]), "v"(kt0[0][2]),
-                 "v"(kt0[0][3]), "v"(kt0[1][0]), "v"(kt0[1][1]),
-                 "v"(kt0[1][2]), "v"(kt0[1][3]));
-    asm volatile("" ::"v"(vt0[0]), "v"(vt0[1]), "v"(vt0[2]), "v"(vt0[3]),
-                 "v"(vt0[4]), "v"(vt0[5]), "v"(vt0[6]), "v"(vt0[7]));
-  }
-  const int len = static_cast<int>(
-      min(max(len_word, int64_t{1}), static_cast<int64_t>(a.len)));
-  const int end = min(begin + a.span, len);
-  if constexpr (AT) {
-    if (begin >= len) {
-      // A split past the current length (the grid is sized for the
-      // capacity): an empty partial, m = -inf and l = 0, which the merge
-      // weighs 0.  Split 0 always holds position 0, so nsplits > 1 here.
-      const int64_t slot0 = (static_cast<int64_t>(g) * a.nsplits + split) * G;
-      for (int i = tid; i < G * D; i += WAVES * kWave)
-        a.part_acc[slot0 * D + i] = 0.0f;
-      if (tid < G) {
-        a.part_ml[(slot0 + tid) * 2] = -INFINITY;
-        a.part_ml[(slot0 + tid) * 2 + 1] = 0.0f;
-      }
-      return;
-    }
-  }
 
   __shared__ float s_ml[WAVES][G][2];
   __shared__ float s_acc[WAVES][G][D];
@@ -210,17 +228,7 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
       o[e] = mfma_16x16x32_bf16(v_operand(vt, e), pop, o[e]);
   };
 
-  int r0 = begin + wave * kAttnBlock;
-  if constexpr (AT) {
-    if (r0 < end) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (r0 + 8 * g4 + j >= end) vt0[j] = u32x4{0u, 0u, 0u, 0u};
-      block_step(r0, kt0, vt0);
-    }
-    r0 += kPassRows;
-  }
-  for (; r0 < end; r0 += kPassRows) {
+  for (int r0 = begin + wave * kAttnBlock; r0 < end; r0 += kPassRows) {
     u32x4 kt[2][4];
     u32x4 vt[8];
     load_block(r0, last, kt, vt);
@@ -655,25 +663,6 @@ __attribute__((amdgpu_waves_per_eu(HW / 2))) void prefill_attention_kernel(
   if (half == 1) write_out();
 }
 
-struct AttnShape {
-  int64_t span;
-  int64_t nsplits;
-};
-
-// Split policy: at most kAttnMaxSplits splits per KV head (512 workgroups
-// for 8 heads at long contexts), spans a multiple of the 32-row block.  At
-// context 32769 this gives 61 spans of 544 rows (an MI355X sweep of spans
-// 544 .. 1024 rows and 4 / 8 waves per workgroup put this within 0.5 us of
-// the best).
-static AttnShape attention_shape(int64_t len) {
-  AttnShape s;
-  int64_t span = (len + kAttnMaxSplits - 1) / kAttnMaxSplits;
-  span = (span + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
-  s.span = span;
-  s.nsplits = (len + span - 1) / span;
-  return s;
-}
-
 constexpr size_t attention_workspace(int64_t nsplits, int64_t n_kv_heads) {
   const size_t per = static_cast<size_t>(n_kv_heads) * nsplits * kAttnG;
   return kAttnHeaderBytes + per * 2 * sizeof(float) +
@@ -713,20 +702,19 @@ static int decode_attention_args(const void *q, const void *k_cache,
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) ||
       !aligned16(out) || !aligned16(workspace) || (kv_head_stride & 7))
     return CASCADE_EALIGN;
-  const AttnShape shape = attention_shape(len);
-  if (workspace_bytes < attention_workspace(shape.nsplits, n_kv_heads))
+  const int nsplits = split_count(static_cast<int>(len));
+  if (workspace_bytes < attention_workspace(nsplits, n_kv_heads))
     return CASCADE_EWORKSPACE;
   a.q = static_cast<const uint16_t *>(q);
   a.k = static_cast<const uint16_t *>(k_cache);
   a.v = static_cast<const uint16_t *>(v_cache);
   a.head_stride = kv_head_stride;
   a.len = static_cast<int32_t>(len);
-  a.span = static_cast<int32_t>(shape.span);
-  a.nsplits = static_cast<int32_t>(shape.nsplits);
+  a.nsplits = nsplits;
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<uint16_t *>(out);
   char *ws = static_cast<char *>(workspace);
-  const size_t per = static_cast<size_t>(n_kv_heads) * shape.nsplits * kAttnG;
+  const size_t per = static_cast<size_t>(n_kv_heads) * nsplits * kAttnG;
   a.part_ml = reinterpret_cast<float *>(ws + kAttnHeaderBytes);
   a.part_acc = reinterpret_cast<float *>(ws + kAttnHeaderBytes +
                                          per * 2 * sizeof(float));

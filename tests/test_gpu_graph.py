@@ -2,9 +2,10 @@
 
 Kernel level: cascade_qkv_rope_at_bf16 and cascade_decode_attention_at_bf16
 must give, bit for bit, what the host-position entry points give at the same
-position / length (the attention's split plan follows the capacity, so the
-cases pick capacities with the same split span; one case has splits past the
-length, which must contribute exactly nothing); cascade_decode_step_begin_bf16
+position / length (the attention's grid follows the capacity and its splits
+the length word, so cases whose capacity has more splits than the length
+check that the splits past the length's plan contribute exactly nothing);
+cascade_decode_step_begin_bf16
 must gather, record and advance as declared, and refuse a full history.
 
 Model level: a 2-layer, full-width Llama-3.1-8B-shaped resident model decodes
@@ -37,12 +38,6 @@ TOP_K = 10
 
 def _say(*parts):
     print(*parts, flush=True)
-
-
-def _span(length):
-    # the split rule of attention.hip (at most 64 splits, spans of 32 rows)
-    span = -(-length // 64)
-    return -(-span // 32) * 32
 
 
 # ----------------------------------------------------------------- kernels
@@ -104,11 +99,13 @@ def test_qkv_at_clamps_a_length_past_capacity(gpu_device):
     assert torch.equal(caches[0].cpu(), caches[1].cpu())
 
 
+# (splits of the length's plan, of the capacity's): (1, 1), (1, 1), (2, 2),
+# (2, 64), (64, 64) with rows moving between splits as the length grows,
+# (64, 64), (64, 64)
 @pytest.mark.parametrize("length,capacity", [(1, 1), (7, 12), (33, 40),
-                                             (2101, 2200), (4100, 4100),
-                                             (32769, 34800)])
+                                             (40, 2200), (2101, 2200),
+                                             (4100, 4100), (32769, 34800)])
 def test_attention_at_equals_attention(gpu_device, length, capacity):
-    assert _span(length) == _span(capacity)
     dev = torch.device(gpu_device)
     gen = torch.Generator(device=dev).manual_seed(length)
     stride = capacity * 128
@@ -182,10 +179,11 @@ def model(gpu_device):
     return resident, runtime
 
 
-@pytest.mark.parametrize("past,max_new", [(6, 6), (2100, 100)])
+@pytest.mark.parametrize("past,max_new", [(6, 6), (40, 2000), (2100, 100)])
 def test_decode_graph_replays_equal_eager_steps(gpu_device, model, past, max_new):
-    # (2100, 100): the capacity's split plan has two splits past the first
-    # lengths, with the same span as the eager plan
+    # (40, 2000): the capacity's grid has 64 splits, the lengths' plans 2;
+    # (2100, 100): 64 splits in both, rows moving between them as the
+    # length grows
     dev = torch.device(gpu_device)
     resident, runtime = model
     steps = 6

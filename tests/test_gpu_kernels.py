@@ -135,7 +135,8 @@ def test_qkv_rope_split_matrices_equal_fused(gpu_device):
 
 @pytest.mark.parametrize("length,q_scale", [
     (1, 1), (2, 1), (17, 1), (32, 1), (33, 1), (64, 1), (65, 1), (129, 1),
-    (1000, 1), (2048, 1), (2049, 1), (8192, 1), (8193, 1), (32769, 1),
+    (1000, 1), (2048, 1), (2049, 1), (4100, 1), (8192, 1), (8193, 1),
+    (32769, 1), (34000, 1),
     # sharp softmax: the running maximum moves between blocks and splits
     (4097, 8), (32769, 8)])
 def test_decode_attention_matches_oracle(gpu_device, length, q_scale):
