@@ -150,10 +150,12 @@ int cascade_decode_attention_bf16(const void *q, const void *k_cache,
                                   float scale, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream);
 /* The same over positions [0, L) with L = *length (device int64, clamped to
- * [1, capacity]).  The split plan, and with it the launch shape, follows
- * capacity, so one captured launch serves every L <= capacity; splits past
- * L contribute nothing.  kv_head_stride >= capacity * head_dim; workspace as
- * above (cascade_decode_attention_workspace_bytes(capacity, ...)).         */
+ * [1, capacity]).  The launch shape follows capacity, so one captured
+ * launch serves every L <= capacity; the workgroups split [0, L) as the
+ * host-length form does (the result is bit-identical to it), and splits
+ * past L's plan contribute nothing.  kv_head_stride >= capacity *
+ * head_dim; workspace as above
+ * (cascade_decode_attention_workspace_bytes(capacity, ...)).               */
 int cascade_decode_attention_at_bf16(const void *q, const void *k_cache,
                                      const void *v_cache,
                                      int64_t kv_head_stride,
