@@ -20,9 +20,9 @@ namespace cascade {
 
 constexpr int kTopkThreads = 256;
 constexpr int kTopkWaves = kTopkThreads / kWave;
-constexpr int kTopkSlots = 16;  // keys per thread
-constexpr int kTopkMaxSpan = kTopkSlots * kTopkThreads;   // 4096 logits
-constexpr int kTopkMaxMerge = kTopkSlots * kTopkThreads;  // 4096 keys
+constexpr int kTopkMaxSlots = 16;  // keys per thread, at most
+constexpr int kTopkMaxSpan = kTopkMaxSlots * kTopkThreads;   // 4096 logits
+constexpr int kTopkMaxMerge = kTopkMaxSlots * kTopkThreads;  // 4096 keys
 constexpr int kTopkMinSpan = 1024;
 constexpr int kLmMaxTopK = 64;
 constexpr size_t kLmHeaderBytes = 256;  // reserved
@@ -45,13 +45,15 @@ struct TopkArgs {
 
 // Largest key strictly below `thr` among a thread's keys, maximised over the
 // workgroup.  `parity` alternates the LDS slot between passes so one barrier
-// per pass suffices.
+// per pass suffices.  SLOTS (keys per thread) is the smallest of 4, 8, 16
+// that holds the kernel's keys: the per-thread scan is most of a pass.
+template <int SLOTS>
 __device__ __forceinline__ uint64_t block_next_key(
-    const uint64_t (&keys)[kTopkSlots], uint64_t thr,
+    const uint64_t (&keys)[SLOTS], uint64_t thr,
     uint64_t (&red)[2][kTopkWaves], int parity) {
   uint64_t best = 0ull;
 #pragma unroll
-  for (int t = 0; t < kTopkSlots; ++t)
+  for (int t = 0; t < SLOTS; ++t)
     if (keys[t] < thr && keys[t] > best) best = keys[t];
   best = wave_max_u64(best);
   if ((threadIdx.x & (kWave - 1)) == 0) red[parity][threadIdx.x / kWave] = best;
@@ -63,16 +65,18 @@ __device__ __forceinline__ uint64_t block_next_key(
   return best;
 }
 
-// Candidates: workgroup b selects the top-k of logits [b*span, (b+1)*span).
+// Candidates: workgroup b selects the top-k of logits [b*span, (b+1)*span)
+// (span <= SLOTS * kTopkThreads).
+template <int SLOTS>
 __global__ __launch_bounds__(kTopkThreads) void topk_candidates_kernel(
     TopkArgs a) {
   __shared__ uint64_t s_red[2][kTopkWaves];
   const int tid = threadIdx.x;
   const int64_t begin = static_cast<int64_t>(blockIdx.x) * a.span;
   const int n = static_cast<int>(min(static_cast<int64_t>(a.span), a.rows - begin));
-  uint64_t keys[kTopkSlots];
+  uint64_t keys[SLOTS];
 #pragma unroll
-  for (int t = 0; t < kTopkSlots; ++t) {
+  for (int t = 0; t < SLOTS; ++t) {
     const int i = t * kTopkThreads + tid;
     keys[t] = i < n ? topk_key(a.logits[begin + i],
                                static_cast<uint32_t>(a.row_offset + begin + i))
@@ -86,16 +90,18 @@ __global__ __launch_bounds__(kTopkThreads) void topk_candidates_kernel(
 }
 
 // Merge (one workgroup): all spans' candidates plus the running list of
-// earlier chunks.  A separate launch, so the kernel boundary publishes the
-// candidates (no per-workgroup L2 writeback for a ticket).
+// earlier chunks (at most SLOTS * kTopkThreads keys).  A separate launch, so
+// the kernel boundary publishes the candidates (no per-workgroup L2
+// writeback for a ticket).
+template <int SLOTS>
 __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(TopkArgs a) {
   __shared__ uint64_t s_red[2][kTopkWaves];
   const int tid = threadIdx.x;
   const int ncand = a.nblocks * a.top_k;
   const int ntot = ncand + (a.first ? 0 : a.top_k);
-  uint64_t keys[kTopkSlots];
+  uint64_t keys[SLOTS];
 #pragma unroll
-  for (int t = 0; t < kTopkSlots; ++t) {
+  for (int t = 0; t < SLOTS; ++t) {
     const int i = t * kTopkThreads + tid;
     keys[t] = i < ncand ? a.cand[i] : (i < ntot ? a.running[i - ncand] : 0ull);
   }
@@ -130,6 +136,27 @@ static bool topk_shape(int64_t rows, int64_t top_k, TopkShape *out) {
   out->span = static_cast<int>(span);
   out->nblocks = static_cast<int>((rows + span - 1) / span);
   return true;
+}
+
+// The candidates (CAND) or merge kernel with the fewest key slots per
+// thread that hold `keys` keys.
+template <bool CAND>
+static hipError_t launch_topk(const TopkArgs &a, int keys, dim3 grid,
+                              hipStream_t s) {
+  if (keys <= 4 * kTopkThreads)
+    return CAND ? launch_kernel(topk_candidates_kernel<4>, grid,
+                                dim3(kTopkThreads), 0, s, a)
+                : launch_kernel(topk_merge_kernel<4>, grid,
+                                dim3(kTopkThreads), 0, s, a);
+  if (keys <= 8 * kTopkThreads)
+    return CAND ? launch_kernel(topk_candidates_kernel<8>, grid,
+                                dim3(kTopkThreads), 0, s, a)
+                : launch_kernel(topk_merge_kernel<8>, grid,
+                                dim3(kTopkThreads), 0, s, a);
+  return CAND ? launch_kernel(topk_candidates_kernel<kTopkMaxSlots>, grid,
+                              dim3(kTopkThreads), 0, s, a)
+              : launch_kernel(topk_merge_kernel<kTopkMaxSlots>, grid,
+                              dim3(kTopkThreads), 0, s, a);
 }
 
 static size_t lm_workspace(int64_t rows) {
@@ -190,8 +217,7 @@ extern "C" int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
   a.cand = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes + kLmRunningBytes);
   a.out_values = out_values;
   a.out_indices = out_indices;
-  e = launch_kernel(topk_candidates_kernel, dim3(shape.nblocks),
-                    dim3(kTopkThreads), 0, s, a);
+  e = launch_topk<true>(a, a.span, dim3(shape.nblocks), s);
   if (e != hipSuccess) return e;
-  return launch_kernel(topk_merge_kernel, dim3(1), dim3(kTopkThreads), 0, s, a);
+  return launch_topk<false>(a, shape.nblocks * a.top_k + a.top_k, dim3(1), s);
 }
