@@ -895,7 +895,10 @@ def unit_copy_gaps(runtime, plan):
     units = plan.units
     by_op = {}
     gaps = []
+    timed = runtime._timed_copies  # units copied ahead of the call have no events
     for i in range(len(units) - 1):
+        if i not in timed or i + 1 not in timed:
+            continue
         gap = timing["copy_end"][i].elapsed_time(timing["copy_start"][i + 1])
         gaps.append(gap)
         op = units[i + 1].operation

@@ -138,6 +138,28 @@ class ResidentDeviceArena:
         return key in self.views
 
 
+class _CallStaging:
+    """Ring staging of one call's units (pinned_staging): futures of the
+    staged pinned sources, the next unit to stage, and the units whose
+    copies were made ahead of the call.  Ring keys are (serial, unit), so
+    placements of successive calls never share a key."""
+
+    def __init__(self, serial, generation):
+        self.serial = serial
+        self.generation = generation
+        self.staged = {}
+        self.next = 0
+        self.copied = set()
+
+    def drain(self):
+        for future in list(self.staged.values()):
+            try:
+                future.result()
+            except Exception:  # the call that used it already raised
+                pass
+        self.staged = {}
+
+
 def _unit_views(unit, base):
     views = {}
     for piece in unit.pieces:
@@ -169,8 +191,12 @@ class DoubleBufferRuntime:
       their slots, the first LM-head chunks are copied in (``release_hook``,
       set by VocabStreamingRuntime); as the last chunks (or, with a resident
       vocabulary, the last units) free theirs, the next call's first units
-      are, when the store is full_pinned (``prefetch_across_calls``).  The
-      copy engine then never waits for the host between tokens.
+      are (``prefetch_across_calls``): from the arena when the store is
+      full_pinned; for pinned_staging, from the staging ring once
+      ``stage_call_ahead`` (called by the vocabulary runtime behind its last
+      chunk, and again when the next call gathers its embedding rows) has
+      staged them.  The copy engine then never waits for the host between
+      calls.
 
     run() returns once every unit's work is enqueued; the coordinator
     (caller's) stream waits for the last unit, without a host
@@ -209,6 +235,10 @@ class DoubleBufferRuntime:
         # gone to the staging workers (VocabStreamingRuntime queues the
         # staging of its first chunks behind it)
         self.staging_done_hook = None
+        # pinned_staging: the next call's staging, started ahead of it by
+        # stage_call_ahead (None: not started)
+        self._ahead = None
+        self._serial = 0
         # (kind, index, ready event, store generation of the bytes)
         self._owner = [None] * self.slot_count
         self._last_free = [None] * self.slot_count  # event of the last reader
@@ -298,6 +328,7 @@ class DoubleBufferRuntime:
             except Exception:  # the run that made it already raised
                 pass
         self.copy_stream.synchronize()
+        self._drop_ahead()
 
     def slot_released(self, slot, free):
         """``free`` (a compute-stream event) marks the end of the last
@@ -314,17 +345,106 @@ class DoubleBufferRuntime:
 
     def prefetch_next_call(self, slot):
         """Copy the first unit a call reads from ``slot`` ahead of that
-        call, when the store's source needs no staging (full_pinned)."""
+        call: from the store's arena when it needs no staging (full_pinned),
+        or, for pinned_staging, from the ring once stage_call_ahead has
+        staged it (a unit still staging is left to the call)."""
 
         units = self.plan.units
-        if (not self.prefetch_across_calls or slot >= len(units)
-                or self.store.mode.value != "full_pinned"):
+        if not self.prefetch_across_calls or slot >= len(units):
             return
         if self.slot_holding(slot, "unit", slot) is not None:
             return
         unit = units[slot]
-        self.slot_copy(slot, "unit", slot, self.store.unit_source(unit),
-                       unit.nbytes, self._ready[slot])
+        mode = self.store.mode.value
+        if mode == "full_pinned":
+            self.slot_copy(slot, "unit", slot, self.store.unit_source(unit),
+                           unit.nbytes, self._ready[slot])
+            return
+        call = self._ahead
+        if mode != "pinned_staging" or call is None or slot in call.copied:
+            return
+        future = call.staged.get(slot)
+        if future is None or not future.done() or future.exception() is not None:
+            return
+        self.slot_copy(slot, "unit", slot, future.result(), unit.nbytes,
+                       self._ready[slot])
+        self.store.staging_ring.copied((call.serial, slot), self._ready[slot])
+        del call.staged[slot]
+        call.copied.add(slot)
+
+    # ------------------------------------------------------ ahead staging
+
+    def _ring(self):
+        if self.store.mode.value != "pinned_staging":
+            return None
+        return getattr(self.store, "staging_ring", None)
+
+    def _stage_ahead(self, call, done):
+        """Ring staging: units after ``done`` (whose copy is enqueued) go to
+        the staging workers while the ring has room for them."""
+
+        units = self.plan.units
+        count = len(units)
+        ring = self.store.staging_ring
+        while call.next < count and call.next - done <= self.stage_lookahead:
+            i = call.next
+            placed = ring.place(units[i].nbytes, (call.serial, i))
+            if placed is None:
+                break
+            call.staged[i] = self.store.stage_in_ring(units[i], *placed)
+            call.next += 1
+            if call.next == count and self.staging_done_hook is not None:
+                self.staging_done_hook()
+
+    def _new_call(self):
+        self._serial += 1
+        return _CallStaging(self._serial, self._store_generation())
+
+    def stage_call_ahead(self):
+        """pinned_staging: start staging the next run's first units now, into
+        the ring behind the copies that last read it, so they stage while
+        the caller finishes this call (VocabStreamingRuntime calls this once
+        the LM head's last chunk is queued) or gathers the next call's
+        embedding rows.  prefetch_next_call may then copy them ahead too.
+        No-op in other modes, after a run that raised, or when already
+        started."""
+
+        if self._ring() is None or self._ahead is not None or self._failed:
+            return
+        self.store.reset_profile()  # the staging profile counts the next call
+        call = self._new_call()
+        self._ahead = call
+        self._stage_ahead(call, -1)
+
+    def _take_ahead(self):
+        """The call staged ahead, if it can serve this run: the store's bytes
+        unchanged, and every unit copied ahead still in its slot (an LM-head
+        call between runs may have taken the slot back).  Otherwise it is
+        drained and dropped."""
+
+        call = self._ahead
+        if call is None:
+            return None
+        if call.generation == self._store_generation() and all(
+                self.slot_holding(i % self.slot_count, "unit", i) is not None
+                for i in call.copied):
+            self._ahead = None
+            return call
+        self._drop_ahead()
+        return None
+
+    def _drop_ahead(self):
+        """Forget the call staged ahead once nothing of it is in flight
+        (staging jobs done, copies done): its ring placements go too."""
+
+        call, self._ahead = self._ahead, None
+        if call is None:
+            return
+        call.drain()
+        self.copy_stream.synchronize()
+        ring = self._ring()
+        if ring is not None:
+            ring.reset()
 
     # ----------------------------------------------------------------- run
 
@@ -339,6 +459,7 @@ class DoubleBufferRuntime:
         self._staging_left = {}
         self.copy_stream.synchronize()
         self.compute_stream.synchronize()
+        self._drop_ahead()
         ring = getattr(self.store, "staging_ring", None)
         if ring is not None:
             ring.reset()
@@ -361,7 +482,6 @@ class DoubleBufferRuntime:
         slots = self.slot_count
         compute_stream = self.compute_stream
         timing = self._timing_events() if self.profile else None
-        self.store.reset_profile()
         self._timed_copies = {}
 
         # work the caller enqueued before (the embedding) precedes the units
@@ -371,24 +491,19 @@ class DoubleBufferRuntime:
             timing["pipeline"][0].record(self.coordinator)
 
         staging = self.store.mode.value == "pinned_staging"
-        ring = getattr(self.store, "staging_ring", None) if staging else None
-        staged = {}
+        ring = self._ring()
+        call = None
+        if ring is not None:
+            call = self._take_ahead()
+            if call is None:
+                ring.reset()  # every copy that read the pinned slots is done
+                self.store.reset_profile()
+                call = self._new_call()
+            staged = call.staged
+        else:
+            self.store.reset_profile()
+            staged = {}
         self._staging_left = staged
-        next_stage = 0
-
-        def stage_ahead(done):
-            # ring staging: units after ``done`` (whose copy is enqueued) go
-            # to the staging workers while the ring has room for them
-            nonlocal next_stage
-            while next_stage < count and next_stage - done <= self.stage_lookahead:
-                placed = ring.place(units[next_stage].nbytes, next_stage)
-                if placed is None:
-                    break
-                staged[next_stage] = self.store.stage_in_ring(units[next_stage],
-                                                              *placed)
-                next_stage += 1
-                if next_stage == count and self.staging_done_hook is not None:
-                    self.staging_done_hook()
 
         source_wait_ms = 0.0
 
@@ -409,8 +524,8 @@ class DoubleBufferRuntime:
             self.slot_copy(slot, "unit", i, source, units[i].nbytes,
                            self._ready[i], pair)
             if ring is not None:
-                ring.copied(i, self._ready[i])
-                stage_ahead(i)
+                ring.copied((call.serial, i), self._ready[i])
+                self._stage_ahead(call, i)
             elif staging and i + slots < count:
                 # the staging worker may refill this pinned slot once this
                 # copy has read it (it need not wait for the compute)
@@ -418,15 +533,15 @@ class DoubleBufferRuntime:
                     units[i + slots], slot, reuse_event=self._ready[i])
 
         if ring is not None:
-            ring.reset()  # every copy that read the pinned slots is done
-            stage_ahead(-1)
+            self._stage_ahead(call, -1)
         elif staging:
             for i in range(min(slots, count)):
                 staged[i] = self.store.prepare_unit(units[i], i)
         ready = {}
         for i in range(min(slots, count)):
             held = self.slot_holding(i % slots, "unit", i)
-            if held is not None and not staging:
+            if held is not None and (not staging
+                                     or (call is not None and i in call.copied)):
                 ready[i] = held  # copied ahead of this call
             else:
                 copy_unit(i)

@@ -3,8 +3,9 @@ layer_streaming/vocab.py).
 
 * ``embedding(ids)`` gathers the requested rows of the host embedding into a
   page-locked row buffer and copies them to the device on the caller's
-  stream (vocab.py:100-131).  Nothing waits on the host: an event guards the
-  row buffer until the copy that reads it is done.
+  stream (vocab.py:100-131).  The buffer's two halves take turns, so one
+  group of rows is gathered while the previous group's copy runs; an event
+  per half guards it until the copy that reads it is done.
 * ``lm_head_topk(h, top_k, return_full_logits)`` streams the LM head in row
   chunks through the transformer runtime's two device slots and keeps an
   exact running top-k on the device (vocab.py:149-300).  Per chunk there is
@@ -12,12 +13,14 @@ layer_streaming/vocab.py).
   top-k and the merge with the running list).  Hand-off and slot ownership
   follow DoubleBufferRuntime: the host waits for a chunk's copy, then
   enqueues its kernel; the first two chunks are copied while the
-  transformer's last units still run, and (full_pinned) the next call's
-  first units while the last chunks run.  With a pinned_staging store the
-  chunks pass through two pinned halves, staged on the store's staging
-  workers ahead of their copies: the first two queued behind the call's last
-  unit, chunk c + 2 as soon as chunk c's copy is enqueued (the reference
-  stages each chunk on the calling thread, vocab.py:133-147).  The call
+  transformer's last units still run, and the next call's first units while
+  the last chunks run.  With a pinned_staging store the chunks pass through
+  two pinned halves, staged on the store's staging workers ahead of their
+  copies: the first two queued behind the call's last unit, chunk c + 2 as
+  soon as chunk c's copy is enqueued (the reference stages each chunk on
+  the calling thread, vocab.py:133-147); behind the last chunk the next
+  call's first units are staged into the transformer's ring
+  (DoubleBufferRuntime.stage_call_ahead).  The call
   returns when the top-k is in HBM (the reference synchronises there too,
   vocab.py:268-271).
 * ``merge_topk`` is the reference's public helper (vocab.py:11-32) with a
@@ -117,7 +120,12 @@ class VocabStreamingRuntime:
         self._staging_read = [None, None]  # copy that last read a pinned half
         self._prestaged = {}  # chunk -> future of its staged pinned half
         self._start = _hip.HipEvent()
-        self._rows_free = _hip.HipEvent()
+        # gather groups alternate between the two halves of the row buffer
+        # (one group of its single row when it holds one)
+        group = max(1, row_buffer // 2)
+        self._row_halves = [self.embedding_staging[h * group:(h + 1) * group]
+                            for h in range(min(2, row_buffer))]
+        self._rows_free = [_hip.HipEvent() for _ in self._row_halves]
         self._timers = None
         self._timed = {}
         self._workspaces = {}
@@ -145,6 +153,9 @@ class VocabStreamingRuntime:
     def embedding(self, input_ids):
         """Gather only the requested CPU rows and copy them to the GPU."""
 
+        # pinned_staging: the call's first units stage while the rows are
+        # gathered (no-op if the last call already started them)
+        self.transformer_runtime.stage_call_ahead()
         shape = tuple(input_ids.shape)
         ids = input_ids.detach().reshape(-1).to(device="cpu", dtype=torch.long)
         count = ids.numel()
@@ -155,15 +166,20 @@ class VocabStreamingRuntime:
         out = torch.empty((count, width), dtype=torch.bfloat16, device=self.device)
         self.last_embedding_bytes = count * width * 2
         stream = torch.cuda.current_stream(self.device)
-        for first in range(0, count, self.embedding_staging_rows):
-            rows = min(self.embedding_staging_rows, count - first)
-            # the row buffer is free once the copy that last read it is done
-            self._rows_free.synchronize()
-            buffer = self.embedding_staging[:rows]
+        # the row buffer's halves take turns: one is gathered into while the
+        # other's copy runs
+        halves = self._row_halves
+        group = halves[0].shape[0]
+        for n, first in enumerate(range(0, count, group)):
+            rows = min(group, count - first)
+            half = n % len(halves)
+            # the half is free once the copy that last read it is done
+            self._rows_free[half].synchronize()
+            buffer = halves[half][:rows]
             torch.index_select(table, 0, ids[first:first + rows], out=buffer)
             _hip.memcpy_h2d_async(out[first:first + rows], buffer,
                                   rows * width * 2, stream)
-            self._rows_free.record(stream)
+            self._rows_free[half].record(stream)
         return out.view(shape + (width,))
 
     # ----------------------------------------------------------- LM head
@@ -186,6 +202,10 @@ class VocabStreamingRuntime:
         target = self.head_staging_slots[half][: rows.numel()]
         self._prestaged[chunk] = self.store.stage_into(
             target, rows, () if reader is None else (reader,))
+        if chunk == self.vocab.chunk_count - 1:
+            # the next call's first units stage behind the last chunk, and
+            # are copied as the last chunks free their slots
+            self.transformer_runtime.stage_call_ahead()
 
     def _prestage_first_chunks(self):
         for chunk in range(min(2, self.vocab.chunk_count)):

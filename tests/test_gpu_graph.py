@@ -100,11 +100,13 @@ def test_qkv_at_clamps_a_length_past_capacity(gpu_device):
 
 
 # (splits of the length's plan, of the capacity's): (1, 1), (1, 1), (2, 2),
-# (2, 64), (64, 64) with rows moving between splits as the length grows,
-# (64, 64), (64, 64)
+# (2, 64), then 64 and 64, with rows past the length NaN in the last block
+# ((33, 40), (2049, 2080)) and the longer splits of the two plans starting
+# at different rows ((2101, 2200), (32769, 34800))
 @pytest.mark.parametrize("length,capacity", [(1, 1), (7, 12), (33, 40),
-                                             (40, 2200), (2101, 2200),
-                                             (4100, 4100), (32769, 34800)])
+                                             (40, 2200), (2049, 2080),
+                                             (2101, 2200), (4100, 4100),
+                                             (32769, 34800)])
 def test_attention_at_equals_attention(gpu_device, length, capacity):
     dev = torch.device(gpu_device)
     gen = torch.Generator(device=dev).manual_seed(length)

@@ -300,3 +300,82 @@ def test_store_close_drains_the_runtime_copies(doubles):
     # were waited for before the arena was dropped
     assert doubles == [("stream_sync", "copy")]
     assert store.arena is None and runtime.slot_holding(0, "unit", 0) is None
+
+
+def _staged_runtime(doubles):
+    plan = build_llama31_8b_plan("matrix", num_layers=1, stream_vocab=True)
+    store = PinnedStagingWeightStore(plan, tensor_factory=cpu_factory)
+    mark_units(store)
+    runtime = rt.DoubleBufferRuntime(plan, store, resident=None, device="cpu")
+    return plan, store, runtime
+
+
+def _stage_and_copy_ahead(runtime):
+    # what VocabStreamingRuntime does at the end of a call: stage the next
+    # call's first units, then copy them as the last chunks free the slots
+    runtime.stage_call_ahead()
+    for i in (0, 1):
+        runtime._ahead.staged[i].result()
+        runtime.prefetch_next_call(i)
+
+
+def test_staged_next_call_is_staged_and_copied_ahead(doubles):
+    plan, store, runtime = _staged_runtime(doubles)
+    runtime.run(UnitChecker(store, doubles), state=None)
+    del doubles[:]
+    _stage_and_copy_ahead(runtime)
+    assert len(events_of(doubles, "copy")) == 2
+    assert runtime.slot_holding(0, "unit", 0) is runtime._ready[0]
+    # a second request changes nothing
+    runtime.stage_call_ahead()
+    runtime.prefetch_next_call(0)
+    assert len(events_of(doubles, "copy")) == 2
+    del doubles[:]
+    check = UnitChecker(store, doubles)
+    runtime.run(check, state=None)
+    assert check.seen == [u.unit_id for u in plan.units]
+    # units 0 and 1 were in place: this call copied the others only, and
+    # every unit was staged exactly once for it
+    assert len(events_of(doubles, "copy")) == len(plan.units) - 2
+    assert store.profile_stats()["staging_copy_count"] == len(plan.units)
+    # and the next call again
+    _stage_and_copy_ahead(runtime)
+    del doubles[:]
+    check = UnitChecker(store, doubles)
+    runtime.run(check, state=None)
+    assert check.seen == [u.unit_id for u in plan.units]
+    store.close()
+
+
+def test_staged_ahead_units_are_dropped_when_the_store_reloads(doubles, monkeypatch):
+    plan, store, runtime = _staged_runtime(doubles)
+    runtime.run(UnitChecker(store, doubles), state=None)
+    _stage_and_copy_ahead(runtime)
+    del doubles[:]
+    _loading(monkeypatch, doubles, base=500)
+    store.load_checkpoint("weights.safetensors")
+    # the copies made ahead were waited for before the new bytes
+    assert doubles.index(("stream_sync", "copy")) < doubles.index(
+        ("load", "weights.safetensors"))
+    assert runtime._ahead is None
+    del doubles[:]
+    check = UnitChecker(store, doubles)  # compares with the new bytes
+    runtime.run(check, state=None)
+    assert check.seen == [u.unit_id for u in plan.units]
+    assert len(events_of(doubles, "copy")) == len(plan.units)
+    store.close()
+
+
+def test_staged_ahead_units_whose_slot_was_taken_are_staged_again(doubles):
+    plan, store, runtime = _staged_runtime(doubles)
+    runtime.run(UnitChecker(store, doubles), state=None)
+    _stage_and_copy_ahead(runtime)
+    # an LM-head chunk copied into slot 0 between the calls
+    chunk = torch.zeros(64, dtype=torch.bfloat16)
+    runtime.slot_copy(0, "chunk", 0, chunk, chunk.numel() * 2, FakeEvent(doubles))
+    del doubles[:]
+    check = UnitChecker(store, doubles)
+    runtime.run(check, state=None)
+    assert check.seen == [u.unit_id for u in plan.units]
+    assert len(events_of(doubles, "copy")) == len(plan.units)
+    store.close()

@@ -87,3 +87,69 @@ def test_streamed_vocabulary_needs_two_device_slots():
                                                          device="meta")])
     with pytest.raises(ValueError, match="two device slots"):
         VocabStreamingRuntime(plan, store=None, transformer_runtime=one_slot)
+
+
+@pytest.mark.parametrize("row_buffer", [1, 3, 256])
+@pytest.mark.parametrize("count", [1, 5, 300])
+def test_embedding_rows_through_alternating_buffer_halves(monkeypatch, row_buffer,
+                                                          count):
+    # the gathered rows equal the table's; group g reuses a half only after
+    # waiting for the copy of group g - 2 (the last one that read it)
+    from types import SimpleNamespace
+
+    from layer_streaming import _hip
+    from layer_streaming import vocab as vocab_mod
+    from layer_streaming.plan import build_llama31_8b_plan
+    from layer_streaming.weight_store import WeightStoreMode
+
+    log = []
+
+    class Event:
+        def __init__(self, enable_timing=False):
+            self.id = len([e for e in log if e[0] == "new"])
+            log.append(("new", self.id))
+
+        def record(self, stream=None):
+            log.append(("record", self.id))
+
+        def synchronize(self):
+            log.append(("sync", self.id))
+
+    def copy(dst, src, nbytes, stream):
+        dst.view(-1)[: nbytes // 2].copy_(src.reshape(-1)[: nbytes // 2])
+        log.append(("copy", src.data_ptr()))
+
+    monkeypatch.setattr(_hip, "load", lambda: None)
+    monkeypatch.setattr(_hip, "HipEvent", Event)
+    monkeypatch.setattr(_hip, "memcpy_h2d_async", copy)
+    monkeypatch.setattr(vocab_mod, "_pinned_rows",
+                        lambda n, w: torch.empty((n, w), dtype=torch.bfloat16))
+    monkeypatch.setattr(vocab_mod.torch.cuda, "current_stream", lambda device=None: None)
+    plan = build_llama31_8b_plan("matrix_group", num_layers=1, stream_vocab=True)
+    gen = torch.Generator().manual_seed(count)
+    table = torch.randn(400, 4096, generator=gen).to(torch.bfloat16)
+    store = SimpleNamespace(mode=WeightStoreMode.FULL_PINNED,
+                            tensor=lambda key: table)
+    slots = [torch.empty(plan.slot_elements, dtype=torch.bfloat16, device="meta")
+             for _ in range(2)]
+    runtime = SimpleNamespace(device_slots=slots, device=torch.device("cpu"),
+                              copy_stream=None, compute_stream=None,
+                              coordinator=None, stage_call_ahead=lambda: None)
+    vocab = vocab_mod.VocabStreamingRuntime(plan, store, runtime,
+                                            embedding_staging_rows=row_buffer)
+    ids = torch.randint(0, 400, (1, count), generator=gen)
+    del log[:]
+    out = vocab.embedding(ids)
+    assert out.shape == (1, count, 4096)
+    assert torch.equal(out[0], table[ids[0]])
+    halves = len(vocab._rows_free)
+    assert halves == min(2, row_buffer)
+    group = max(1, row_buffer // 2)
+    groups = -(-count // group)
+    sources = [e[1] for e in log if e[0] == "copy"]
+    assert len(sources) == groups
+    assert len(set(sources)) == min(groups, halves)
+    waits = [e for e in log if e[0] in ("sync", "record")]
+    for n in range(groups):
+        half = vocab._rows_free[n % halves].id
+        assert waits[2 * n] == ("sync", half) and waits[2 * n + 1] == ("record", half)
