@@ -102,7 +102,43 @@ struct AttnArgs {
   // then holds the cache capacity, which sets nsplits; the splits follow
   // the word's length, and those past its plan write empty partials)
   const int64_t *len_word;
+  // FUSED kernels: per-KV-head arrival / completion counters (one 128-byte
+  // line per head, zero before and after every call) and the caller's
+  // error word (kFusedErr* bits are or-ed in)
+  uint32_t *sync;
+  int32_t *error;
 };
+
+// Split merge inside the attention launch ("fused").  The grid is 1-D,
+// nsplits x 8 workgroups: workgroup b serves split b / 8 of the KV head
+// whose index is the XCC id of the XCD it runs on.  Workgroups are dealt to
+// the 8 XCDs round-robin, so each XCD receives one workgroup of every
+// index b / 8 -- whichever XCD the round starts at: eagerly launched
+// workgroup b lands on XCD b % 8, graph-replayed launches were seen to start
+// elsewhere -- and every split of head g runs on XCD g, sharing that XCD's
+// L2.  Counters and partials of head g are therefore only touched through
+// one L2, where the atomics are performed: after its
+// partial stores are acknowledged, a workgroup takes an arrival ticket; the
+// last kFusedMergers to arrive wait (bounded) until all nsplits have
+// arrived, then each merges one eighth of the head's 4 x 128 outputs --
+// the arithmetic, and so the result, of decode_attention_merge_kernel, bit
+// for bit -- and the last of them to finish resets the counters.  No
+// workgroup waits for one that has not started: only the last arrivals
+// wait, for workgroups that already hold their CUs.
+// decode_attention_merge_kernel's shape: four quarters of the splits per
+// output dim (also the fused merge's)
+constexpr int kMergeQuarters = 4;
+constexpr int kMergeThreads = kMergeQuarters * kAttnD;
+constexpr int kMergePerQuarter = kAttnMaxSplits / kMergeQuarters;
+constexpr int kFusedHeads = 8;     // KV heads = XCDs
+constexpr int kFusedMergers = 8;   // 4 query heads x 2 halves of 64 dims
+constexpr int kFusedLineWords = 32;  // one 128-byte line per head
+constexpr int kFusedSpinLimit = 1 << 16;
+constexpr int32_t kFusedErrPlacement = 2;  // XCDs got unequal shares of the grid
+constexpr int32_t kFusedErrTimeout = 4;    // a merger's wait ran out
+
+static_assert(CASCADE_DECODE_ATTENTION_SYNC_BYTES >= kFusedHeads * kFusedLineWords * 4,
+              "sync buffer holds one line per KV head");
 
 template <bool NT>
 __device__ __forceinline__ u32x4 kv_load(const uint16_t *p) {
@@ -112,14 +148,151 @@ __device__ __forceinline__ u32x4 kv_load(const uint16_t *p) {
     return *reinterpret_cast<const u32x4 *>(p);
 }
 
-template <int WAVES, bool NT, bool AT = false>
+// Atomics performed in the L2 of the calling XCD (workgroup scope: no
+// write-back or bypass of the L2), for the fused merge's counters.
+__device__ __forceinline__ uint32_t l2_fetch_add(uint32_t *p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The counter's current value by an atomic add of zero, issued as an
+// instruction of its own: the compiler would turn a fetch_add(p, 0) into a
+// plain load, whose hit in the CU's vector cache could return a stale value
+// on every poll.
+__device__ __forceinline__ uint32_t l2_atomic_read(uint32_t *p) {
+  uint32_t old;
+  const uint32_t zero = 0;
+  asm volatile("global_atomic_add %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)"
+               : "=&v"(old)
+               : "v"(p), "v"(zero)
+               : "memory");
+  return old;
+}
+
+__device__ __forceinline__ void l2_exchange(uint32_t *p, uint32_t v) {
+  (void)__hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// A load that skips the CU's vector cache and reads the L2, where the other
+// CUs' partial stores of this XCD landed (global_load ... sc0).
+__device__ __forceinline__ float l2_load(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xfu;
+}
+
+// The fused tail of one workgroup of KV head g (its partial already
+// stored): arrival, and for the last kFusedMergers arrivals the merge of
+// one slice of the head's outputs.  256 threads.
+__device__ __forceinline__ void fused_merge_tail(const AttnArgs &a, int g, int tid) {
+  constexpr int G = kAttnG, D = kAttnD;
+  constexpr int kSlice = G * D / kFusedMergers;  // 64 dims of one query head
+  __shared__ uint32_t s_ticket, s_ok;
+  __shared__ float s_w[kAttnMaxSplits];
+  __shared__ float s_part[kMergeQuarters][kSlice];
+  __shared__ float s_den;
+  uint32_t *line = a.sync + g * kFusedLineWords;
+  // this wave's partial stores acknowledged by the L2 (stores count in
+  // vmcnt on gfx9), then every wave's, before the ticket
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  __syncthreads();
+  if (tid == 0) s_ticket = l2_fetch_add(line, 1u);
+  __syncthreads();
+  const int first = a.nsplits - kFusedMergers;
+  const int ticket = static_cast<int>(s_ticket);
+  if (ticket < first) return;
+  if (ticket >= a.nsplits) {
+    // more workgroups of this head than splits: the XCDs did not receive
+    // equal shares of the grid (workgroups not dealt round-robin)
+    if (tid == 0)
+      __hip_atomic_fetch_or(a.error, kFusedErrPlacement, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (tid == 0) {
+    uint32_t seen = 0;
+    for (int n = 0; n < kFusedSpinLimit; ++n) {
+      seen = l2_atomic_read(line);
+      if (seen >= static_cast<uint32_t>(a.nsplits)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    s_ok = seen >= static_cast<uint32_t>(a.nsplits);
+    if (!s_ok)
+      __hip_atomic_fetch_or(a.error, kFusedErrTimeout, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_ok) return;
+
+  // slice = (query head h, dims 64 hf ..): decode_attention_merge_kernel's
+  // per-output arithmetic with the quarters over 64 instead of 128 dims
+  const int slice = ticket - first;
+  const int h = slice / 2;
+  const int dl = tid % kSlice;
+  const int d = kSlice * (slice % 2) + dl;
+  const int quarter = tid / kSlice;
+  const int64_t base = static_cast<int64_t>(g) * a.nsplits * G + h;
+  float v[kMergePerQuarter];
+#pragma unroll
+  for (int i = 0; i < kMergePerQuarter; ++i) {
+    const int c = quarter * kMergePerQuarter + i;
+    v[i] = c < a.nsplits ? l2_load(a.part_acc + (base + static_cast<int64_t>(c) * G) * D + d)
+                         : 0.0f;
+  }
+  if (tid < kWave) {
+    const float mc = tid < a.nsplits ? l2_load(a.part_ml + (base + tid * G) * 2) : -INFINITY;
+    const float lc = tid < a.nsplits ? l2_load(a.part_ml + (base + tid * G) * 2 + 1) : 0.0f;
+    const float mx = wave_max(mc);
+    const float wc = tid < a.nsplits ? exp2_fast(mc - mx) : 0.0f;
+    s_w[tid] = wc;
+    const float den = wave_sum(wc * lc);
+    if (tid == 0) s_den = den;
+  }
+  __syncthreads();
+  float r = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMergePerQuarter; ++i)
+    r = fmaf(s_w[quarter * kMergePerQuarter + i], v[i], r);
+  s_part[quarter][dl] = r;
+  __syncthreads();
+  if (quarter == 0) {
+    r = s_part[0][dl];
+#pragma unroll
+    for (int q = 1; q < kMergeQuarters; ++q) r += s_part[q][dl];
+    a.out[(static_cast<int64_t>(g) * G + h) * D + d] = f32_to_bf16(r / s_den);
+  }
+  // the last merger to finish leaves the counters at zero for the next
+  // call (every merger has passed its wait by then)
+  if (tid == 0 && l2_fetch_add(line + 16, 1u) == kFusedMergers - 1) {
+    l2_exchange(line + 16, 0u);
+    l2_exchange(line, 0u);
+  }
+}
+
+template <int WAVES, bool NT, bool AT = false, bool FUSED = false>
 __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
     AttnArgs a) {
   constexpr int G = kAttnG, D = kAttnD;
   constexpr int kPassRows = WAVES * kAttnBlock;
-  const int split = blockIdx.x;
-  const int g = blockIdx.y;
+  static_assert(!FUSED || WAVES * kWave == kMergeQuarters * kAttnD / 2,
+                "the fused merge runs on 256 threads");
+  // FUSED: the XCD the workgroup runs on picks its KV head, its index
+  // picks the split (see "Split merge inside the attention launch")
+  const int split = FUSED ? static_cast<int>(blockIdx.x) / kFusedHeads
+                          : static_cast<int>(blockIdx.x);
+  const int g = FUSED ? static_cast<int>(xcc_id()) : static_cast<int>(blockIdx.y);
   const int tid = threadIdx.x;
+  if constexpr (FUSED) {
+    if (g >= kFusedHeads) {  // a device with more XCDs than KV heads
+      if (tid == 0)
+        __hip_atomic_fetch_or(a.error, kFusedErrPlacement, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+  }
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int c16 = lane & 15;
@@ -150,6 +323,7 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
         a.part_ml[(slot0 + tid) * 2] = -INFINITY;
         a.part_ml[(slot0 + tid) * 2 + 1] = 0.0f;
       }
+      if constexpr (FUSED) fused_merge_tail(a, g, tid);
       return;
     }
   }
@@ -278,6 +452,7 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
       }
     }
   }
+  if constexpr (FUSED) fused_merge_tail(a, g, tid);
 }
 
 // Merge of the splits, one workgroup per (KV head, query head): lane c of
@@ -287,9 +462,6 @@ __global__ __launch_bounds__(WAVES *kWave) void decode_attention_kernel(
 // before the weights are known) and the quarters add up in LDS.  A separate
 // launch (rather than a last-workgroup ticket) lets the kernel boundary
 // publish the partials with one L2 writeback instead of one per workgroup.
-constexpr int kMergeQuarters = 4;
-constexpr int kMergeThreads = kMergeQuarters * kAttnD;
-constexpr int kMergePerQuarter = kAttnMaxSplits / kMergeQuarters;
 
 __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(
     AttnArgs a) {
@@ -733,6 +905,53 @@ static int launch_decode_attention(const AttnArgs &a, int64_t n_kv_heads,
   return launch_kernel(decode_attention_merge_kernel,
                        dim3(static_cast<unsigned>(n_kv_heads * kAttnG)),
                        dim3(kMergeThreads), 0, s, a);
+}
+
+// One launch of nsplits x 8 workgroups with the split merge inside.
+template <bool AT>
+static int launch_decode_attention_fused(AttnArgs &a, int64_t n_kv_heads, void *sync,
+                                         int32_t *error_flag, hipStream_t s) {
+  if (sync == nullptr || error_flag == nullptr) return CASCADE_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(sync) & 127) || (reinterpret_cast<uintptr_t>(error_flag) & 3))
+    return CASCADE_EALIGN;
+  if (n_kv_heads != kFusedHeads || a.nsplits < kFusedMergers) return CASCADE_ESHAPE;
+  a.sync = static_cast<uint32_t *>(sync);
+  a.error = error_flag;
+  return launch_kernel(decode_attention_kernel<kAttnWaves, true, AT, true>,
+                       dim3(static_cast<unsigned>(a.nsplits * kFusedHeads)),
+                       dim3(kAttnWaves * kWave), 0, s, a);
+}
+
+extern "C" int cascade_decode_attention_fused_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, int64_t len, int64_t n_q_heads, int64_t n_kv_heads,
+    int64_t head_dim, float scale, void *out, void *workspace,
+    size_t workspace_bytes, void *sync, int32_t *error_flag, void *stream) {
+  AttnArgs a{};
+  if (int e = decode_attention_args(q, k_cache, v_cache, kv_head_stride, len,
+                                    n_q_heads, n_kv_heads, head_dim, scale,
+                                    out, workspace, workspace_bytes, a))
+    return e;
+  return launch_decode_attention_fused<false>(a, n_kv_heads, sync, error_flag,
+                                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cascade_decode_attention_fused_at_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, const int64_t *length, int64_t capacity,
+    int64_t n_q_heads, int64_t n_kv_heads, int64_t head_dim, float scale,
+    void *out, void *workspace, size_t workspace_bytes, void *sync,
+    int32_t *error_flag, void *stream) {
+  if (length == nullptr) return CASCADE_EINVAL;
+  if (reinterpret_cast<uintptr_t>(length) & 7) return CASCADE_EALIGN;
+  AttnArgs a{};
+  if (int e = decode_attention_args(q, k_cache, v_cache, kv_head_stride,
+                                    capacity, n_q_heads, n_kv_heads, head_dim,
+                                    scale, out, workspace, workspace_bytes, a))
+    return e;
+  a.len_word = length;
+  return launch_decode_attention_fused<true>(a, n_kv_heads, sync, error_flag,
+                                             static_cast<hipStream_t>(stream));
 }
 
 extern "C" int cascade_decode_attention_bf16(

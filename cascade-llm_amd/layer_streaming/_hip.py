@@ -68,6 +68,15 @@ _SIGNATURES = {
         _INT,
         [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P],
     ),
+    "cascade_decode_attention_fused_bf16": (
+        _INT,
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P, _P, _P],
+    ),
+    "cascade_decode_attention_fused_at_bf16": (
+        _INT,
+        [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _SZ, _P, _P,
+         _P],
+    ),
     "cascade_decode_attention_noalloc_bf16": (
         _INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P]),
     "cascade_gemm_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
@@ -115,8 +124,16 @@ _SIGNATURES = {
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 ESHAPE = 1003  # CASCADE_ESHAPE
+# fused decode attention: sync buffer size and the bits it ors into the
+# caller's error word (include/cascade_hip.h)
+ATTENTION_SYNC_BYTES = 1024
+ATTN_EPLACEMENT = 2
+ATTN_ETIMEOUT = 4
+# the fused form needs one KV head per XCD and at least 8 splits of 32 rows
+FUSED_ATTENTION_KV_HEADS = 8
+FUSED_ATTENTION_MIN_LEN = 225
 
 
 class HipLibraryError(RuntimeError):
@@ -665,6 +682,74 @@ def decode_attention_at(q, k_cache, v_cache, kv_head_stride, length, capacity,
          int(capacity), n_q_heads, n_kv_heads, head_dim, float(scale),
          out.data_ptr(), workspace.data_ptr(), workspace.numel(),
          stream_handle(stream))
+    return out
+
+
+def _fused_attention_args(sync, error_flag, n_kv_heads):
+    require_device(sync, "sync", torch.uint8, ATTENTION_SYNC_BYTES)
+    require_device(error_flag, "error_flag", torch.int32, 1)
+    if n_kv_heads != FUSED_ATTENTION_KV_HEADS:
+        raise ValueError("the fused attention needs {} KV heads".format(
+            FUSED_ATTENTION_KV_HEADS))
+
+
+def decode_attention_fused(q, k_cache, v_cache, kv_head_stride, length, out,
+                           workspace, sync, error_flag, scale, n_q_heads=32,
+                           n_kv_heads=8, head_dim=128, stream=None):
+    """decode_attention with the split merge inside the attention launch
+    (bit-identical results).  ``sync``: ATTENTION_SYNC_BYTES zero-filled
+    bytes, left zeroed; ``error_flag``: int32 word that receives
+    ATTN_EPLACEMENT / ATTN_ETIMEOUT.  length >= FUSED_ATTENTION_MIN_LEN."""
+
+    if int(length) < FUSED_ATTENTION_MIN_LEN:
+        raise ValueError("the fused attention needs length >= {}".format(
+            FUSED_ATTENTION_MIN_LEN))
+    _fused_attention_args(sync, error_flag, n_kv_heads)
+    _bf16(q, "q", n_q_heads * head_dim)
+    _bf16(out, "out", n_q_heads * head_dim)
+    for name, buf in (("k_cache", k_cache), ("v_cache", v_cache)):
+        require_device(buf, name, torch.bfloat16, contiguous=False)
+        end = buf.storage_offset() + (n_kv_heads - 1) * kv_head_stride + (
+            length * head_dim
+        )
+        if end > buf.untyped_storage().nbytes() // 2:
+            raise ValueError("{} is too small for length {}".format(name, length))
+    require_device(workspace, "workspace", torch.uint8)
+    call("cascade_decode_attention_fused_bf16", q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), int(kv_head_stride), int(length), n_q_heads,
+         n_kv_heads, head_dim, float(scale), out.data_ptr(),
+         workspace.data_ptr(), workspace.numel(), sync.data_ptr(),
+         error_flag.data_ptr(), stream_handle(stream))
+    return out
+
+
+def decode_attention_fused_at(q, k_cache, v_cache, kv_head_stride, length,
+                              capacity, out, workspace, sync, error_flag, scale,
+                              n_q_heads=32, n_kv_heads=8, head_dim=128,
+                              stream=None):
+    """decode_attention_at with the split merge inside the attention launch;
+    capacity >= FUSED_ATTENTION_MIN_LEN."""
+
+    _length_word(length, capacity)
+    if int(capacity) < FUSED_ATTENTION_MIN_LEN:
+        raise ValueError("the fused attention needs capacity >= {}".format(
+            FUSED_ATTENTION_MIN_LEN))
+    _fused_attention_args(sync, error_flag, n_kv_heads)
+    _bf16(q, "q", n_q_heads * head_dim)
+    _bf16(out, "out", n_q_heads * head_dim)
+    for name, buf in (("k_cache", k_cache), ("v_cache", v_cache)):
+        require_device(buf, name, torch.bfloat16, contiguous=False)
+        end = buf.storage_offset() + (n_kv_heads - 1) * kv_head_stride + (
+            capacity * head_dim
+        )
+        if end > buf.untyped_storage().nbytes() // 2:
+            raise ValueError("{} is too small for capacity {}".format(name, capacity))
+    require_device(workspace, "workspace", torch.uint8)
+    call("cascade_decode_attention_fused_at_bf16", q.data_ptr(),
+         k_cache.data_ptr(), v_cache.data_ptr(), int(kv_head_stride),
+         length.data_ptr(), int(capacity), n_q_heads, n_kv_heads, head_dim,
+         float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+         sync.data_ptr(), error_flag.data_ptr(), stream_handle(stream))
     return out
 
 

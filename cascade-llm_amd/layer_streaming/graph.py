@@ -13,7 +13,8 @@ device word instead:
   at its position, and advances the word;
 - the q|k|v launches (cascade_qkv_rope_at_bf16) take RoPE row and KV slot
   from the word, and the attention launches
-  (cascade_decode_attention_at_bf16) their length;
+  (cascade_decode_attention_fused_at_bf16, or cascade_decode_attention_at_bf16
+  where the fused form does not apply) their length;
 - the LM head writes its top-k into fixed buffers, whose first id is the
   next step's input.
 
@@ -149,7 +150,8 @@ class DecodeGraph:
         ex = self.executor
         return (ex.kv_cache.buffer.data_ptr(), ex.kv_cache.capacity,
                 ex.rope.cos.data_ptr(), ex.rope.sin.data_ptr(),
-                ex._attn_ws.data_ptr(), ex._head_ws.data_ptr(), ex._q_ptr,
+                ex._attn_ws.data_ptr(), ex._attn_sync.data_ptr(),
+                ex._head_ws.data_ptr(), ex._q_ptr,
                 ex._attn_ptr, ex._normed_ptr, ex._gate_ptr, ex._inter_ptr)
 
     def step(self, count=1):
@@ -182,8 +184,12 @@ class DecodeGraph:
         """Raise if a step saw an id outside the vocabulary or ran out of
         positions (waits for the GPU)."""
 
-        if int(self.step_buffers.error.item()) != 0:
-            raise RuntimeError("decode step error flag set")
+        value = int(self.step_buffers.error.item())
+        if value != 0:
+            if value & (_hip.ATTN_EPLACEMENT | _hip.ATTN_ETIMEOUT):
+                # the fused attention's counters are no longer at zero
+                self.executor._attn_sync.zero_()
+            raise RuntimeError("decode step error flag set ({})".format(value))
 
     def close(self):
         self.executor._device_step = None

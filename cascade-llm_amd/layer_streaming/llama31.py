@@ -213,10 +213,15 @@ def _check_ids(ids, vocab):
 class _ErrorWord:
     """An int32 device flag that kernels set on bad input, read back without
     blocking: ``publish`` copies it to pinned memory behind the step's work,
-    ``raise_if_set`` raises once that copy has landed (or waits for it)."""
+    ``raise_if_set`` raises once that copy has landed (or waits for it).
 
-    def __init__(self, device, message):
+    The embedding gather stores 1 for an id outside the vocabulary
+    (IndexError); the fused decode attention ors in _hip.ATTN_EPLACEMENT /
+    ATTN_ETIMEOUT (RuntimeError, after ``on_attention_error`` has run)."""
+
+    def __init__(self, device, message, on_attention_error=None):
         self.message = message
+        self.on_attention_error = on_attention_error
         self.flag = torch.zeros(1, dtype=torch.int32, device=device)
         self.host = torch.zeros(1, dtype=torch.int32,
                                 pin_memory=device.type == "cuda")
@@ -240,10 +245,22 @@ class _ErrorWord:
             elif not self.event.query():
                 return
         self.pending = False
-        if int(self.host[0]) != 0:
+        value = int(self.host[0])
+        if value != 0:
             self.flag.zero_()
             self.host.zero_()
+            if value & ~1:
+                if self.on_attention_error is not None:
+                    self.on_attention_error()
+                raise RuntimeError(_attention_error_message(value))
             raise IndexError(self.message)
+
+
+def _attention_error_message(value):
+    if value & _hip.ATTN_EPLACEMENT:
+        return ("fused decode attention: the device did not deal the "
+                "workgroups evenly over 8 XCDs")
+    return "fused decode attention: a split-merge wait ran out"
 
 
 class Llama31DecodeExecutor:
@@ -317,6 +334,8 @@ class Llama31DecodeExecutor:
         self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
         self._k_qkv_at = lib.cascade_qkv_rope_at_bf16
         self._k_attn_at = lib.cascade_decode_attention_at_bf16
+        self._k_attn_fused = lib.cascade_decode_attention_fused_bf16
+        self._k_attn_fused_at = lib.cascade_decode_attention_fused_at_bf16
         self._k_step_begin = lib.cascade_decode_step_begin_bf16
         # Set by DecodeGraph (layer_streaming/graph.py): decode steps take
         # their position from a device word instead of host values.
@@ -333,8 +352,14 @@ class Llama31DecodeExecutor:
         self._attn_ws = None
         self._attn_ws_len = 0
         self._head_ws = None
+        # decode attention merges its splits inside the attention launch
+        # where the shape allows (one KV head per XCD, >= 8 splits); its
+        # counters live in this zero-filled buffer, reset after an error
+        self._fused_attention = self.n_kv_heads == _hip.FUSED_ATTENTION_KV_HEADS
+        self._attn_sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8,
+                                      device=self.device)
         self._id_errors = _ErrorWord(self.device, "token id outside [0, {})".format(
-            config.vocab_size))
+            config.vocab_size), on_attention_error=self._attn_sync.zero_)
         self._ensure_buffers(1)
 
     # ------------------------------------------------------------ buffers
@@ -531,24 +556,45 @@ class Llama31DecodeExecutor:
         stride = self.kv_cache.head_stride
         ws, ws_bytes = self._attn_ws.data_ptr(), self._attn_ws.numel()
         step = self._device_step
+        sync = self._attn_sync.data_ptr()
+        min_len = _hip.FUSED_ATTENTION_MIN_LEN
         for t, slot in enumerate(self._slots(state)):
             ev = self._mark_begin("attention")
             if step is not None:
-                rc = self._k_attn_at(
-                    self._q_ptr, k0, v0, stride, step.length.data_ptr(),
-                    step.capacity, self.n_heads, self.n_kv_heads, self.head_dim,
-                    self.scale, self._attn_ptr, ws, ws_bytes, stream)
+                if self._fused_attention and step.capacity >= min_len:
+                    name = "cascade_decode_attention_fused_at_bf16"
+                    rc = self._k_attn_fused_at(
+                        self._q_ptr, k0, v0, stride, step.length.data_ptr(),
+                        step.capacity, self.n_heads, self.n_kv_heads,
+                        self.head_dim, self.scale, self._attn_ptr, ws, ws_bytes,
+                        sync, step.error.data_ptr(), stream)
+                else:
+                    name = "cascade_decode_attention_at_bf16"
+                    rc = self._k_attn_at(
+                        self._q_ptr, k0, v0, stride, step.length.data_ptr(),
+                        step.capacity, self.n_heads, self.n_kv_heads,
+                        self.head_dim, self.scale, self._attn_ptr, ws, ws_bytes,
+                        stream)
                 self._mark_end("attention", ev, rc)
-                _hip.check("cascade_decode_attention_at_bf16", rc)
+                _hip.check(name, rc)
                 if with_o:
                     self._o_residual(ptrs, state, t, stream)
                 continue
-            rc = self._k_attn(self._q_ptr + t * row, k0, v0, stride, slot + 1,
-                              self.n_heads, self.n_kv_heads, self.head_dim,
-                              self.scale, self._attn_ptr + t * row, ws, ws_bytes,
-                              stream)
+            if self._fused_attention and slot + 1 >= min_len:
+                name = "cascade_decode_attention_fused_bf16"
+                rc = self._k_attn_fused(
+                    self._q_ptr + t * row, k0, v0, stride, slot + 1, self.n_heads,
+                    self.n_kv_heads, self.head_dim, self.scale,
+                    self._attn_ptr + t * row, ws, ws_bytes, sync,
+                    self._id_errors.flag.data_ptr(), stream)
+            else:
+                name = "cascade_decode_attention_bf16"
+                rc = self._k_attn(self._q_ptr + t * row, k0, v0, stride, slot + 1,
+                                  self.n_heads, self.n_kv_heads, self.head_dim,
+                                  self.scale, self._attn_ptr + t * row, ws,
+                                  ws_bytes, stream)
             self._mark_end("attention", ev, rc)
-            _hip.check("cascade_decode_attention_bf16", rc)
+            _hip.check(name, rc)
             if with_o:
                 self._o_residual(ptrs, state, t, stream)
         self.kv_cache.set_length(layer, self._first_slot + len(state.positions))
@@ -814,6 +860,9 @@ class Llama31DecodeExecutor:
         stream = self._stream()
         final_norm = self.resident["model.norm.weight"]
         if self.vocab_runtime is not None:
+            # the flag carries only the fused attention's bits here (the
+            # streamed embedding checks ids on the host)
+            self._id_errors.raise_if_set()
             last = self._normed[:1]
             _hip.rmsnorm(rows[count - 1 :], final_norm, last, self.eps)
             result = self.vocab_runtime.lm_head_topk(
@@ -824,6 +873,7 @@ class Llama31DecodeExecutor:
             state.topk_values = result["values"]
             state.topk_indices = result["indices"]
             state.logits = result["logits"]
+            self._id_errors.publish()
             return state
         step = self._device_step
         if step is None:

@@ -33,8 +33,9 @@ extern "C" {
 #endif
 
 /* 2: cascade_hbm_read takes a workgroup count; the one-launch decoder layer
-   exports are gone. */
-#define CASCADE_ABI_VERSION 2
+   exports are gone.  3: cascade_decode_attention_fused_bf16 /
+   _fused_at_bf16 added. */
+#define CASCADE_ABI_VERSION 3
 
 /* Argument errors (no work enqueued). */
 #define CASCADE_EINVAL 1001     /* null pointer, bad size or count */
@@ -164,6 +165,40 @@ int cascade_decode_attention_at_bf16(const void *q, const void *k_cache,
                                      int64_t head_dim, float scale, void *out,
                                      void *workspace, size_t workspace_bytes,
                                      void *stream);
+
+/* The two forms above with the split merge inside the attention launch: one
+ * launch instead of two, results bit-identical to theirs.  The splits of KV
+ * head g all run on XCD g (a workgroup serves the head numbered by the XCC
+ * id it runs on; workgroups are dealt round-robin over the XCDs), and the
+ * last of them to finish merge the head's outputs through that XCD's L2.  Needs
+ * n_kv_heads == 8 (one KV head per XCD of an MI355X) and at least 8 splits
+ * (len > 224; the _at form: capacity > 224); other shapes return
+ * CASCADE_ESHAPE.  sync: CASCADE_DECODE_ATTENTION_SYNC_BYTES of device
+ * memory, zero-filled once by the caller and left zeroed by every call that
+ * completes; calls sharing one sync buffer must not overlap.  error_flag: a
+ * device int32 into which the launch ors CASCADE_ATTN_EPLACEMENT (the
+ * device did not deal the workgroups evenly over 8 XCDs) or
+ * CASCADE_ATTN_ETIMEOUT (a merge wait ran out); after either, the outputs
+ * are invalid and sync must be zero-filled again.  Workspace as for the
+ * forms above.
+ * Replaces the same reference code (llama31.py:213-234).                   */
+#define CASCADE_DECODE_ATTENTION_SYNC_BYTES 1024
+#define CASCADE_ATTN_EPLACEMENT 2
+#define CASCADE_ATTN_ETIMEOUT 4
+int cascade_decode_attention_fused_bf16(const void *q, const void *k_cache,
+                                        const void *v_cache,
+                                        int64_t kv_head_stride, int64_t len,
+                                        int64_t n_q_heads, int64_t n_kv_heads,
+                                        int64_t head_dim, float scale,
+                                        void *out, void *workspace,
+                                        size_t workspace_bytes, void *sync,
+                                        int32_t *error_flag, void *stream);
+int cascade_decode_attention_fused_at_bf16(
+    const void *q, const void *k_cache, const void *v_cache,
+    int64_t kv_head_stride, const int64_t *length, int64_t capacity,
+    int64_t n_q_heads, int64_t n_kv_heads, int64_t head_dim, float scale,
+    void *out, void *workspace, size_t workspace_bytes, void *sync,
+    int32_t *error_flag, void *stream);
 
 /* The same computation as cascade_decode_attention_bf16 with no workspace
  * argument and no allocation of any kind: the split partials live in a

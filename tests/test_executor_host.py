@@ -491,3 +491,29 @@ def test_begin_rejects_token_ids_outside_the_vocabulary(monkeypatch, weights,
             executor.begin(torch.tensor(bad))
     assert fakes.calls == []
     executor.begin(torch.tensor([[128255]]))  # the last valid id
+
+
+def test_error_word_bits_name_their_cause():
+    # 1 (the embedding gather's id check) raises IndexError; the fused
+    # attention's bits raise RuntimeError after the reset hook has run
+    from layer_streaming.llama31 import _ErrorWord
+
+    resets = []
+    word = _ErrorWord(torch.device("cpu"), "token id outside [0, 10)",
+                      on_attention_error=lambda: resets.append(1))
+    word.raise_if_set()  # nothing published yet
+    word.publish()
+    word.raise_if_set()  # published zero
+    word.flag.fill_(1)
+    word.publish()
+    with pytest.raises(IndexError):
+        word.raise_if_set()
+    assert resets == [] and int(word.flag[0]) == 0
+    for bit in (_hip.ATTN_EPLACEMENT, _hip.ATTN_ETIMEOUT,
+                _hip.ATTN_EPLACEMENT | 1):
+        word.flag.fill_(bit)
+        word.publish()
+        with pytest.raises(RuntimeError, match="fused decode attention"):
+            word.raise_if_set()
+        assert int(word.flag[0]) == 0
+    assert resets == [1, 1, 1]

@@ -168,6 +168,123 @@ def test_decode_attention_matches_oracle(gpu_device, length, q_scale):
     assert torch.equal(out.cpu(), out2.cpu())
 
 
+def _attention_inputs(dev, length, capacity, q_scale, seed=71):
+    dim = 128
+    q = cases.normal_bf16((32 * dim,), seed)
+    if q_scale != 1:
+        q = (q.float() * q_scale).to(BF16)
+    kc = torch.zeros((8, capacity, dim), dtype=BF16, device=dev)
+    vc = torch.zeros_like(kc)
+    kc[:, :length].copy_(cases.normal_bf16((8, length, dim), seed + 1).to(dev))
+    vc[:, :length].copy_(cases.normal_bf16((8, length, dim), seed + 2).to(dev))
+    return q.to(dev), kc, vc
+
+
+@pytest.mark.parametrize("length,q_scale", [
+    (225, 1), (256, 1), (300, 1), (2048, 1), (2049, 1), (32769, 1), (34000, 1),
+    (4097, 8), (32769, 8)])
+def test_fused_decode_attention_equals_two_launch_form(gpu_device, length, q_scale):
+    # the split merge inside the attention launch reproduces the merge
+    # launch's arithmetic: bit-identical outputs, counters back at zero
+    print("fused attention length={} q_scale={}".format(length, q_scale), flush=True)
+    dev = gpu_device
+    capacity = length + 5
+    q, kc, vc = _attention_inputs(dev, length, capacity, q_scale)
+    stride = capacity * 128
+    ws = torch.zeros(_hip.attention_workspace_bytes(length), dtype=torch.uint8,
+                     device=dev)
+    sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    scale = 128 ** -0.5
+    expected = torch.empty(32 * 128, dtype=BF16, device=dev)
+    _hip.decode_attention(q, kc.view(-1), vc.view(-1), stride, length, expected,
+                          ws, scale)
+    for _ in range(2):  # a second call finds the counters it left at zero
+        out = torch.empty_like(expected)
+        _hip.decode_attention_fused(q, kc.view(-1), vc.view(-1), stride, length,
+                                    out, ws, sync, err, scale)
+        assert torch.equal(out.cpu(), expected.cpu())
+        assert int(err.item()) == 0
+        assert int(sync.count_nonzero().item()) == 0
+
+
+@pytest.mark.parametrize("length_word", [1, 5, 224, 225, 4097, 33000])
+def test_fused_decode_attention_at_equals_two_launch_form(gpu_device, length_word):
+    print("fused attention at length word {}".format(length_word), flush=True)
+    dev = gpu_device
+    capacity = 33000
+    q, kc, vc = _attention_inputs(dev, capacity, capacity, 1, seed=81)
+    stride = capacity * 128
+    ws = torch.zeros(_hip.attention_workspace_bytes(capacity), dtype=torch.uint8,
+                     device=dev)
+    sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    length = torch.tensor([length_word], dtype=torch.int64, device=dev)
+    scale = 128 ** -0.5
+    expected = torch.empty(32 * 128, dtype=BF16, device=dev)
+    out = torch.empty_like(expected)
+    _hip.decode_attention_at(q, kc.view(-1), vc.view(-1), stride, length, capacity,
+                             expected, ws, scale)
+    _hip.decode_attention_fused_at(q, kc.view(-1), vc.view(-1), stride, length,
+                                   capacity, out, ws, sync, err, scale)
+    assert torch.equal(out.cpu(), expected.cpu())
+    assert int(err.item()) == 0
+    assert int(sync.count_nonzero().item()) == 0
+
+
+def test_fused_decode_attention_flags_a_counter_left_set(gpu_device):
+    # A counter left at 1 (a phantom arrival: the state an interrupted call
+    # could leave) gives one ticket past the split count; the launch flags
+    # it instead of merging silently, every workgroup exits, and once the
+    # caller zero-fills the sync buffer the next call is exact again.
+    dev = gpu_device
+    length = 4097
+    q, kc, vc = _attention_inputs(dev, length, length, 1, seed=91)
+    stride = length * 128
+    ws = torch.zeros(_hip.attention_workspace_bytes(length), dtype=torch.uint8,
+                     device=dev)
+    sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    scale = 128 ** -0.5
+    expected = torch.empty(32 * 128, dtype=BF16, device=dev)
+    _hip.decode_attention(q, kc.view(-1), vc.view(-1), stride, length, expected,
+                          ws, scale)
+    sync.view(torch.int32)[0] = 1  # KV head 0's arrival counter
+    out = torch.empty_like(expected)
+    _hip.decode_attention_fused(q, kc.view(-1), vc.view(-1), stride, length, out,
+                                ws, sync, err, scale)
+    torch.cuda.synchronize(dev)
+    assert int(err.item()) & _hip.ATTN_EPLACEMENT
+    sync.zero_()
+    err.zero_()
+    _hip.decode_attention_fused(q, kc.view(-1), vc.view(-1), stride, length, out,
+                                ws, sync, err, scale)
+    assert torch.equal(out.cpu(), expected.cpu())
+    assert int(err.item()) == 0
+
+
+def test_fused_decode_attention_rejects_unsupported_shapes(gpu_device):
+    dev = gpu_device
+    q, kc, vc = _attention_inputs(dev, 300, 300, 1)
+    ws = torch.zeros(_hip.attention_workspace_bytes(300), dtype=torch.uint8, device=dev)
+    sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.empty(32 * 128, dtype=BF16, device=dev)
+    with pytest.raises(ValueError):  # 7 splits: fewer than one per merger
+        _hip.decode_attention_fused(q, kc.view(-1), vc.view(-1), 300 * 128, 224, out,
+                                    ws, sync, err, 0.1)
+    # the C entry point refuses the same call with nothing launched
+    lib = _hip.load()
+    rc = lib.cascade_decode_attention_fused_bf16(
+        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), 300 * 128, 224, 32, 8, 128, 0.1,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), sync.data_ptr(), err.data_ptr(), None)
+    assert rc == _hip.ESHAPE
+    with pytest.raises(ValueError):  # a sync buffer short of one line per head
+        _hip.decode_attention_fused(q, kc.view(-1), vc.view(-1), 300 * 128, 300, out,
+                                    ws, sync[:512], err, 0.1)
+    assert int(sync.count_nonzero().item()) == 0 and int(err.item()) == 0
+
+
 def test_attention_single_position_is_value_row(gpu_device):
     # softmax over one position is 1: the output is V itself (bit-exact)
     dev = gpu_device
