@@ -345,7 +345,7 @@ def resident_decode(args):
             graph = {
                 "ms_per_step": round(g_elapsed * 1000.0 / args.steps, 4),
                 "tokens": args.steps,
-                "launches_per_step": "one graph replay (197 kernel nodes)",
+                "launches_per_step": "one graph replay (165 kernel nodes)",
                 "last_token": int(decoder.tokens()[0, -1]),
             }
             decoder.close()
@@ -845,7 +845,7 @@ def config2_layer(args, past=2048, repeats=20):
             "frac_of_peak": round(kernel_bytes[group] / (avg_us * 1e-6) / 1e9
                                   / HBM_PEAK_GBPS, 4),
         }
-    kernels["attention"]["timing"] = ("main + split-merge launches between "
+    kernels["attention"]["timing"] = ("one launch, split merge inside, between "
                                       "stream events (dispatch included)")
     layer_bytes = (436207616 + 2 * HIDDEN * 2 + 2 * mean_attended * 8 * 128 * 2
                    + 8 * 128 * 2 * 2)
@@ -1214,7 +1214,7 @@ def main():
                         "context {}".format(args.context),
             "context": args.context,
             "units": "matrix_group",
-            "layer_launches": "6 per-stage kernels",
+            "layer_launches": "5 per layer: q|k|v, attention (split merge inside), o_proj, gate/up, down",
             "batch": 1,
             "layers": LAYERS,
             "vocab": VOCAB,
