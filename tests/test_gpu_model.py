@@ -271,6 +271,57 @@ def test_out_of_vocabulary_ids_raise(gpu_device, source_store):
     store.close()
 
 
+def test_fused_attention_error_raises_and_resets(gpu_device, source_store):
+    # Past 224 positions the executor's decode attention merges its splits
+    # inside the attention launch, with counters in executor._attn_sync.  A
+    # counter left set (here planted: one phantom arrival on KV head 0) is
+    # flagged by the kernel into the step's error word; check_errors raises
+    # RuntimeError and zero-fills the counters, after which the fused
+    # attention is exact again.
+    from layer_streaming import _hip
+
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    store = create_weight_store(plan, "full_pinned")
+    copy_weights(source_store, store)
+    resident = ResidentDeviceArena(plan, store, gpu_device)
+    runtime = ResidentTransformerRuntime(plan, store, resident, gpu_device)
+    executor = Llama31DecodeExecutor(Llama31Config(num_hidden_layers=LAYERS),
+                                     resident, top_k=TOP_K)
+    prompt = torch.tensor([[(7919 * i + 11) % 128000 for i in range(240)]],
+                          device=gpu_device)
+    with torch.inference_mode():
+        state = executor.finish(runtime.run(executor, executor.begin(prompt)))
+        token = state.topk_indices.reshape(1, -1)[:, :1].clone()
+        state = executor.finish(runtime.run(executor, executor.begin(token)))
+        executor.check_errors()  # a clean fused step
+        executor._attn_sync.view(torch.int32)[0] = 1
+        token = state.topk_indices.reshape(1, -1)[:, :1].clone()
+        executor.finish(runtime.run(executor, executor.begin(token)))
+        with pytest.raises(RuntimeError, match="fused decode attention"):
+            executor.check_errors()
+        torch.cuda.synchronize(gpu_device)
+        assert int(executor._attn_sync.count_nonzero().item()) == 0
+        executor.check_errors()  # the flag was cleared
+        # the reset counters serve the kernel exactly again
+        length = 300
+        kc = torch.randn((8, length, 128), device=gpu_device).to(torch.bfloat16)
+        vc = torch.randn_like(kc)
+        q = torch.randn(4096, device=gpu_device).to(torch.bfloat16)
+        ws = torch.zeros(_hip.attention_workspace_bytes(length), dtype=torch.uint8,
+                         device=gpu_device)
+        expected = torch.empty_like(q)
+        out = torch.empty_like(q)
+        _hip.decode_attention(q, kc.view(-1), vc.view(-1), length * 128, length,
+                              expected, ws, 128 ** -0.5)
+        _hip.decode_attention_fused(q, kc.view(-1), vc.view(-1), length * 128, length,
+                                    out, ws, executor._attn_sync,
+                                    executor._id_errors.flag, 128 ** -0.5)
+        assert torch.equal(out.cpu(), expected.cpu())
+        executor._id_errors.publish()
+        executor.check_errors()
+    store.close()
+
+
 def test_refilled_store_is_copied_again(gpu_device):
     # The runtime copies the next call's first units ahead (full_pinned).
     # Refilling the store between calls, without discard_slots(), must make
