@@ -37,10 +37,11 @@
 // cannot tell which ring buffer such a load writes, adds no waits of its
 // own.  Slab s lives in ring buffer s % STAGES.  Step s waits (explicit
 // vmcnt) for this wave's loads of slab s + 1 only, one barrier publishes
-// slab s + 1 and frees slab s's buffer, slab s + STAGES goes out into it,
-// and slab s + 1's fragments are read into registers while slab s's MFMAs
-// run from the registers filled one step earlier, so the MFMAs never wait
-// on an LDS read.
+// slab s + 1 and frees slab s's buffer, the first MFMAs of slab s issue,
+// slab s + STAGES goes out into the freed buffer, and slab s + 1's
+// fragments are read into registers while slab s's other MFMAs run from
+// the registers filled one step earlier, so the MFMAs never wait on an LDS
+// read and the matrix core restarts right after the barrier.
 //
 // LDS layout of a slab: 128-byte rows (64 bf16) back to back; 16-byte
 // chunk c of row r sits at chunk c ^ ((r / 2) % 8) (32-deep slabs: 64-byte
@@ -607,6 +608,9 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   constexpr int kReads = KS * (T::FM + T::FN);
   constexpr int kMfmas = KS * T::FM * T::FN;
   static_assert(kMfmas >= kReads, "one MFMA ahead of every fragment read");
+  // MFMAs issued between the barrier and the slab loads (at most 8, and
+  // leaving one MFMA for every fragment read after the loads)
+  constexpr int kLead = kMfmas - kReads < 8 ? kMfmas - kReads : 8;
   using FragA = u32x4[KS][T::FM];
   using FragB = u32x4[KS][T::FN];
   auto read_frags = [&](int buf, FragA &fa, FragB &fb) {
@@ -635,23 +639,30 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   auto step = [&](int s, const FragA &fa, const FragB &fb, FragA &na, FragB &nb) {
     const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
     publish_step();
+    // the first kLead MFMAs of slab s go out right after the barrier, ahead
+    // of the slab loads, so the matrix core restarts at once (q/o_proj at
+    // M = 2048 64.5 -> 60.9 us, down_proj 197.4 -> 190.6 us, same bits)
+#pragma unroll
+    for (int idx = 0; idx < kLead; ++idx) {
+      const int ks = idx / (T::FM * T::FN), i = (idx / T::FN) % T::FM, j = idx % T::FN;
+      acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     ring_load(min(s + STAGES, slabs - 1), cur);
     __builtin_amdgcn_sched_barrier(0);
     read_frags(nxt, na, nb);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < T::FN; ++j)
-          acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
+    for (int idx = kLead; idx < kMfmas; ++idx) {
+      const int ks = idx / (T::FM * T::FN), i = (idx / T::FN) % T::FM, j = idx % T::FN;
+      acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
+    }
     // MFMA, read, MFMA, read, ..., then the remaining MFMAs
 #pragma unroll
     for (int r = 0; r < kReads; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kReads, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kLead - kReads, 0);
     __builtin_amdgcn_sched_barrier(0);
     cur = nxt;
   };
