@@ -11,8 +11,9 @@ Operation -> kernels (reference lines in parentheses):
   qkv / q_proj / k_proj / v_proj   cascade_qkv_rope_bf16: input RMSNorm,
       the projection(s), RoPE and the KV-cache write in one launch per
       token (:169-180, :206-218, :241-245)
-  o_proj     cascade_decode_attention_bf16 then cascade_gemv_residual_bf16
-      (:182-234, :246-251)
+  o_proj     cascade_decode_attention_fused_bf16 (split merge inside the
+      launch; cascade_decode_attention_bf16 below 225 positions) then
+      cascade_gemv_residual_bf16 (:182-234, :246-251)
   gate_up    cascade_gate_up_swiglu_bf16 (post-attention RMSNorm, both
       projections, SiLU and the product; :252-275)
   gate_proj / up_proj   cascade_gate_silu_bf16 / cascade_up_mul_bf16
@@ -217,7 +218,8 @@ class _ErrorWord:
 
     The embedding gather stores 1 for an id outside the vocabulary
     (IndexError); the fused decode attention ors in _hip.ATTN_EPLACEMENT /
-    ATTN_ETIMEOUT (RuntimeError, after ``on_attention_error`` has run)."""
+    ATTN_ETIMEOUT (RuntimeError, after ``on_attention_error(value)`` has
+    run)."""
 
     def __init__(self, device, message, on_attention_error=None):
         self.message = message
@@ -251,7 +253,7 @@ class _ErrorWord:
             self.host.zero_()
             if value & ~1:
                 if self.on_attention_error is not None:
-                    self.on_attention_error()
+                    self.on_attention_error(value)
                 raise RuntimeError(_attention_error_message(value))
             raise IndexError(self.message)
 
@@ -359,8 +361,18 @@ class Llama31DecodeExecutor:
         self._attn_sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8,
                                       device=self.device)
         self._id_errors = _ErrorWord(self.device, "token id outside [0, {})".format(
-            config.vocab_size), on_attention_error=self._attn_sync.zero_)
+            config.vocab_size), on_attention_error=self._attention_failed)
         self._ensure_buffers(1)
+
+    def _attention_failed(self, value):
+        """The fused attention flagged ``value``: its counters are zero-filled
+        for the next call, and a device that does not deal workgroups evenly
+        over 8 XCDs (another partition mode or part) gets the two-launch
+        attention from then on."""
+
+        self._attn_sync.zero_()
+        if value & _hip.ATTN_EPLACEMENT:
+            self._fused_attention = False
 
     # ------------------------------------------------------------ buffers
 

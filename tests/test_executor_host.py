@@ -500,7 +500,7 @@ def test_error_word_bits_name_their_cause():
 
     resets = []
     word = _ErrorWord(torch.device("cpu"), "token id outside [0, 10)",
-                      on_attention_error=lambda: resets.append(1))
+                      on_attention_error=resets.append)
     word.raise_if_set()  # nothing published yet
     word.publish()
     word.raise_if_set()  # published zero
@@ -516,4 +516,5 @@ def test_error_word_bits_name_their_cause():
         with pytest.raises(RuntimeError, match="fused decode attention"):
             word.raise_if_set()
         assert int(word.flag[0]) == 0
-    assert resets == [1, 1, 1]
+    assert resets == [_hip.ATTN_EPLACEMENT, _hip.ATTN_ETIMEOUT,
+                      _hip.ATTN_EPLACEMENT | 1]

@@ -276,8 +276,9 @@ def test_fused_attention_error_raises_and_resets(gpu_device, source_store):
     # inside the attention launch, with counters in executor._attn_sync.  A
     # counter left set (here planted: one phantom arrival on KV head 0) is
     # flagged by the kernel into the step's error word; check_errors raises
-    # RuntimeError and zero-fills the counters, after which the fused
-    # attention is exact again.
+    # RuntimeError, zero-fills the counters and switches the executor to the
+    # two-launch attention; the zero-filled counters serve the fused kernel
+    # exactly again.
     from layer_streaming import _hip
 
     plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
@@ -301,6 +302,9 @@ def test_fused_attention_error_raises_and_resets(gpu_device, source_store):
             executor.check_errors()
         torch.cuda.synchronize(gpu_device)
         assert int(executor._attn_sync.count_nonzero().item()) == 0
+        # a ticket past the split count reads as uneven XCD dealing: the
+        # executor keeps to the two-launch attention from then on
+        assert not executor._fused_attention
         executor.check_errors()  # the flag was cleared
         # the reset counters serve the kernel exactly again
         length = 300
