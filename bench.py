@@ -453,6 +453,75 @@ SWEEP_ROWS = (16, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768)
 LAYER_MACS = (HIDDEN + 2 * 1024 + HIDDEN + 3 * INTER) * HIDDEN  # 218,103,808
 
 
+# Prefill projection shapes at M = 2048 (N, K): the per-matrix units of
+# config 5 and the fused units of the resident prefill.
+VENDOR_SHAPES = (
+    ("q_proj / o_proj", HIDDEN, HIDDEN),
+    ("k_proj / v_proj", 1024, HIDDEN),
+    ("gate_proj / up_proj", INTER, HIDDEN),
+    ("down_proj", HIDDEN, INTER),
+    ("q|k|v fused", HIDDEN + 2 * 1024, HIDDEN),
+    ("gate|up fused", 2 * INTER, HIDDEN),
+)
+
+
+def prefill_vs_vendor(m=2048, copies=4, rounds=6, per_round=4):
+    """Each prefill projection shape at M = 2048: this library's bf16 GEMM
+    (cascade_gemm_bf16, the tile schedule the fused epilogues use) against
+    torch's F.linear (hipBLASLt on this image), both on cold weights (weight
+    copies rotating over >= 512 MiB, twice the 256 MB MALL),
+    alternating rounds, each launch between stream events; medians."""
+    import torch
+    import torch.nn.functional as F
+    from layer_streaming import _hip
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(11)
+    x = (torch.randn((m, INTER), device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    out = {}
+    for name, n, k in VENDOR_SHAPES:
+        ncopy = max(copies, -(-(512 << 20) // (n * k * 2)))
+        ws = [(torch.randn((n, k), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+              for _ in range(ncopy)]
+        xk = x[:, :k].contiguous()
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        times = {"ours": [], "vendor": []}
+        idx = 0
+        for _ in range(rounds):
+            for who in ("ours", "vendor"):
+                for _ in range(per_round):
+                    w = ws[idx % ncopy]
+                    idx += 1
+                    start = torch.cuda.Event(enable_timing=True)
+                    stop = torch.cuda.Event(enable_timing=True)
+                    start.record()
+                    if who == "ours":
+                        _hip.gemm(xk, w, y)
+                    else:
+                        F.linear(xk, w)
+                    stop.record()
+                    times[who].append((start, stop))
+        torch.cuda.synchronize(dev)
+        flops = 2.0 * m * n * k
+        row = {"m_n_k": [m, n, k], "weight_copies": ncopy}
+        for who, evs in times.items():
+            us = statistics.median(a.elapsed_time(b) * 1000.0 for a, b in evs)
+            row[who + "_us"] = round(us, 1)
+            row[who + "_tflops"] = round(flops / (us * 1e-6) / 1e12, 1)
+        row["ours_over_vendor"] = round(row["ours_us"] / row["vendor_us"], 3)
+        out[name] = row
+        del ws, y
+    torch.cuda.empty_cache()
+    return {
+        "workload": "prefill projection GEMMs at M = 2048 rows, bf16 in / out, "
+                    "fp32 accumulation; this library's cascade_gemm_bf16 against "
+                    "torch F.linear (hipBLASLt), cold weights, stream events "
+                    "around each launch (dispatch included), medians of "
+                    "{} launches each".format(rounds * per_round),
+        "shapes": out,
+    }
+
+
 def prefill_sweep(args):
     """The copy/compute crossover of a streamed prefill, measured the way the
     reference measures it (an M sweep of one layer's projections,
@@ -1270,6 +1339,7 @@ def main():
     if not args.no_prefill:
         line["prefill"] = prefill_streamed(args)
         line["prefill_sweep"] = prefill_sweep(args)
+        line["prefill_vs_vendor"] = prefill_vs_vendor()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(line), flush=True)
