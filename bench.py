@@ -113,7 +113,8 @@ def counter_probe():
     its config-4 shape over 3 rotating operand copies (beyond the 256 MB
     MALL), 12 launches each, in this order: gate/up SwiGLU, q|k|v + RoPE,
     o_proj + residual, down_proj + residual, decode attention at L = 32769
-    (main kernel + split merge)."""
+    (main kernel + split merge, then the fused form that merges inside
+    the attention launch)."""
 
     import torch
     from layer_streaming import _hip
@@ -182,6 +183,17 @@ def counter_probe():
                               length, out, ws, 128 ** -0.5)
     torch.cuda.synchronize(dev)
     log("probe: 12 attention launches done")
+    sync = torch.zeros(_hip.ATTENTION_SYNC_BYTES, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    for i in range(12):
+        cache = kv[i % 3]
+        _hip.decode_attention_fused(q, cache[0].view(-1), cache[1].view(-1),
+                                    stride, length, out, ws, sync, err,
+                                    128 ** -0.5)
+    torch.cuda.synchronize(dev)
+    if int(err.item()) != 0:
+        raise RuntimeError("fused attention error word {}".format(int(err.item())))
+    log("probe: 12 fused attention launches done")
 
 
 def measured_traffic(path):
