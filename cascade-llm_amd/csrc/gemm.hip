@@ -38,10 +38,16 @@
 // own.  Slab s lives in ring buffer s % STAGES.  Step s waits (explicit
 // vmcnt) for this wave's loads of slab s + 1 only, one barrier publishes
 // slab s + 1 and frees slab s's buffer, the first MFMAs of slab s issue,
-// slab s + STAGES goes out into the freed buffer, and slab s + 1's
-// fragments are read into registers while slab s's other MFMAs run from
-// the registers filled one step earlier, so the MFMAs never wait on an LDS
-// read and the matrix core restarts right after the barrier.
+// and the rest of the step runs in chunks, one per load instruction of
+// slab s + STAGES (into the freed buffer): each chunk issues its load, then
+// its share of slab s's MFMAs interleaved with its share of slab s + 1's
+// fragment reads.  The MFMAs run from the registers filled one step
+// earlier, so they never wait on an LDS read; and the loads leave one at a
+// time over the step instead of all eight waves queueing theirs at the
+// CU's load path right after the barrier, where a wave stuck behind its
+// own burst held up its MFMAs (M = 2048, rotating weights, same bits:
+// q/o_proj 61.3 -> 55.7 us, down_proj 190.5 -> 185.9, q|k|v-shaped
+// N = 6144 95.8 -> 85.2, fused gate|up 407.0 -> 395.1).
 //
 // LDS layout of a slab: 128-byte rows (64 bf16) back to back; 16-byte
 // chunk c of row r sits at chunk c ^ ((r / 2) % 8) (32-deep slabs: 64-byte
@@ -558,20 +564,19 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   // The whole byte offset goes in voffset: the buffer range check covers
   // voffset (not soffset), so rows past the end read as zeros instead of
   // leaving the allocation.  Offsets stay below 2^31 (checked on the host).
-  auto ring_load = [&](int slab, int buf) {
+  // Load instruction h (0 .. XW + WW - 1) of this wave for slab `slab`
+  // into ring buffer `buf`: X rows first, then W rows.
+  auto ring_load_one = [&](int slab, int buf, int h) __attribute__((always_inline)) {
     const uint32_t dx = ring_lds + static_cast<uint32_t>(buf * kSlab * 2);
     const uint32_t dw = dx + XB * 2;
     const int kb = slab * BK * 2;
-#pragma unroll
-    for (int h = 0; h < XW; ++h) {
+    if (h < XW) {
       const int i = wave * XW + h;
       const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
       dma_lds16(xw, ((i & 1) ? ld_off1 : ld_off0) + static_cast<int>(row * k_bytes) + kb,
                 dx + i * 1024);
-    }
-#pragma unroll
-    for (int h = 0; h < WW; ++h) {
-      const int i = wave * WW + h;
+    } else {
+      const int i = wave * WW + (h - XW);
       const int trow = L::RPI * i;  // tile row of the instruction
       // SwiGLU: sub-tile trow / 128 holds 64 gate rows, then their 64 up rows
       const int tt = trow % kTileN;
@@ -585,12 +590,17 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
                 dw + i * 1024);
     }
   };
+  auto ring_load = [&](int slab, int buf) {
+#pragma unroll
+    for (int h = 0; h < XW + WW; ++h) ring_load_one(slab, buf, h);
+  };
   // Slab j lives in ring buffer j % STAGES.  Step s (one per slab):
   //   wait for this wave's loads of slab s + 1 (the loads of the
   //   STAGES - 2 slabs after it may stay in flight) and for its LDS reads
   //   of slab s (lgkmcnt 0); one barrier publishes slab s + 1 and frees
   //   slab s's buffer;
-  //   slab s + STAGES goes out into that buffer;
+  //   slab s + STAGES goes out into that buffer, one load instruction at
+  //   the head of each of the step's D chunks;
   //   slab s + 1's fragments are read into registers while slab s's
   //   MFMAs, whose fragments were read one step earlier, run: the MFMA
   //   queue never waits on an LDS read.
@@ -607,25 +617,28 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   constexpr int KS = BK / 32;
   constexpr int kReads = KS * (T::FM + T::FN);
   constexpr int kMfmas = KS * T::FM * T::FN;
-  static_assert(kMfmas >= kReads, "one MFMA ahead of every fragment read");
-  // MFMAs issued between the barrier and the slab loads (at most 8, and
-  // leaving one MFMA for every fragment read after the loads)
-  constexpr int kLead = kMfmas - kReads < 8 ? kMfmas - kReads : 8;
+  // MFMAs issued right after the step barrier (at most 4, leaving one MFMA
+  // for every fragment read in the chunks after them)
+  constexpr int kLead = kMfmas - kReads < 4 ? kMfmas - kReads : 4;
+  constexpr int kRest = kMfmas - kLead;
+  // every chunk holds at least as many MFMAs as fragment reads
+  static_assert(kRest >= kReads && kRest / D >= (kReads + D - 1) / D,
+                "one MFMA ahead of every fragment read in each chunk");
   using FragA = u32x4[KS][T::FM];
   using FragB = u32x4[KS][T::FN];
-  auto read_frags = [&](int buf, FragA &fa, FragB &fb) {
+  // Fragment read r (0 .. kReads - 1) of slab buffer `buf`: for each
+  // 32-deep half ks of the slab, the FM A fragments, then the FN B ones.
+  auto read_frag = [&](int buf, int r, FragA &fa, FragB &fb) __attribute__((always_inline)) {
     const char *ax = reinterpret_cast<const char *>(sb0 + buf * kSlab) + arow0 * L::ROWB;
     const char *aw = reinterpret_cast<const char *>(sb0 + buf * kSlab + XB);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int off = ks ? rd_off1 : rd_off0;
-#pragma unroll
-      for (int i = 0; i < T::FM; ++i)
-        fa[ks][i] = *reinterpret_cast<const u32x4 *>(ax + off + 16 * i * L::ROWB);
-#pragma unroll
-      for (int j = 0; j < T::FN; ++j)
-        fb[ks][j] = *reinterpret_cast<const u32x4 *>(
-            aw + off + (kTileN * sub + gemm_col<T>(wn, j, lr) - lr) * L::ROWB);
+    const int ks = r / (T::FM + T::FN), q = r % (T::FM + T::FN);
+    const int off = ks ? rd_off1 : rd_off0;
+    if (q < T::FM) {
+      fa[ks][q] = *reinterpret_cast<const u32x4 *>(ax + off + 16 * q * L::ROWB);
+    } else {
+      const int j = q - T::FM;
+      fb[ks][j] = *reinterpret_cast<const u32x4 *>(
+          aw + off + (kTileN * sub + gemm_col<T>(wn, j, lr) - lr) * L::ROWB);
     }
   };
   // publish: every LDS read issued so far stays above the wait (the empty
@@ -639,31 +652,42 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   auto step = [&](int s, const FragA &fa, const FragB &fb, FragA &na, FragB &nb) {
     const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
     publish_step();
-    // the first kLead MFMAs of slab s go out right after the barrier, ahead
-    // of the slab loads, so the matrix core restarts at once (q/o_proj at
-    // M = 2048 64.5 -> 60.9 us, down_proj 197.4 -> 190.6 us, same bits)
+    // the first kLead MFMAs of slab s go out right after the barrier, so
+    // the matrix core restarts at once
 #pragma unroll
     for (int idx = 0; idx < kLead; ++idx) {
       const int ks = idx / (T::FM * T::FN), i = (idx / T::FN) % T::FM, j = idx % T::FN;
       acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    ring_load(min(s + STAGES, slabs - 1), cur);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(nxt, na, nb);
+    // the rest of the step in D chunks, each opening with one load
+    // instruction of slab s + STAGES, then its share of slab s's MFMAs
+    // interleaved with its share of slab s + 1's fragment reads
+    const int slab_next = min(s + STAGES, slabs - 1);
 #pragma unroll
-    for (int idx = kLead; idx < kMfmas; ++idx) {
-      const int ks = idx / (T::FM * T::FN), i = (idx / T::FN) % T::FM, j = idx % T::FN;
-      acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
-    }
-    // MFMA, read, MFMA, read, ..., then the remaining MFMAs
+    for (int c = 0; c < D; ++c) {
+      const int m0 = kLead + c * kRest / D, m1 = kLead + (c + 1) * kRest / D;
+      const int r0 = c * kReads / D, r1 = (c + 1) * kReads / D;
+      ring_load_one(slab_next, cur, c);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < kReads; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int idx = m0; idx < m1; ++idx) {
+        const int ks = idx / (T::FM * T::FN), i = (idx / T::FN) % T::FM, j = idx % T::FN;
+        acc[i][j] = mfma_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j]);
+      }
+#pragma unroll
+      for (int r = r0; r < r1; ++r) read_frag(nxt, r, na, nb);
+      // MFMA, read, MFMA, read, ..., then the chunk's remaining MFMAs
+#pragma unroll
+      for (int r = r0; r < r1; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < (m1 - m0) - (r1 - r0); ++k)
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kLead - kReads, 0);
-    __builtin_amdgcn_sched_barrier(0);
     cur = nxt;
   };
 #pragma unroll
@@ -672,7 +696,8 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   FragB fb0, fb1;
   __builtin_amdgcn_s_waitcnt(kWaitFirst);
   __builtin_amdgcn_s_barrier();
-  read_frags(0, fa0, fb0);
+#pragma unroll
+  for (int r = 0; r < kReads; ++r) read_frag(0, r, fa0, fb0);
   int s = 0;
   for (; s + 2 <= slabs; s += 2) {
     step(s, fa0, fb0, fa1, fb1);
