@@ -15,11 +15,11 @@
 // bytes a lane) from LDS.  Shapes (launch_gemm picks one):
 //   GemmTileWide 256 x 256 (two 128-column sub-tiles), 8 waves of 128 x 64,
 //                32-deep slabs on a ring of 4: where its schedule of rounds
-//                is shorter than GemmTile256's (the fused gate|up at
-//                M = 2048: 3 rounds, then a round of 128 x 256 half tiles);
+//                is shorter than GemmTile256's (the resident LM head over
+//                every prompt row at M = 2048: 16 rounds);
 //   GemmTile256  256 x 128, 8 waves, a ring of 3 slab buffers: the large
 //                GEMMs (at least as many 256-row tiles as CUs: q, o, gate,
-//                up, down at M = 2048);
+//                up, down and the fused gate|up at M = 2048);
 //   GemmTile128  128 x 128, 4 waves, a ring of 4;
 //   GemmTile64   64 x 128, 4 waves, a ring of 6: where 128-row tiles would
 //                leave CUs idle (the N = 1024 K / V projections at M = 2048,
@@ -1043,23 +1043,30 @@ static hipError_t launch_gemm(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
     return launch_skinny<EPI>(a, tiles_n, s);
   const int64_t tiles256 = (a.m + 255) / 256 * tiles_n;
   if (a.m > 128 && tiles256 >= cus) {
-    // 256 x 256 tiles read a quarter less X and W per MFMA: a round of them
-    // takes 0.91 of two rounds of 256 x 128 tiles (M = 2048, N = 8192:
-    // 137.6 -> 125.5 us), and their half-height tail tiles (128 x 256) as
-    // long as one round of 256 x 128.  They need 32-deep slabs (a ring of
-    // four 32 KiB slabs; 64-deep ones would not fit three in the LDS), and
-    // SwiGLU whole pairs of 128-column gate / up groups.  q|k|v keeps one
-    // head per tile.  M = 2048, gate|up (N = 2 x 14336): 7 rounds of 256 x
-    // 128 tiles against 3 rounds + a half-height round of 256 x 256.
+    // 256 x 256 tiles read a quarter less X and W per MFMA but need 32-deep
+    // slabs (a ring of four 32 KiB slabs; 64-deep ones would not fit three
+    // in the LDS), so twice the step barriers.  The schedule of rounds
+    // decides, with round costs measured at M = 2048, K = 4096 (in rounds
+    // of 256 x 128 tiles, about 58 us each): a round of 256 x 256 tiles
+    // 1.98 (N = 16384: 230 us for 2 rounds against 244 us for 4), a round of
+    // their 128 x 256 half-height tail tiles 1.2, a round of 128 x 128 tail
+    // tiles 0.7.  So the fused gate|up (N = 2 x 14336) runs 7 rounds of
+    // 256 x 128 tiles (405.8 us) rather than 3 rounds + a half-height round
+    // of 256 x 256 (414.5 us), and the resident LM head (N = 128256) 16
+    // rounds of 256 x 256 (1712 against 1784 us).  SwiGLU needs whole
+    // pairs of 128-column gate / up groups; q|k|v keeps one head per tile.
     if constexpr (EPI != kGemmQkvRope) {
       const int64_t tm256 = (a.m + 255) / 256, tm128 = (a.m + 127) / 128;
       const int64_t wide_n = (tiles_n + 1) / 2;
       const TileRounds std_r = tile_rounds(tm256, tiles_n, tm128, cus);
       const TileRounds wide_r = tile_rounds(tm256, wide_n, tm128, cus);
-      constexpr double kWideRound = 1.82;  // in rounds of 256 x 128 tiles
-      const double std_t = static_cast<double>(std_r.full) + 0.5 * std_r.tail;
+      constexpr double kWideRound = 1.98;  // in rounds of 256 x 128 tiles
+      constexpr double kWideHalfRound = 1.2;
+      constexpr double kHalfRound = 0.7;
+      const double std_t = static_cast<double>(std_r.full) +
+                           (std_r.tail == 1 ? kHalfRound : std_r.tail == 2 ? 1.0 : 0.0);
       const double wide_t = kWideRound * static_cast<double>(wide_r.full) +
-                            (wide_r.tail == 1 ? 1.0 : wide_r.tail == 2 ? kWideRound : 0.0);
+                            (wide_r.tail == 1 ? kWideHalfRound : wide_r.tail == 2 ? kWideRound : 0.0);
       if (wide_t < std_t && (EPI != kGemmSwiglu || tiles_n % 2 == 0))
         return launch_tiles<EPI, 32, GemmTileWide, 4, GemmTileWideHalf, 4>(a, wide_n, cus, s);
     }
