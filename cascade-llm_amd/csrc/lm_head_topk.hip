@@ -159,6 +159,28 @@ static hipError_t launch_topk(const TopkArgs &a, int keys, dim3 grid,
                               dim3(kTopkThreads), 0, s, a);
 }
 
+// Candidates then merge over logits[0..rows) (global index row_offset + r);
+// first: start a new running list instead of merging with the stored one.
+static int run_topk(const float *logits, int64_t rows, int64_t row_offset,
+                    int64_t top_k, bool first, const TopkShape &shape, char *ws,
+                    float *out_values, int64_t *out_indices, hipStream_t s) {
+  TopkArgs a{};
+  a.logits = logits;
+  a.rows = rows;
+  a.row_offset = row_offset;
+  a.top_k = static_cast<int>(top_k);
+  a.first = first ? 1 : 0;
+  a.span = shape.span;
+  a.nblocks = shape.nblocks;
+  a.running = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes);
+  a.cand = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes + kLmRunningBytes);
+  a.out_values = out_values;
+  a.out_indices = out_indices;
+  hipError_t e = launch_topk<true>(a, a.span, dim3(shape.nblocks), s);
+  if (e != hipSuccess) return e;
+  return launch_topk<false>(a, shape.nblocks * a.top_k + a.top_k, dim3(1), s);
+}
+
 static size_t lm_workspace(int64_t rows) {
   const size_t logits = ((static_cast<size_t>(rows) * 4 + 255) / 256) * 256;
   return kLmHeaderBytes + kLmRunningBytes + kLmCandBytes + logits;
@@ -205,19 +227,26 @@ extern "C" int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
   hipError_t e = launch_logits_gemv(static_cast<const uint16_t *>(w), rows, k,
                                     static_cast<const uint16_t *>(h), logits, s);
   if (e != hipSuccess) return e;
-  TopkArgs a{};
-  a.logits = logits;
-  a.rows = rows;
-  a.row_offset = row_offset;
-  a.top_k = static_cast<int>(top_k);
-  a.first = first_chunk ? 1 : 0;
-  a.span = shape.span;
-  a.nblocks = shape.nblocks;
-  a.running = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes);
-  a.cand = reinterpret_cast<uint64_t *>(ws + kLmHeaderBytes + kLmRunningBytes);
-  a.out_values = out_values;
-  a.out_indices = out_indices;
-  e = launch_topk<true>(a, a.span, dim3(shape.nblocks), s);
-  if (e != hipSuccess) return e;
-  return launch_topk<false>(a, shape.nblocks * a.top_k + a.top_k, dim3(1), s);
+  return run_topk(logits, rows, row_offset, top_k, first_chunk != 0, shape, ws,
+                  out_values, out_indices, s);
+}
+
+extern "C" int cascade_topk_f32(const float *logits, int64_t rows, int64_t top_k,
+                                void *workspace, size_t workspace_bytes,
+                                float *out_values, int64_t *out_indices,
+                                void *stream) {
+  if (logits == nullptr || workspace == nullptr || out_values == nullptr ||
+      out_indices == nullptr)
+    return CASCADE_EINVAL;
+  if (rows <= 0 || top_k < 1 || top_k > kLmMaxTopK) return CASCADE_EINVAL;
+  if (rows > 0xffffffffll) return CASCADE_ESHAPE;
+  if (!aligned16(workspace)) return CASCADE_EALIGN;
+  TopkShape shape;
+  if (!topk_shape(rows, top_k, &shape)) return CASCADE_ESHAPE;
+  if (workspace_bytes < lm_workspace(rows)) return CASCADE_EWORKSPACE;
+  // first = 1: the merge reads no running list, so the workspace needs no
+  // zero-fill
+  return run_topk(logits, rows, 0, top_k, true, shape,
+                  static_cast<char *>(workspace), out_values, out_indices,
+                  static_cast<hipStream_t>(stream));
 }

@@ -100,6 +100,7 @@ _SIGNATURES = {
         _INT,
         [_P, _I64, _I64, _I64, _P, _I64, _INT, _P, _P, _SZ, _P, _P, _P],
     ),
+    "cascade_topk_f32": (_INT, [_P, _I64, _I64, _P, _SZ, _P, _P, _P]),
     "cascade_embedding_gather_bf16": (
         _INT, [_P, _I64, _I64, _P, _I64, _P, _P, _P]),
     "cascade_decode_step_begin_bf16": (
@@ -124,7 +125,7 @@ _SIGNATURES = {
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 ESHAPE = 1003  # CASCADE_ESHAPE
 # fused decode attention: sync buffer size and the bits it ors into the
 # caller's error word (include/cascade_hip.h)
@@ -793,6 +794,21 @@ def lm_head_topk(weight, hidden, top_k, row_offset, first_chunk, workspace,
          int(row_offset), hidden.data_ptr(), int(top_k),
          1 if first_chunk else 0,
          0 if logits_out is None else logits_out.data_ptr(),
+         workspace.data_ptr(), workspace.numel(), out_values.data_ptr(),
+         out_indices.data_ptr(), stream_handle(stream))
+
+
+def topk_f32(logits, top_k, workspace, out_values, out_indices, stream=None):
+    """Exact top-k of one row of fp32 logits already on the device (value
+    descending, index ascending; lm_head_topk's order) into out_values /
+    out_indices.  workspace: lm_head_workspace_bytes(rows, top_k) bytes."""
+
+    require_device(logits, "logits", torch.float32)
+    rows = logits.numel()
+    require_device(workspace, "workspace", torch.uint8)
+    require_device(out_values, "out_values", torch.float32, top_k)
+    require_device(out_indices, "out_indices", torch.int64, top_k)
+    call("cascade_topk_f32", logits.data_ptr(), rows, int(top_k),
          workspace.data_ptr(), workspace.numel(), out_values.data_ptr(),
          out_indices.data_ptr(), stream_handle(stream))
 

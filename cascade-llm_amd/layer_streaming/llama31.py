@@ -334,6 +334,7 @@ class Llama31DecodeExecutor:
         self._k_silu_gemm = lib.cascade_gate_silu_gemm_bf16
         self._k_mul_gemm = lib.cascade_up_mul_gemm_bf16
         self._k_f32_gemm = lib.cascade_gemm_f32out_bf16
+        self._k_topk = lib.cascade_topk_f32
         self._k_qkv_at = lib.cascade_qkv_rope_at_bf16
         self._k_attn_at = lib.cascade_decode_attention_at_bf16
         self._k_attn_fused = lib.cascade_decode_attention_fused_bf16
@@ -624,12 +625,12 @@ class Llama31DecodeExecutor:
         """Time ``launches`` launches of kernel group ``name`` ("gate_up",
         "qkv", "attention", "o_proj", "down_proj", "lm_head"; at prefill
         "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_gate", "gemm_up",
-        "gemm_down", "gemm_lm_head", "prefill_attention"): of the group's
+        "gemm_down", "gemm_lm_head", "topk", "prefill_attention"): of the group's
         coming launches, numbers offset, offset + stride, ...; read them back
         with :meth:`kernel_times_ms` after a synchronize.  The one-kernel
         groups (gate_up, qkv, o_proj, down_proj) bind the events to the
-        kernel's own execution; attention (main + split merge) and lm_head
-        (GEMV + two top-k kernels) are bracketed by events recorded on the
+        kernel's own execution; attention, lm_head (GEMV + two top-k
+        kernels) and topk (two kernels) are bracketed by events recorded on the
         launching stream, which include dispatch time.  A timed launch costs
         a few microseconds of extra queue time (the timestamp packets), so a
         stride spreads a few samples over a long run."""
@@ -913,22 +914,26 @@ class Llama31DecodeExecutor:
             indices = torch.empty((1, 1, self.top_k), dtype=torch.int64,
                                   device=self.device)
         ws, ws_bytes = self._head_ws.data_ptr(), self._head_ws.numel()
-        first = 0
         if count > 1:
             # every position's logits in one GEMM (the reference's F.linear
-            # over [1, S, H]); the last row is recomputed below together
-            # with its top-k, so its logits and top-k agree bit for bit
+            # over [1, S, H]), then the top-k of the last row's logits
+            # (torch.topk(state.logits[:, -1:, :]), llama31.py:335-339)
             ev = self._mark_begin("gemm_lm_head")
             rc = self._k_f32_gemm(normed.data_ptr(), head_ptr, logits.data_ptr(),
                                   count, vocab, self.hidden, stream)
             self._mark_end("gemm_lm_head", ev, rc)
             _hip.check("cascade_gemm_f32out_bf16", rc)
-            first = count - 1
-        for s in range(first, count):
+            ev = self._mark_begin("topk")
+            rc = self._k_topk(logits.data_ptr() + 4 * vocab * (count - 1), vocab,
+                              self.top_k, ws, ws_bytes, values.data_ptr(),
+                              indices.data_ptr(), stream)
+            self._mark_end("topk", ev, rc)
+            _hip.check("cascade_topk_f32", rc)
+        else:
+            # one position: its logits and their top-k in one call
             ev = self._mark_begin("lm_head")
-            rc = self._k_head(head_ptr, vocab, self.hidden, 0,
-                              normed.data_ptr() + 2 * self.hidden * s, self.top_k,
-                              1, logits.data_ptr() + 4 * vocab * s, ws, ws_bytes,
+            rc = self._k_head(head_ptr, vocab, self.hidden, 0, normed.data_ptr(),
+                              self.top_k, 1, logits.data_ptr(), ws, ws_bytes,
                               values.data_ptr(), indices.data_ptr(), stream)
             self._mark_end("lm_head", ev, rc)
             _hip.check("cascade_lm_head_topk_bf16", rc)

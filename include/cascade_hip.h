@@ -34,8 +34,8 @@ extern "C" {
 
 /* 2: cascade_hbm_read takes a workgroup count; the one-launch decoder layer
    exports are gone.  3: cascade_decode_attention_fused_bf16 /
-   _fused_at_bf16 added. */
-#define CASCADE_ABI_VERSION 3
+   _fused_at_bf16 added.  4: cascade_topk_f32 added. */
+#define CASCADE_ABI_VERSION 4
 
 /* Argument errors (no work enqueued). */
 #define CASCADE_EINVAL 1001     /* null pointer, bad size or count */
@@ -305,6 +305,16 @@ int cascade_lm_head_topk_bf16(const void *w, int64_t rows, int64_t k,
                               void *workspace, size_t workspace_bytes,
                               float *out_values, int64_t *out_indices,
                               void *stream);
+/* The same exact top-k over a row of fp32 logits already in memory
+ * (logits[0..rows), indices 0..rows-1; same order, ties and NaN rule),
+ * with no running list: out_values / out_indices receive the row's top_k.
+ * The workspace is one of cascade_lm_head_workspace_bytes(rows, top_k)
+ * bytes (no zero-fill needed).  Replaces torch.topk(state.logits[:, -1:, :],
+ * k) of the resident finish after its F.linear over every position,
+ * layer_streaming/llama31.py:335-339.                                      */
+int cascade_topk_f32(const float *logits, int64_t rows, int64_t top_k,
+                     void *workspace, size_t workspace_bytes,
+                     float *out_values, int64_t *out_indices, void *stream);
 
 /* ----------------------------------------------------------- embedding
  * out[i, :] = table[ids[i], :] for i < n_ids (ids are int64 on the device).

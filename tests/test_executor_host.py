@@ -247,9 +247,19 @@ class FakeKernels:
         return 0
 
     def f32_gemm(self, x, w, y, m, n, k, stream):
+        # each row as the oracle's LM head computes it, so the last row's
+        # logits (and their top-k) match the oracle bit for bit
         self.calls.append("f32_gemm")
-        out = at(x, m * k).view(m, k).double() @ at(w, n * k).view(n, k).double().t()
-        at(y, m * n, torch.float32).copy_(out.float().reshape(-1))
+        xs, ws = at(x, m * k).view(m, k), at(w, n * k).view(n, k)
+        out = torch.stack([ref.lm_head_logits(xs[r], ws) for r in range(m)])
+        at(y, m * n, torch.float32).copy_(out.reshape(-1))
+        return 0
+
+    def topk(self, logits, rows, top_k, ws, ws_bytes, values, indices, stream):
+        self.calls.append("topk")
+        v, i = ref.topk(at(logits, rows, torch.float32), top_k)
+        at(values, top_k, torch.float32).copy_(v)
+        at(indices, top_k, torch.int64).copy_(i)
         return 0
 
 
@@ -312,7 +322,7 @@ def make_executor(monkeypatch, plan, store):
     ex._k_qkv_gemm, ex._k_prefill_attn = fakes.qkv_gemm, fakes.prefill_attention
     ex._k_gemm_residual, ex._k_swiglu_gemm = fakes.gemm_residual, fakes.swiglu_gemm
     ex._k_silu_gemm, ex._k_mul_gemm = fakes.silu_gemm, fakes.mul_gemm
-    ex._k_f32_gemm = fakes.f32_gemm
+    ex._k_f32_gemm, ex._k_topk = fakes.f32_gemm, fakes.topk
     ex._k_qkv_at, ex._k_attn_at = fakes.qkv_at, fakes.attention_at
     ex._k_step_begin = fakes.step_begin
     return ex, fakes
@@ -363,9 +373,11 @@ def test_executor_addressing_matches_oracle_bit_for_bit(monkeypatch, weights,
     per_prefill = {"matrix_group": 7, "matrix": 10, "layer": 7}[granularity]
     # decode, per layer and token: qkv launch(es), attention, o residual,
     # MLP, down; finish: one rmsnorm, then (prefill) one logits GEMM over
-    # every position and one LM-head launch for the last
+    # every position and the top-k of the last row's logits, (decode) one
+    # LM-head launch
     assert fakes.calls.count("prefill_attention") == LAYERS
     assert fakes.calls.count("f32_gemm") == 1
+    assert fakes.calls.count("topk") == 1
     expected = (LAYERS * per_prefill + 3) + 3 * (LAYERS * per_token + 2)
     assert len(fakes.calls) == expected
 

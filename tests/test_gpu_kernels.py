@@ -349,6 +349,33 @@ def test_lm_head_fewer_rows_than_top_k(gpu_device):
     assert bool(torch.isinf(values[5:]).all())
 
 
+@pytest.mark.parametrize("rows,top_k", [(128256, 10), (5, 10), (3000, 1),
+                                         (65536, 64)])
+def test_topk_f32_matches_oracle(gpu_device, rows, top_k):
+    # top-k of a row of logits already in memory (the resident finish after
+    # its GEMM over every position): exact ties, -0.0 / +0.0 and fewer rows
+    # than top_k; the workspace is left dirty (no zero-fill is needed)
+    g = torch.Generator().manual_seed(rows + top_k)
+    logits = torch.randn(rows, generator=g)
+    logits[::7] = logits[min(3, rows - 1)].item()
+    if rows > 8:
+        logits[1] = -0.0
+        logits[2] = 0.0
+    dev = gpu_device
+    ws = torch.full((_hip.lm_head_workspace_bytes(rows, top_k),), 0xAB,
+                    dtype=torch.uint8, device=dev)
+    values = torch.empty(top_k, dtype=torch.float32, device=dev)
+    indices = torch.empty(top_k, dtype=torch.int64, device=dev)
+    _hip.topk_f32(logits.to(dev), top_k, ws, values, indices)
+    n = min(rows, top_k)
+    ev, ei = ref.topk(logits, n)
+    assert torch.equal(indices[:n].cpu(), ei)
+    assert torch.equal(values[:n].cpu(), ev)
+    if n < top_k:
+        assert indices[n:].cpu().tolist() == [-1] * (top_k - n)
+        assert bool(torch.isinf(values[n:].cpu()).all())
+
+
 def test_lm_head_ties_break_to_lower_index(gpu_device):
     # duplicated rows give exactly equal logits: order must be index-ascending
     dev = gpu_device
