@@ -241,8 +241,10 @@ def _random_gemm_shapes(count, seed):
     return shapes
 
 
-# seed 11: 256 x 256 tiles with and without a half-height round, 256 x 128
-# tiles, 128- and 64-row tiles, and SwiGLU on 256 x 256 and 128-row tiles
+# seed 11: 256 x 256 tiles, 256 x 128 tiles with and without a
+# half-height round, 128- and 64-row tiles, and SwiGLU on 256 x 256,
+# 256 x 128 (with and without a half-height round) and 128-row tiles; the
+# 256 x 256 tiles with a half-height round are tested below
 @pytest.mark.parametrize("m,n,k", _random_gemm_shapes(8, 11))
 def test_gemm_random_shapes_match_oracle(gpu_device, m, n, k):
     print("random shape m={} n={} k={}".format(m, n, k), flush=True)
@@ -272,6 +274,31 @@ def test_gemm_random_shapes_match_oracle(gpu_device, m, n, k):
     _hip.up_mul_gemm(xd, w2d, g, split)
     _hip.gate_up_swiglu_gemm(xd, wd, w2d, fused)
     assert torch.equal(fused.cpu(), split.cpu())
+
+
+def test_swiglu_gemm_wide_tiles_with_half_round(gpu_device):
+    # The smallest shapes that still run 256 x 256 tiles with a last round
+    # of 128 x 256 half-height tiles are large SwiGLUs such as this one
+    # (M = 1537, 2 x 52736 columns).  The fused launch equals the split
+    # silu / mul launches bit for bit, and the gate GEMM's first rows stay
+    # within the float64 product bound.
+    m, n, k = 1537, 52736, 64
+    print("swiglu wide tiles m={} n={} k={}".format(m, n, k), flush=True)
+    dev = gpu_device
+    x = cases.normal_bf16((m, k), 201)
+    wg = cases.normal_bf16((n, k), 202, 0.05)
+    wu = cases.normal_bf16((n, k), 203, 0.05)
+    xd, wgd, wud = x.to(dev), wg.to(dev), wu.to(dev)
+    g = torch.empty((m, n), dtype=BF16, device=dev)
+    split = torch.empty_like(g)
+    fused = torch.empty_like(g)
+    _hip.gate_silu_gemm(xd, wgd, g)
+    _hip.up_mul_gemm(xd, wud, g, split)
+    _hip.gate_up_swiglu_gemm(xd, wgd, wud, fused)
+    assert torch.equal(fused, split)
+    y = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm(xd, wgd, y)
+    assert linear_bound_report(y[:64], x[:64], wg) <= 1.0
 
 
 def _rope_tables(positions):
