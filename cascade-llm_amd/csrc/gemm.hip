@@ -192,10 +192,12 @@ __device__ __forceinline__ int gemm_col(int wn, int j, int lr) {
   return 16 * T::H * wn + 16 * (j % T::H) + 64 * (j / T::H) + lr;
 }
 
+// only_j >= 0: store only fragment column only_j (the element-wise
+// epilogues; RoPE and SwiGLU pair fragment j with j + H and need both).
 template <int EPI, class T>
 __device__ __forceinline__ void gemm_epilogue(
     const GemmArgs &a, int tm, int tn, int wm, int wn, int lane,
-    const f32x4 (&acc)[T::FM][T::FN]) {
+    const f32x4 (&acc)[T::FM][T::FN], int only_j = -1) {
   const int lr = lane & 15;
   const int lq = lane >> 4;
 #pragma unroll
@@ -251,6 +253,7 @@ __device__ __forceinline__ void gemm_epilogue(
       } else {
 #pragma unroll
         for (int j = 0; j < T::FN; ++j) {
+          if (only_j >= 0 && j != only_j) continue;
           const int64_t col =
               static_cast<int64_t>(tn) * kTileN + gemm_col<T>(wn, j, lr);
           if (col >= a.n0) continue;
@@ -824,14 +827,16 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_
 // padding so the fragment reads of 16 rows spread over the banks, and each
 // wave runs the MFMAs of its quarter of a slab's K.  The waves' fp32 partials are summed through LDS in wave
 // order and wave 0 runs the element-wise epilogue.
-template <int MR>
+template <int MR, int NF = 2>
 struct SkinnyShape {
   using T = GemmTile<MR, 1, 4>;  // one 16 x 32 column pair of MR rows per workgroup
+  static_assert(NF == 1 || NF == 2, "a column pair or one fragment of it");
   static constexpr int SLAB_K = MR == 16 ? 512 : 256;
   static constexpr int RUN = SLAB_K * 2;          // bytes of one row in a slab
   static constexpr int RPI = 1024 / RUN;          // rows per load instruction (1 KiB)
   static constexpr int LINE = 1024 + 16;          // LDS pitch of one instruction's rows
-  static constexpr int SLAB_ROWS = 2 * 16 + MR;   // W rows of the pair, X rows
+  static constexpr int WROWS = 16 * NF;           // W rows of the fragment(s)
+  static constexpr int SLAB_ROWS = WROWS + MR;    // W rows, then X rows
   static constexpr int STAGES = 3;
   static constexpr int WAVES = 4;
   static constexpr int LOADS = SLAB_ROWS / RPI / WAVES;  // per wave and slab
@@ -847,16 +852,24 @@ constexpr int kSkinnyRows = 64;
 // (r / RPI) * LINE + (r % RPI) * RUN of its buffer.  With 512-byte runs two
 // rows share one 1 KiB line, so a fragment read (16 rows) meets each bank
 // group twice; with 1 KiB runs, once.
-template <int EPI, int MR>
+template <int EPI, int MR, int NF = 2>
 __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_kernel(GemmArgs a) {
-  using S = SkinnyShape<MR>;
+  using S = SkinnyShape<MR, NF>;
   using T = typename S::T;
+  static_assert(S::WAVES == SkinnyShape<MR>::WAVES, "one workgroup size");
+  static_assert(NF == 2 || (EPI != kGemmQkvRope && EPI != kGemmSwiglu),
+                "RoPE and SwiGLU pair fragment j with j + 1");
   constexpr int kSlabBytes = S::SLAB_ROWS / S::RPI * S::LINE;
   __shared__ __attribute__((aligned(16))) unsigned char ring[S::STAGES * kSlabBytes];
-  static_assert(S::WAVES * T::FM * T::FN * kWave * sizeof(f32x4) <= sizeof(ring),
+  static_assert(S::WAVES * T::FM * NF * kWave * sizeof(f32x4) <= sizeof(ring),
                 "the reduction fits in the ring");
-  const int tn = static_cast<int>(blockIdx.x) / T::WN;
+  // NF = 2: workgroup x holds the fragment pair of wave column x % 4 of
+  // tile x / 4; NF = 1: fragment (x / 4) % 2 of wave column x % 4 of tile
+  // x / 8 (twice the workgroups for the same columns)
+  constexpr int kPerTile = T::WN * (2 / NF);
+  const int tn = static_cast<int>(blockIdx.x) / kPerTile;
   const int wn = static_cast<int>(blockIdx.x) % T::WN;
+  const int jsel = NF == 2 ? 0 : (static_cast<int>(blockIdx.x) % kPerTile) / T::WN;
   const int rb = static_cast<int>(blockIdx.y);  // block of MR rows of X
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -868,7 +881,7 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
   // tile column gemm_col(wn, r / 16, r % 16)); rows past a matrix read as
   // zeros through its buffer bounds
   auto w_row = [&](int r, const uint16_t *&base, int64_t &rows) -> int64_t {
-    const int j = r / 16;
+    const int j = NF == 2 ? r / 16 : jsel;
     const int tc = gemm_col<T>(wn, j, r % 16);
     if constexpr (EPI == kGemmSwiglu) {
       base = tc < kGemmHalfHead ? a.w0 : a.w1;
@@ -898,10 +911,10 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
     const int r0 = (wave * S::LOADS + t) * S::RPI;
     const uint16_t *base;
     int64_t rows, row;
-    if (r0 < 32) {
+    if (r0 < S::WROWS) {
       row = w_row(r0, base, rows);
     } else {
-      base = a.x; rows = a.m; row = static_cast<int64_t>(rb) * MR + r0 - 32;
+      base = a.x; rows = a.m; row = static_cast<int64_t>(rb) * MR + r0 - S::WROWS;
     }
     rsrc[t] = buffer_rsrc_words(base, rows * row_bytes);
     voff[t] = static_cast<int>((row + lane / kLanesPerRow) * row_bytes) +
@@ -919,11 +932,11 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
   // fragment reads: lane (lr, g4) of 32-deep chunk q reads row lr of the
   // operand's 16-row group, bytes 64 q + 16 g4 of its run
   auto row_at = [&](int r) { return (r / S::RPI) * S::LINE + (r % S::RPI) * S::RUN; };
-  f32x4 acc[T::FM][T::FN];
+  f32x4 acc[T::FM][NF];
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NF; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   constexpr int kChunks = S::SLAB_K / 32 / S::WAVES;  // per wave and slab
   auto compute = [&](int slab, int buf) {
     const unsigned char *b0 = ring + buf * kSlabBytes + 16 * g4;
@@ -933,17 +946,18 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
     for (int q = 0; q < kChunks; ++q) {
       const int chunk = wave * kChunks + q;
       if (chunk >= valid) break;  // wave-uniform: the last slab of a short K
-      u32x4 xa[T::FM], wb[T::FN];
+      u32x4 xa[T::FM], wb[NF];
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
-        xa[i] = *reinterpret_cast<const u32x4 *>(b0 + row_at(32 + 16 * i + lr) + 64 * chunk);
+        xa[i] = *reinterpret_cast<const u32x4 *>(b0 + row_at(S::WROWS + 16 * i + lr) +
+                                                 64 * chunk);
 #pragma unroll
-      for (int j = 0; j < T::FN; ++j)
+      for (int j = 0; j < NF; ++j)
         wb[j] = *reinterpret_cast<const u32x4 *>(b0 + row_at(16 * j + lr) + 64 * chunk);
 #pragma unroll
       for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < T::FN; ++j) acc[i][j] = mfma_16x16x32_bf16(xa[i], wb[j], acc[i][j]);
+        for (int j = 0; j < NF; ++j) acc[i][j] = mfma_16x16x32_bf16(xa[i], wb[j], acc[i][j]);
     }
   };
   // slab s in buffer s % STAGES; step s waits for this wave's loads of
@@ -968,37 +982,63 @@ __global__ __launch_bounds__(SkinnyShape<MR>::WAVES *kWave) void gemm_skinny_ker
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
   __syncthreads();
-  f32x4(*partial)[T::FM * T::FN][kWave] =
-      reinterpret_cast<f32x4(*)[T::FM * T::FN][kWave]>(ring);
+  f32x4(*partial)[T::FM * NF][kWave] =
+      reinterpret_cast<f32x4(*)[T::FM * NF][kWave]>(ring);
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) partial[wave][i * T::FN + j][lane] = acc[i][j];
+    for (int j = 0; j < NF; ++j) partial[wave][i * NF + j][lane] = acc[i][j];
   __syncthreads();
   if (wave != 0) return;
+  // the wave partials in wave order, into the pair's fragment slots
+  f32x4 out[T::FM][T::FN];
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) {
-      f32x4 sum = partial[0][i * T::FN + j][lane];
-      for (int w = 1; w < S::WAVES; ++w) sum += partial[w][i * T::FN + j][lane];
-      acc[i][j] = sum;
+    for (int j = 0; j < T::FN; ++j) out[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+      f32x4 sum = partial[0][i * NF + j][lane];
+      for (int w = 1; w < S::WAVES; ++w) sum += partial[w][i * NF + j][lane];
+      if (NF == 2) {
+        out[i][j] = sum;
+      } else {  // no register array indexed at run time
+        out[i][0] = jsel == 0 ? sum : out[i][0];
+        out[i][1] = jsel == 1 ? sum : out[i][1];
+      }
     }
-  gemm_epilogue<EPI, T>(a, rb, tn, 0, wn, lane, acc);
+  gemm_epilogue<EPI, T>(a, rb, tn, 0, wn, lane, out, NF == 2 ? -1 : jsel);
 }
 
 template <int EPI>
 static hipError_t launch_skinny(GemmArgs &a, int64_t tiles_n, hipStream_t s) {
-  const int64_t grid = tiles_n * 4;  // one workgroup per column pair
-  if (grid > (int64_t{1} << 30)) return static_cast<hipError_t>(CASCADE_ESHAPE);
+  const int64_t pairs = tiles_n * 4;  // one workgroup per column pair
+  if (pairs > (int64_t{1} << 29)) return static_cast<hipError_t>(CASCADE_ESHAPE);
+  const unsigned blocks = a.m <= 16 ? 1u : static_cast<unsigned>((a.m + 63) / 64);
+  // where the column pairs would leave CUs idle (o_proj / down_proj,
+  // N = 4096: 128 pairs), the element-wise epilogues split each pair over
+  // two workgroups, one fragment each; RoPE and SwiGLU keep their pairs
+  constexpr bool kSplittable = EPI != kGemmQkvRope && EPI != kGemmSwiglu;
+  const bool split = kSplittable && 2 * pairs * blocks <= gemm_device_cus(s);
+  const unsigned grid = static_cast<unsigned>(split ? 2 * pairs : pairs);
+  if constexpr (kSplittable) {
+    if (split) {
+      if (a.m <= 16)
+        return launch_kernel(gemm_skinny_kernel<EPI, 16, 1>, dim3(grid),
+                             dim3(SkinnyShape<16, 1>::WAVES * kWave), 0, s, a);
+      return launch_kernel(gemm_skinny_kernel<EPI, 64, 1>, dim3(grid, blocks),
+                           dim3(SkinnyShape<64, 1>::WAVES * kWave), 0, s, a);
+    }
+  }
   if (a.m <= 16)
-    return launch_kernel(gemm_skinny_kernel<EPI, 16>, dim3(static_cast<unsigned>(grid)),
+    return launch_kernel(gemm_skinny_kernel<EPI, 16>, dim3(grid),
                          dim3(SkinnyShape<16>::WAVES * kWave), 0, s, a);
   // blocks of 64 rows side by side (grid.y); with an even pair count the
   // blocks of one column pair run on one XCD (linear index mod 8) and share
   // its W slabs through that XCD's L2
-  const unsigned blocks = static_cast<unsigned>((a.m + 63) / 64);
-  return launch_kernel(gemm_skinny_kernel<EPI, 64>, dim3(static_cast<unsigned>(grid), blocks),
+  return launch_kernel(gemm_skinny_kernel<EPI, 64>, dim3(grid, blocks),
                        dim3(SkinnyShape<64>::WAVES * kWave), 0, s, a);
 }
 
