@@ -76,6 +76,35 @@ def test_gemm_matches_oracle(gpu_device, m, n, k):
     assert r["ok"], r
 
 
+@pytest.mark.parametrize("m", [3, 16, 40, 64])
+def test_skinny_single_fragment_equals_column_pairs(gpu_device, m):
+    # At N = 4096 the short-prompt kernels give each 16-column fragment its
+    # own workgroup (the column pairs would fill half the CUs); at
+    # N = 14336 they keep the pairs.  The first 4096 columns of the wide
+    # product are the narrow product, so the two forms must agree bit for
+    # bit, for the plain, residual and fp32 epilogues.
+    print("skinny single-fragment m={}".format(m), flush=True)
+    dev = gpu_device
+    k = 4096
+    x = cases.normal_bf16((m, k), 121).to(dev)
+    w = cases.normal_bf16((14336, k), 122, 0.02).to(dev)
+    res = cases.normal_bf16((m, 14336), 123).to(dev)
+    narrow = torch.empty((m, 4096), dtype=BF16, device=dev)
+    wide = torch.empty((m, 14336), dtype=BF16, device=dev)
+    _hip.gemm(x, w[:4096], narrow)
+    _hip.gemm(x, w, wide)
+    assert torch.equal(narrow, wide[:, :4096])
+    res_narrow = res[:, :4096].contiguous()
+    _hip.gemm_residual(x, w[:4096], res_narrow, narrow)
+    _hip.gemm_residual(x, w, res, wide)
+    assert torch.equal(narrow, wide[:, :4096])
+    f_narrow = torch.empty((m, 4096), dtype=torch.float32, device=dev)
+    f_wide = torch.empty((m, 14336), dtype=torch.float32, device=dev)
+    _hip.gemm_f32out(x, w[:4096], f_narrow)
+    _hip.gemm_f32out(x, w, f_wide)
+    assert torch.equal(f_narrow, f_wide[:, :4096])
+
+
 @pytest.mark.parametrize("m", [5, 37])
 def test_gemm_f32out_matches_float64(gpu_device, m):
     # m = 5: the skinny kernel's fp32 epilogue; m = 37: 64-row tiles
