@@ -58,6 +58,14 @@ def test_argument_checks_reject_without_launching():
     assert lib.cascade_lm_head_topk_bf16(16, 100, 4096, 0, 16, 65, 1, None, 16,
                                          1 << 20, 16, 16, None) == 1001
     assert lib.cascade_memcpy_h2d_async(None, None, 0, None) == 1001
+    # top-k of a logits row: pointers, 1 <= top_k <= 64, workspace size and
+    # alignment
+    ws_bytes = _hip.lm_head_workspace_bytes(1000, 10)
+    assert lib.cascade_topk_f32(None, 1000, 10, 16, ws_bytes, 16, 16, None) == 1001
+    assert lib.cascade_topk_f32(16, 1000, 65, 16, ws_bytes, 16, 16, None) == 1001
+    assert lib.cascade_topk_f32(16, 0, 10, 16, ws_bytes, 16, 16, None) == 1001
+    assert lib.cascade_topk_f32(16, 1000, 10, 16, ws_bytes - 4, 16, 16, None) == 1004
+    assert lib.cascade_topk_f32(16, 1000, 10, 20, ws_bytes, 16, 16, None) == 1002
     # prefill attention: cache positions past + tokens are limited to 2^24,
     # head_dim to 128 and n_q_heads to 4 n_kv_heads
     pos = 1 << 24
