@@ -449,7 +449,9 @@ def resident_prefill(args, executor, runtime, dev):
         "workload": "{}-token random-ID prompt through the config-4 executor "
                     "(matrix_group, all weights HBM-resident): 1 warm-up + {} "
                     "timed prefills + 1 with every GEMM and attention launch "
-                    "timed".format(tokens, args.prefill_repeats),
+                    "timed; wall time from begin() to finish(): 32 layers, the "
+                    "fp32 logits of every position (the reference's resident "
+                    "finish) and the last row's top-k".format(tokens, args.prefill_repeats),
         "prefill_ms_median": round(median, 2),
         "prompt_tokens_per_s": round(tokens / (median / 1e3), 1),
         "gemm": gemms,
