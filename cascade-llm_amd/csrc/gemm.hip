@@ -132,6 +132,11 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n, tiles, per_xcd;
   int32_t htiles_m, htiles_n, htiles, hper_xcd;
   int32_t vec_out;  // row pitches and widths allow 16-byte output accesses
+  // split K (fp32 partials, kGemmF32 only): workgroup row blockIdx.y runs
+  // slabs [blockIdx.y * split_slabs, + split_slabs) of K and writes its
+  // partial at yf + blockIdx.y * split_stride; 0: the whole K
+  int32_t split_slabs;
+  int64_t split_stride;
 };
 
 __device__ __forceinline__ float gemm_silu(float g) {
@@ -560,7 +565,9 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
 #pragma unroll
     for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int slabs = static_cast<int>(a.k / BK);
+  const int slab0 = a.split_slabs ? static_cast<int>(blockIdx.y) * a.split_slabs : 0;
+  const int slabs = a.split_slabs ? min(a.split_slabs, static_cast<int>(a.k / BK) - slab0)
+                                  : static_cast<int>(a.k / BK);
   // LDS byte address of sb0 (the ring's buffer b starts kSlab * 2 b bytes
   // later)
   const uint32_t ring_lds = lds_address(sb0);
@@ -572,7 +579,7 @@ __device__ __forceinline__ void gemm_tile_run(const GemmArgs &a, int tm, int tn,
   auto ring_load_one = [&](int slab, int buf, int h) __attribute__((always_inline)) {
     const uint32_t dx = ring_lds + static_cast<uint32_t>(buf * kSlab * 2);
     const uint32_t dw = dx + XB * 2;
-    const int kb = slab * BK * 2;
+    const int kb = (slab0 + slab) * BK * 2;
     if (h < XW) {
       const int i = wave * XW + h;
       const int64_t row = static_cast<int64_t>(tm) * T::BM + L::RPI * i;
@@ -737,6 +744,9 @@ __global__ __launch_bounds__(T::WAVES *kWave) void gemm_kernel(GemmArgs a) {
                            : GemmRing<TH, STAGES_H, BK>::LDS;
   static_assert(kLds * 2 <= 160 * 1024, "LDS of one CU");
   __shared__ __attribute__((aligned(16))) uint16_t sb0[kLds];
+  if constexpr (EPI == kGemmF32) {
+    if (a.split_slabs) a.yf += static_cast<int64_t>(blockIdx.y) * a.split_stride;
+  }
   const int xcd = static_cast<int>(blockIdx.x % kXcds);
   const int j = static_cast<int>(blockIdx.x / kXcds);
   int tm, tn;
@@ -777,7 +787,8 @@ static int gemm_device_cus(hipStream_t s) {
 }
 
 template <int EPI, int BK, class T, int STAGES, class TH = T, int STAGES_H = STAGES>
-static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_t s) {
+static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_t s,
+                               int splits = 1) {
   const int64_t tiles_m = (a.m + T::BM - 1) / T::BM;
   const int64_t htiles_m = (a.m + TH::BM - 1) / TH::BM;
   int64_t tail_n = 0;
@@ -808,7 +819,8 @@ static hipError_t launch_tiles(GemmArgs &a, int64_t tiles_n, int cus, hipStream_
               (a.kv_head_stride % 8 == 0);
   const int64_t grid = static_cast<int64_t>(kXcds) * (a.per_xcd + a.hper_xcd);
   return launch_kernel(gemm_kernel<EPI, T, STAGES, TH, STAGES_H, BK>,
-                       dim3(static_cast<unsigned>(grid)), dim3(T::WAVES * kWave), 0, s, a);
+                       dim3(static_cast<unsigned>(grid), static_cast<unsigned>(splits)),
+                       dim3(T::WAVES * kWave), 0, s, a);
 }
 
 // Short prompts (M <= 64 rows, or up to 256 over few columns).  The weights are nearly all the traffic, so
@@ -1150,6 +1162,96 @@ static int gemm_check_w(const void *w, int64_t n, int64_t granule, int64_t k) {
 
 using namespace cascade;
 
+// Split K.  Where 256-row tiles would keep at most half of the CUs busy
+// (prompts of 65 to about 1000 rows over N = 4096: down_proj, and o_proj up
+// to 128 rows; M = 256, down_proj: 102.7 -> 46.1 us, M = 1024: 136.5 ->
+// 110.7 us, o_proj at M = 65: 28.5 -> 19.2 us), K is
+// split over up to kSplitMax rows of workgroups (blockIdx.y), each writing
+// an fp32 partial tile into the caller's workspace; a second launch sums
+// the partials in split order and applies the element-wise epilogue at the
+// same rounding points as the one-pass tile (bf16(sum), then the residual
+// add).  The partials associate the K sum differently from one pass, so a
+// result may differ from the one-pass tile in the last bf16 place, within
+// the same rounding bound.
+constexpr int kSplitMax = 8;
+constexpr int kSplitMinSlabs = 8;  // 64-deep slabs per split, at least
+
+struct SplitPlan {
+  int splits;  // 1: no split
+  int per;     // slabs per split
+};
+
+static SplitPlan split_plan(int64_t m, int64_t n, int64_t k, int cus) {
+  SplitPlan p{1, 0};
+  if (m <= kSkinnyRows || n % 8 != 0 || k % kTileK != 0) return p;
+  // short K past the skinny blocks: the one-pass 64-row tiles finish first
+  // (o_proj, M = 192..1024: 22.0..33.8 us one pass, 23.3..42.8 split)
+  if (k < 8192 && m > 2 * kSkinnyRows) return p;
+  const int64_t tiles = (m + 255) / 256 * ((n + kTileN - 1) / kTileN);
+  if (2 * tiles > cus) return p;
+  const int64_t slabs = k / kTileK;
+  const int64_t sp = std::min<int64_t>(std::min<int64_t>(kSplitMax, cus / tiles),
+                                       slabs / kSplitMinSlabs);
+  if (sp < 2) return p;
+  const int64_t per = (slabs + sp - 1) / sp;
+  p.splits = static_cast<int>((slabs + per - 1) / per);  // no empty split
+  p.per = static_cast<int>(per);
+  return p;
+}
+
+// y = epilogue(sum over s < splits of part[s]), 8 consecutive outputs per
+// thread (n % 8 == 0, so a group never crosses a row).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs a, int splits) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (i >= a.m * a.n0) return;
+  const float *p = a.yf + i;
+  f32x4 lo = *reinterpret_cast<const f32x4 *>(p);
+  f32x4 hi = *reinterpret_cast<const f32x4 *>(p + 4);
+  for (int sp = 1; sp < splits; ++sp) {
+    p += a.split_stride;
+    lo += *reinterpret_cast<const f32x4 *>(p);
+    hi += *reinterpret_cast<const f32x4 *>(p + 4);
+  }
+  const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  u32x4 aux = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (EPI == kGemmResidual) aux = *reinterpret_cast<const u32x4 *>(a.aux + i);
+  u32x4 out;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float v0 = round_bf16(v[2 * q]), v1 = round_bf16(v[2 * q + 1]);
+    if constexpr (EPI == kGemmResidual) {
+      v0 = lo_f(aux[q]) + v0;
+      v1 = hi_f(aux[q]) + v1;
+    }
+    out[q] = pack_bf16x2(v0, v1);
+  }
+  *reinterpret_cast<u32x4 *>(a.y + i) = out;
+}
+
+template <int EPI>
+static int gemm_split_k(const GemmArgs &a, const SplitPlan &p, void *ws,
+                        size_t ws_bytes, hipStream_t s) {
+  static_assert(EPI == kGemmStore || EPI == kGemmResidual, "element-wise epilogues");
+  const int64_t part = a.m * a.n0;
+  if (ws_bytes < static_cast<size_t>(p.splits) * part * sizeof(float))
+    return CASCADE_EWORKSPACE;
+  GemmArgs b = a;
+  b.yf = static_cast<float *>(ws);
+  b.ldy = a.n0;
+  b.split_slabs = p.per;
+  b.split_stride = part;
+  hipError_t e = launch_tiles<kGemmF32, kTileK, GemmTile256, 3>(
+      b, (a.n0 + kTileN - 1) / kTileN, gemm_device_cus(s), s, p.splits);
+  if (e != hipSuccess) return e;
+  GemmArgs r = a;
+  r.yf = static_cast<float *>(ws);
+  r.split_stride = part;
+  const int64_t groups = (part / 8 + 255) / 256;
+  return launch_kernel(gemm_split_reduce_kernel<EPI>, dim3(static_cast<unsigned>(groups)),
+                       dim3(256), 0, s, r, p.splits);
+}
+
 static int gemm_plain(int epi, const void *x, const void *w, const void *aux,
                       void *y, int64_t m, int64_t n, int64_t k, void *stream) {
   if (int e = gemm_check_x(x, m, k)) return e;
@@ -1196,6 +1298,59 @@ extern "C" int cascade_gemm_residual_bf16(const void *x, const void *w,
                                           int64_t m, int64_t n, int64_t k,
                                           void *stream) {
   return gemm_plain(kGemmResidual, x, w, residual, y, m, n, k, stream);
+}
+
+// The workspace forms: split K where the plan above applies (the workspace
+// then needs cascade_gemm_workspace_bytes() bytes), else the one-pass GEMM.
+static int gemm_ws(int epi, const void *x, const void *w, const void *aux,
+                   void *y, int64_t m, int64_t n, int64_t k, void *workspace,
+                   size_t workspace_bytes, void *stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const SplitPlan p = split_plan(m, n, k, gemm_device_cus(s));
+  if (p.splits == 1)
+    return gemm_plain(epi, x, w, aux, y, m, n, k, stream);
+  if (int e = gemm_check_x(x, m, k)) return e;
+  if (int e = gemm_check_w(w, n, 1, k)) return e;
+  if (y == nullptr || workspace == nullptr || (epi == kGemmResidual && aux == nullptr))
+    return CASCADE_EINVAL;
+  if (!aligned16(y) || !aligned16(workspace) || (aux != nullptr && !aligned16(aux)))
+    return CASCADE_EALIGN;
+  GemmArgs a{};
+  a.x = static_cast<const uint16_t *>(x);
+  a.w0 = static_cast<const uint16_t *>(w);
+  a.n0 = n;
+  a.m = m;
+  a.k = k;
+  a.y = static_cast<uint16_t *>(y);
+  a.ldy = n;
+  a.aux = static_cast<const uint16_t *>(aux);
+  return epi == kGemmResidual
+             ? gemm_split_k<kGemmResidual>(a, p, workspace, workspace_bytes, s)
+             : gemm_split_k<kGemmStore>(a, p, workspace, workspace_bytes, s);
+}
+
+extern "C" size_t cascade_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  const SplitPlan p = split_plan(m, n, k, gemm_device_cus(nullptr));
+  return p.splits > 1 ? static_cast<size_t>(p.splits) * m * n * sizeof(float) : 0;
+}
+
+extern "C" int cascade_gemm_ws_bf16(const void *x, const void *w, void *y,
+                                    int64_t m, int64_t n, int64_t k,
+                                    void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+  return gemm_ws(kGemmStore, x, w, nullptr, y, m, n, k, workspace,
+                 workspace_bytes, stream);
+}
+
+extern "C" int cascade_gemm_residual_ws_bf16(const void *x, const void *w,
+                                             const void *residual, void *y,
+                                             int64_t m, int64_t n, int64_t k,
+                                             void *workspace,
+                                             size_t workspace_bytes,
+                                             void *stream) {
+  return gemm_ws(kGemmResidual, x, w, residual, y, m, n, k, workspace,
+                 workspace_bytes, stream);
 }
 
 extern "C" int cascade_gate_silu_gemm_bf16(const void *x, const void *w_gate,

@@ -101,6 +101,10 @@ _SIGNATURES = {
         [_P, _I64, _I64, _I64, _P, _I64, _INT, _P, _P, _SZ, _P, _P, _P],
     ),
     "cascade_topk_f32": (_INT, [_P, _I64, _I64, _P, _SZ, _P, _P, _P]),
+    "cascade_gemm_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "cascade_gemm_ws_bf16": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "cascade_gemm_residual_ws_bf16": (
+        _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "cascade_embedding_gather_bf16": (
         _INT, [_P, _I64, _I64, _P, _I64, _P, _P, _P]),
     "cascade_decode_step_begin_bf16": (
@@ -125,7 +129,7 @@ _SIGNATURES = {
     "cascade_time_next_launch": (_INT, [_U64, _U64]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 ESHAPE = 1003  # CASCADE_ESHAPE
 # fused decode attention: sync buffer size and the bits it ors into the
 # caller's error word (include/cascade_hip.h)
@@ -437,26 +441,54 @@ def _rows(x, name, k):
     return x.numel() // k
 
 
-def gemm(x, weight, out, stream=None):
-    """out[M, N] = bf16(x[M, K] . weight[N, K]^T) on the matrix cores."""
+def gemm_workspace_bytes(m, n, k):
+    """Workspace bytes of the split-K forms for this shape on the current
+    device (0: these shapes run the one-pass GEMM)."""
+
+    return int(load().cascade_gemm_workspace_bytes(int(m), int(n), int(k)))
+
+
+def _ws(workspace):
+    if workspace is None:
+        return 0, 0
+    require_device(workspace, "workspace", torch.uint8)
+    return workspace.data_ptr(), workspace.numel()
+
+
+def gemm(x, weight, out, stream=None, workspace=None):
+    """out[M, N] = bf16(x[M, K] . weight[N, K]^T) on the matrix cores; with
+    a workspace (gemm_workspace_bytes) K may be split where the tiles would
+    leave CUs idle."""
 
     n, k = _matrix(weight, "weight")
     m = _rows(x, "x", k)
     _bf16(out, "out", m * n)
-    call("cascade_gemm_bf16", x.data_ptr(), weight.data_ptr(), out.data_ptr(),
-         m, n, k, stream_handle(stream))
+    if workspace is None:
+        call("cascade_gemm_bf16", x.data_ptr(), weight.data_ptr(), out.data_ptr(),
+             m, n, k, stream_handle(stream))
+    else:
+        ws, ws_bytes = _ws(workspace)
+        call("cascade_gemm_ws_bf16", x.data_ptr(), weight.data_ptr(),
+             out.data_ptr(), m, n, k, ws, ws_bytes, stream_handle(stream))
     return out
 
 
-def gemm_residual(x, weight, residual, out, stream=None):
-    """out = bf16(residual + bf16(x . weight^T)); out may be residual."""
+def gemm_residual(x, weight, residual, out, stream=None, workspace=None):
+    """out = bf16(residual + bf16(x . weight^T)); out may be residual; with a
+    workspace K may be split as in gemm()."""
 
     n, k = _matrix(weight, "weight")
     m = _rows(x, "x", k)
     _bf16(residual, "residual", m * n)
     _bf16(out, "out", m * n)
-    call("cascade_gemm_residual_bf16", x.data_ptr(), weight.data_ptr(),
-         residual.data_ptr(), out.data_ptr(), m, n, k, stream_handle(stream))
+    if workspace is None:
+        call("cascade_gemm_residual_bf16", x.data_ptr(), weight.data_ptr(),
+             residual.data_ptr(), out.data_ptr(), m, n, k, stream_handle(stream))
+    else:
+        ws, ws_bytes = _ws(workspace)
+        call("cascade_gemm_residual_ws_bf16", x.data_ptr(), weight.data_ptr(),
+             residual.data_ptr(), out.data_ptr(), m, n, k, ws, ws_bytes,
+             stream_handle(stream))
     return out
 
 

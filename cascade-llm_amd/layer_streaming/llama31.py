@@ -330,6 +330,7 @@ class Llama31DecodeExecutor:
         self._k_qkv_gemm = lib.cascade_qkv_rope_gemm_bf16
         self._k_prefill_attn = lib.cascade_prefill_attention_bf16
         self._k_gemm_residual = lib.cascade_gemm_residual_bf16
+        self._k_gemm_residual_ws = lib.cascade_gemm_residual_ws_bf16
         self._k_swiglu_gemm = lib.cascade_gate_up_swiglu_gemm_bf16
         self._k_silu_gemm = lib.cascade_gate_silu_gemm_bf16
         self._k_mul_gemm = lib.cascade_up_mul_gemm_bf16
@@ -352,6 +353,7 @@ class Llama31DecodeExecutor:
         # embedding (layer -1) and after every decoder layer.
         self.capture = None
         self._tokens_cap = 0
+        self._gemm_ws, self._gemm_ws_rows, self._gemm_ws_need = None, -1, 0
         self._attn_ws = None
         self._attn_ws_len = 0
         self._head_ws = None
@@ -395,6 +397,23 @@ class Llama31DecodeExecutor:
         self._gate_ptr = self._gate_buf.data_ptr()
         self._inter_ptr = self._inter.data_ptr()
         self._tokens_cap = tokens
+
+    def _gemm_workspace(self, tokens):
+        """(pointer, bytes) of the split-K workspace for o_proj / down_proj
+        over `tokens` rows ((0, 0) where those shapes run in one pass)."""
+
+        if tokens != self._gemm_ws_rows:
+            need = max(_hip.gemm_workspace_bytes(tokens, self.hidden, self.hidden),
+                       _hip.gemm_workspace_bytes(tokens, self.hidden,
+                                                 self.intermediate))
+            have = 0 if self._gemm_ws is None else self._gemm_ws.numel()
+            if need > have:
+                self._gemm_ws = torch.empty(need, dtype=torch.uint8,
+                                            device=self.device)
+            self._gemm_ws_rows, self._gemm_ws_need = tokens, need
+        if self._gemm_ws_need == 0:
+            return 0, 0
+        return self._gemm_ws.data_ptr(), self._gemm_ws.numel()
 
     def _ensure_attention_workspace(self, length):
         if length <= self._attn_ws_len:
@@ -771,11 +790,13 @@ class Llama31DecodeExecutor:
         self._mark_end("prefill_attention", ev, rc)
         _hip.check("cascade_prefill_attention_bf16", rc)
         x = state.hidden_states.data_ptr()
+        ws, ws_bytes = self._gemm_workspace(tokens)
         ev = self._mark_begin("gemm_o")
-        rc = self._k_gemm_residual(self._attn_ptr, ptrs["o_proj"], x, x, tokens,
-                                   self.hidden, self.hidden, stream)
+        rc = self._k_gemm_residual_ws(self._attn_ptr, ptrs["o_proj"], x, x,
+                                      tokens, self.hidden, self.hidden, ws,
+                                      ws_bytes, stream)
         self._mark_end("gemm_o", ev, rc)
-        _hip.check("cascade_gemm_residual_bf16", rc)
+        _hip.check("cascade_gemm_residual_ws_bf16", rc)
         self.kv_cache.set_length(layer, self._first_slot + tokens)
 
     def _gate_up_rows(self, layer, ptrs, state, stream):
@@ -806,12 +827,14 @@ class Llama31DecodeExecutor:
 
     def _down_rows(self, layer, ptrs, state, stream):
         x = state.hidden_states.data_ptr()
+        tokens = len(state.positions)
+        ws, ws_bytes = self._gemm_workspace(tokens)
         ev = self._mark_begin("gemm_down")
-        rc = self._k_gemm_residual(self._inter_ptr, ptrs["down_proj"], x, x,
-                                   len(state.positions), self.hidden,
-                                   self.intermediate, stream)
+        rc = self._k_gemm_residual_ws(self._inter_ptr, ptrs["down_proj"], x, x,
+                                      tokens, self.hidden, self.intermediate, ws,
+                                      ws_bytes, stream)
         self._mark_end("gemm_down", ev, rc)
-        _hip.check("cascade_gemm_residual_bf16", rc)
+        _hip.check("cascade_gemm_residual_ws_bf16", rc)
         if self.capture is not None:
             self.capture.append((layer, state.hidden_states.detach().clone()))
 

@@ -34,8 +34,10 @@ extern "C" {
 
 /* 2: cascade_hbm_read takes a workgroup count; the one-launch decoder layer
    exports are gone.  3: cascade_decode_attention_fused_bf16 /
-   _fused_at_bf16 added.  4: cascade_topk_f32 added. */
-#define CASCADE_ABI_VERSION 4
+   _fused_at_bf16 added.  4: cascade_topk_f32 added.  5: the split-K
+   workspace forms cascade_gemm_ws_bf16 / cascade_gemm_residual_ws_bf16 and
+   cascade_gemm_workspace_bytes added. */
+#define CASCADE_ABI_VERSION 5
 
 /* Argument errors (no work enqueued). */
 #define CASCADE_EINVAL 1001     /* null pointer, bad size or count */
@@ -238,6 +240,26 @@ int cascade_gemm_bf16(const void *x, const void *w, void *y, int64_t m,
 int cascade_gemm_residual_bf16(const void *x, const void *w,
                                const void *residual, void *y, int64_t m,
                                int64_t n, int64_t k, void *stream);
+/* The same two products with a workspace: where 256-row tiles would keep at
+ * most half of the device's CUs busy (M > 64 rows, N a multiple of 8,
+ * typically 65..1000 prompt rows over N = 4096: o_proj, down_proj), K is
+ * split over up to 8 groups of workgroups writing fp32 partials into the
+ * workspace, which a second launch sums in split order before the
+ * epilogue (same rounding points; the sum's association may move a result
+ * by one bf16 place against the one-pass form).  Elsewhere they run the
+ * one-pass GEMM and the workspace is not touched.  The workspace needs
+ * cascade_gemm_workspace_bytes(m, n, k) bytes for the current device (0:
+ * no split for this shape; a null workspace is then accepted), 16-byte
+ * aligned; calls sharing one workspace must be ordered on one stream.
+ * Replace the same F.linear calls as the forms above.                     */
+size_t cascade_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int cascade_gemm_ws_bf16(const void *x, const void *w, void *y, int64_t m,
+                         int64_t n, int64_t k, void *workspace,
+                         size_t workspace_bytes, void *stream);
+int cascade_gemm_residual_ws_bf16(const void *x, const void *w,
+                                  const void *residual, void *y, int64_t m,
+                                  int64_t n, int64_t k, void *workspace,
+                                  size_t workspace_bytes, void *stream);
 /* fp32 y[M, N] = X . W^T, not rounded: the resident LM head over every
  * position, F.linear(normalized, lm_head).float() (llama31.py:330-334).    */
 int cascade_gemm_f32out_bf16(const void *x, const void *w, float *y,

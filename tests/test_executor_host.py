@@ -225,6 +225,9 @@ class FakeKernels:
         at(y, m * n).copy_(out.reshape(-1))
         return 0
 
+    def gemm_residual_ws(self, x, w, res, y, m, n, k, ws, ws_bytes, stream):
+        return self.gemm_residual(x, w, res, y, m, n, k, stream)
+
     def swiglu_gemm(self, x, wg, wu, y, m, n, k, stream):
         self.calls.append("swiglu_gemm")
         xx = at(x, m * k).view(m, k)
@@ -321,6 +324,7 @@ def make_executor(monkeypatch, plan, store):
     ex._k_rmsnorm, ex._k_head = fakes.rmsnorm, fakes.head
     ex._k_qkv_gemm, ex._k_prefill_attn = fakes.qkv_gemm, fakes.prefill_attention
     ex._k_gemm_residual, ex._k_swiglu_gemm = fakes.gemm_residual, fakes.swiglu_gemm
+    ex._k_gemm_residual_ws = fakes.gemm_residual_ws
     ex._k_silu_gemm, ex._k_mul_gemm = fakes.silu_gemm, fakes.mul_gemm
     ex._k_f32_gemm, ex._k_topk = fakes.f32_gemm, fakes.topk
     ex._k_qkv_at, ex._k_attn_at = fakes.qkv_at, fakes.attention_at

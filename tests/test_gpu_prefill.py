@@ -105,6 +105,50 @@ def test_skinny_single_fragment_equals_column_pairs(gpu_device, m):
     assert torch.equal(f_narrow, f_wide[:, :4096])
 
 
+@pytest.mark.parametrize("m,k", [(65, 4096), (128, 4096), (100, 14336),
+                                 (256, 14336), (300, 14336), (512, 14336),
+                                 (1000, 14336)])
+def test_gemm_split_k_matches_oracle(gpu_device, m, k):
+    # Prompts of 65..1000 rows over N = 4096 (down_proj; o_proj up to 128
+    # rows: past that its one-pass tiles are faster and no split is
+    # planned, checked at the end) split K
+    # over workgroup rows with fp32 partials in the caller's workspace: the
+    # plain and residual (in place, as the executor calls it) products stay
+    # within the float64 product bound and the oracle's tolerance; a
+    # workspace one byte short is refused before any launch.
+    print("split-K m={} k={}".format(m, k), flush=True)
+    dev = gpu_device
+    n = 4096
+    need = _hip.gemm_workspace_bytes(m, n, k)
+    assert need >= 2 * m * n * 4  # the shape splits on this device
+    x = cases.normal_bf16((m, k), 131)
+    w = cases.normal_bf16((n, k), 132, 0.02)
+    res = cases.normal_bf16((m, n), 133)
+    xd, wd = x.to(dev), w.to(dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    y = torch.empty((m, n), dtype=BF16, device=dev)
+    _hip.gemm(xd, wd, y, workspace=ws)
+    assert linear_bound_report(y, x, w) <= 1.0
+    r = cases.compare(y, ref.linear(x, w))
+    assert r["ok"], r
+    h = res.to(dev)
+    _hip.gemm_residual(xd, wd, h, h, workspace=ws)
+    r = cases.compare(h, res + ref.linear(x, w))
+    assert r["ok"], r
+    # the one-pass form of the same product agrees within one bf16 place
+    # (plus a small absolute slack for outputs whose exact value is ~0)
+    one = torch.empty_like(y)
+    _hip.gemm(xd, wd, one)
+    diff = (one.float() - y.float()).abs()
+    mag = torch.maximum(one.float().abs(), y.float().abs()).clamp_min(1e-30)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    assert bool((diff <= ulp + 2.0 ** -14).all())
+    with pytest.raises(_hip.HipCallError):
+        _hip.gemm(xd, wd, y, workspace=ws[: need - 16])
+    assert _hip.gemm_workspace_bytes(256, n, 4096) == 0
+    assert _hip.gemm_workspace_bytes(2048, n, 14336) == 0
+
+
 @pytest.mark.parametrize("m", [5, 37])
 def test_gemm_f32out_matches_float64(gpu_device, m):
     # m = 5: the skinny kernel's fp32 epilogue; m = 37: 64-row tiles
