@@ -584,15 +584,19 @@ def prefill_sweep(args):
         h = torch.zeros(m, HIDDEN, dtype=torch.bfloat16, device=dev)
         g = torch.empty(m, INTER, dtype=torch.bfloat16, device=dev)
         u = torch.empty_like(g)
+        # split-K workspace for o_proj / down_proj, as the executor passes
+        ws_bytes = max(_hip.gemm_workspace_bytes(m, HIDDEN, HIDDEN),
+                       _hip.gemm_workspace_bytes(m, HIDDEN, INTER))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
 
         def layer():
             _hip.gemm(x, wq, q)
             _hip.gemm(x, wk, k)
             _hip.gemm(x, wv, v)
-            _hip.gemm_residual(q, wo, h, h)
+            _hip.gemm_residual(q, wo, h, h, workspace=ws)
             _hip.gate_silu_gemm(x, wg, g)
             _hip.up_mul_gemm(x, wu, g, u)
-            _hip.gemm_residual(u, wd, h, h)
+            _hip.gemm_residual(u, wd, h, h, workspace=ws)
 
         times = []
         for rep in range(2 + 5):
@@ -612,7 +616,7 @@ def prefill_sweep(args):
                      "nominal_weight_gbps": round(layer_bytes / 1e9 / (ms / 1e3), 1),
                      "compute_over_copy": round(ms / copy_ms, 4)})
         log("prefill sweep M={}: {:.3f} ms, {:.1f} TFLOP/s".format(m, ms, tflops))
-        del x, q, k, v, h, g, u
+        del x, q, k, v, h, g, u, ws
     crossover = None
     for lo, hi in zip(rows, rows[1:]):
         if lo["compute_over_copy"] < 1.0 <= hi["compute_over_copy"]:
@@ -624,7 +628,8 @@ def prefill_sweep(args):
     return {
         "workload": "one layer's seven projections (q, k, v, o + residual, "
                     "gate + SiLU, up * gate, down + residual) at M prompt rows, "
-                    "weights read from HBM; 2 warm-up + 5 timed passes per M",
+                    "weights read from HBM, o/down with the split-K workspace; "
+                    "2 warm-up + 5 timed passes per M",
         "layer_weight_bytes": layer_bytes,
         "layer_copy_ms": round(copy_ms, 3),
         "layer_copy_gbps": round(layer_bytes / 1e9 / (copy_ms / 1e3), 2),

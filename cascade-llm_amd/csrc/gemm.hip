@@ -1163,7 +1163,7 @@ static int gemm_check_w(const void *w, int64_t n, int64_t granule, int64_t k) {
 using namespace cascade;
 
 // Split K.  Where 256-row tiles would keep at most half of the CUs busy
-// (prompts of 65 to about 1000 rows over N = 4096: down_proj, and o_proj up
+// (prompts of 17 to about 1000 rows over N = 4096: down_proj, and o_proj up
 // to 128 rows; M = 256, down_proj: 102.7 -> 46.1 us, M = 1024: 136.5 ->
 // 110.7 us, o_proj at M = 65: 28.5 -> 19.2 us), K is
 // split over up to kSplitMax rows of workgroups (blockIdx.y), each writing
@@ -1183,7 +1183,10 @@ struct SplitPlan {
 
 static SplitPlan split_plan(int64_t m, int64_t n, int64_t k, int cus) {
   SplitPlan p{1, 0};
-  if (m <= kSkinnyRows || n % 8 != 0 || k % kTileK != 0) return p;
+  // 16 rows and fewer: one skinny block per column pair streams the weight
+  // faster (M = 16, down_proj: 28.6 us one pass, 31.8 split; M = 24: 42.0
+  // against 32.2, M = 64: 51.1 against 34.4)
+  if (m <= 16 || n % 8 != 0 || k % kTileK != 0) return p;
   // short K past the skinny blocks: the one-pass 64-row tiles finish first
   // (o_proj, M = 192..1024: 22.0..33.8 us one pass, 23.3..42.8 split)
   if (k < 8192 && m > 2 * kSkinnyRows) return p;

@@ -241,8 +241,9 @@ int cascade_gemm_residual_bf16(const void *x, const void *w,
                                const void *residual, void *y, int64_t m,
                                int64_t n, int64_t k, void *stream);
 /* The same two products with a workspace: where 256-row tiles would keep at
- * most half of the device's CUs busy (M > 64 rows, N a multiple of 8,
- * typically 65..1000 prompt rows over N = 4096: o_proj, down_proj), K is
+ * most half of the device's CUs busy (M > 16 rows, N a multiple of 8,
+ * K a multiple of 64; 17..1024 prompt rows over N = 4096 with K = 14336,
+ * down_proj, and 17..128 rows with K = 4096, o_proj), K is
  * split over up to 8 groups of workgroups writing fp32 partials into the
  * workspace, which a second launch sums in split order before the
  * epilogue (same rounding points; the sum's association may move a result

@@ -105,11 +105,12 @@ def test_skinny_single_fragment_equals_column_pairs(gpu_device, m):
     assert torch.equal(f_narrow, f_wide[:, :4096])
 
 
-@pytest.mark.parametrize("m,k", [(65, 4096), (128, 4096), (100, 14336),
+@pytest.mark.parametrize("m,k", [(17, 4096), (40, 14336), (64, 4096),
+                                 (65, 4096), (128, 4096), (100, 14336),
                                  (256, 14336), (300, 14336), (512, 14336),
                                  (1000, 14336)])
 def test_gemm_split_k_matches_oracle(gpu_device, m, k):
-    # Prompts of 65..1000 rows over N = 4096 (down_proj; o_proj up to 128
+    # Prompts of 17..1000 rows over N = 4096 (down_proj; o_proj up to 128
     # rows: past that its one-pass tiles are faster and no split is
     # planned, checked at the end) split K
     # over workgroup rows with fp32 partials in the caller's workspace: the
@@ -146,6 +147,7 @@ def test_gemm_split_k_matches_oracle(gpu_device, m, k):
     with pytest.raises(_hip.HipCallError):
         _hip.gemm(xd, wd, y, workspace=ws[: need - 16])
     assert _hip.gemm_workspace_bytes(256, n, 4096) == 0
+    assert _hip.gemm_workspace_bytes(16, n, 14336) == 0
     assert _hip.gemm_workspace_bytes(2048, n, 14336) == 0
 
 
