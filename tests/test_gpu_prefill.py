@@ -105,11 +105,28 @@ def test_skinny_single_fragment_equals_column_pairs(gpu_device, m):
     assert torch.equal(f_narrow, f_wide[:, :4096])
 
 
-@pytest.mark.parametrize("m,k", [(17, 4096), (40, 14336), (64, 4096),
-                                 (65, 4096), (128, 4096), (100, 14336),
-                                 (256, 14336), (300, 14336), (512, 14336),
-                                 (1000, 14336)])
-def test_gemm_split_k_matches_oracle(gpu_device, m, k):
+def _random_split_shapes(count, seed):
+    # shapes the split plan takes: 17..1024 rows, N a multiple of 8 up to
+    # 4096 (so 256-row tiles fill at most half of 256 CUs), K a multiple of
+    # 64 with at least 16 slabs, K >= 8192 past 128 rows
+    import random
+    rng = random.Random(seed)
+    shapes = []
+    for _ in range(count):
+        m = rng.randint(17, 1024)
+        n = 8 * rng.randint(16, 512)
+        k = 64 * (rng.randint(16, 200) if m <= 128 else rng.randint(128, 200))
+        while m * n * k > 12e9:  # keeps the float64 bound quick
+            n = max(128, (n // 2) // 8 * 8)
+        shapes.append((m, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize("m,n,k", [(m, 4096, k) for m, k in (
+    (17, 4096), (40, 14336), (64, 4096), (65, 4096), (128, 4096),
+    (100, 14336), (256, 14336), (300, 14336), (512, 14336), (1000, 14336))]
+    + _random_split_shapes(6, 23))
+def test_gemm_split_k_matches_oracle(gpu_device, m, n, k):
     # Prompts of 17..1000 rows over N = 4096 (down_proj; o_proj up to 128
     # rows: past that its one-pass tiles are faster and no split is
     # planned, checked at the end) split K
@@ -117,9 +134,8 @@ def test_gemm_split_k_matches_oracle(gpu_device, m, k):
     # plain and residual (in place, as the executor calls it) products stay
     # within the float64 product bound and the oracle's tolerance; a
     # workspace one byte short is refused before any launch.
-    print("split-K m={} k={}".format(m, k), flush=True)
+    print("split-K m={} n={} k={}".format(m, n, k), flush=True)
     dev = gpu_device
-    n = 4096
     need = _hip.gemm_workspace_bytes(m, n, k)
     assert need >= 2 * m * n * 4  # the shape splits on this device
     x = cases.normal_bf16((m, k), 131)
@@ -146,9 +162,9 @@ def test_gemm_split_k_matches_oracle(gpu_device, m, k):
     assert bool((diff <= ulp + 2.0 ** -14).all())
     with pytest.raises(_hip.HipCallError):
         _hip.gemm(xd, wd, y, workspace=ws[: need - 16])
-    assert _hip.gemm_workspace_bytes(256, n, 4096) == 0
-    assert _hip.gemm_workspace_bytes(16, n, 14336) == 0
-    assert _hip.gemm_workspace_bytes(2048, n, 14336) == 0
+    assert _hip.gemm_workspace_bytes(256, 4096, 4096) == 0
+    assert _hip.gemm_workspace_bytes(16, 4096, 14336) == 0
+    assert _hip.gemm_workspace_bytes(2048, 4096, 14336) == 0
 
 
 @pytest.mark.parametrize("m", [5, 37])
