@@ -47,6 +47,7 @@ Run: python bench.py [--steps K] [--warmup W] [--context L]
 """
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -716,8 +717,10 @@ def streamed_decode(args):
     store.fill_random(seed=args.seed, device=dev)
     setup_s = time.perf_counter() - t0
     # the peak counts from here: the synthetic weights are drawn on the GPU
-    # in fp32 (GBs of temporaries a checkpoint load does not have)
+    # in fp32 (GBs of temporaries a checkpoint load does not have); earlier
+    # legs' objects that only a cycle still holds are collected first
     torch.cuda.synchronize(dev)
+    gc.collect()
     torch.cuda.empty_cache()
     torch.cuda.reset_peak_memory_stats(dev)
     allocated_before = torch.cuda.memory_allocated(dev)  # earlier legs' leftovers

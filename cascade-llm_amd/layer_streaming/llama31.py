@@ -34,6 +34,8 @@ cores: cascade_rmsnorm_bf16 over the rows, then
 Position ids with gaps run the per-token kernels for t = 0..S-1 instead.
 """
 
+import inspect
+import weakref
 from dataclasses import dataclass, field
 
 import torch
@@ -223,7 +225,13 @@ class _ErrorWord:
 
     def __init__(self, device, message, on_attention_error=None):
         self.message = message
-        self.on_attention_error = on_attention_error
+        # a method of the word's owner is held weakly: the owner holds the
+        # word, and a strong reference back would keep the owner and its
+        # device buffers alive until a cyclic garbage collection
+        if inspect.ismethod(on_attention_error):
+            self._on_attention_error = weakref.WeakMethod(on_attention_error)
+        else:
+            self._on_attention_error = lambda cb=on_attention_error: cb
         self.flag = torch.zeros(1, dtype=torch.int32, device=device)
         self.host = torch.zeros(1, dtype=torch.int32,
                                 pin_memory=device.type == "cuda")
@@ -252,8 +260,9 @@ class _ErrorWord:
             self.flag.zero_()
             self.host.zero_()
             if value & ~1:
-                if self.on_attention_error is not None:
-                    self.on_attention_error(value)
+                callback = self._on_attention_error()
+                if callback is not None:
+                    callback(value)
                 raise RuntimeError(_attention_error_message(value))
             raise IndexError(self.message)
 

@@ -534,3 +534,28 @@ def test_error_word_bits_name_their_cause():
         assert int(word.flag[0]) == 0
     assert resets == [_hip.ATTN_EPLACEMENT, _hip.ATTN_ETIMEOUT,
                       _hip.ATTN_EPLACEMENT | 1]
+
+
+def test_executor_is_freed_without_a_cycle_collection(monkeypatch, weights, exact_oracle):
+    # The error word keeps the executor's attention-failure method weakly:
+    # once the caller drops the executor (after a prefill and a decode step),
+    # reference counting alone frees it and its buffers, with the cyclic
+    # collector switched off.
+    import gc
+    import weakref
+
+    plan = build_llama31_8b_plan("matrix_group", num_layers=LAYERS)
+    executor, _ = make_executor(monkeypatch, plan, weights)
+    state = executor.finish(run_units(plan, weights, executor,
+                                      executor.begin(torch.tensor([list(range(3, 23))]))))
+    token = state.topk_indices.reshape(1, -1)[:, :1].clone()
+    executor.finish(run_units(plan, weights, executor, executor.begin(token)))
+    alive = weakref.ref(executor)
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        del executor, state
+        assert alive() is None
+    finally:
+        if was_enabled:
+            gc.enable()
