@@ -229,7 +229,8 @@ class DoubleBufferRuntime:
         self.prefetch_across_calls = True
         # called with a slot index when the last unit of a call that uses
         # that slot has been enqueued (VocabStreamingRuntime copies its
-        # first chunks from here)
+        # first chunks from here); a hook that returns False has no owner
+        # left, and the slot goes to the next call's prefetch instead
         self.release_hook = None
         # pinned_staging: called once per call, when the call's last unit has
         # gone to the staging workers (VocabStreamingRuntime queues the
@@ -564,8 +565,8 @@ class DoubleBufferRuntime:
             if following < count:
                 copy_unit(following)
                 ready[following] = self._ready[following]
-            elif self.release_hook is not None:
-                self.release_hook(slot)
+            elif self.release_hook is not None and self.release_hook(slot) is not False:
+                pass
             else:
                 self.prefetch_next_call(slot)
 

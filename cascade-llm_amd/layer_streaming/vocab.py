@@ -32,6 +32,7 @@ shape); the top-k order equals a stable descending sort of them.
 """
 
 import time
+import weakref
 
 import torch
 
@@ -66,6 +67,24 @@ def merge_topk(current_values, current_indices, candidate_values,
 def _pinned_rows(count, width):
     return torch.empty((count, width), dtype=torch.bfloat16, device="cpu",
                        pin_memory=True)
+
+
+def _weak_hook(method):
+    """``method`` as a hook for the transformer runtime that holds its owner
+    weakly (the owner holds that runtime, so a strong reference back would
+    keep both, and the owner's device buffers, alive until a cyclic garbage
+    collection); once the owner is gone the hook returns False."""
+
+    ref = weakref.WeakMethod(method)
+
+    def hook(*args):
+        target = ref()
+        if target is None:
+            return False
+        target(*args)
+        return None
+
+    return hook
 
 
 class VocabStreamingRuntime:
@@ -132,9 +151,9 @@ class VocabStreamingRuntime:
         # the first chunks follow the transformer's last units directly; a
         # pageable store's chunks are staged on its staging workers, the
         # first two queued behind the call's last unit
-        runtime.release_hook = self._copy_first_chunk
+        runtime.release_hook = _weak_hook(self._copy_first_chunk)
         if self._staged:
-            runtime.staging_done_hook = self._prestage_first_chunks
+            runtime.staging_done_hook = _weak_hook(self._prestage_first_chunks)
             add_reader = getattr(store, "add_reader", None)
             if add_reader is not None:
                 add_reader(self)  # staging jobs read the arena

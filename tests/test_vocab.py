@@ -153,3 +153,53 @@ def test_embedding_rows_through_alternating_buffer_halves(monkeypatch, row_buffe
     for n in range(groups):
         half = vocab._rows_free[n % halves].id
         assert waits[2 * n] == ("sync", half) and waits[2 * n + 1] == ("record", half)
+
+
+def test_release_hook_holds_the_vocabulary_runtime_weakly(monkeypatch):
+    # The transformer runtime's release hook forwards to the vocabulary
+    # runtime while it lives; dropping the vocabulary runtime frees it by
+    # reference counting alone (no cycle through the hook), after which the
+    # hook returns False and the transformer runtime prefetches its next
+    # call into the slot instead.
+    import gc
+    import weakref
+    from types import SimpleNamespace
+
+    from layer_streaming import _hip
+    from layer_streaming import vocab as vocab_mod
+    from layer_streaming.plan import build_llama31_8b_plan
+    from layer_streaming.weight_store import WeightStoreMode
+
+    class Event:
+        def __init__(self, enable_timing=False):
+            pass
+
+    released = []
+    monkeypatch.setattr(_hip, "load", lambda: None)
+    monkeypatch.setattr(_hip, "HipEvent", Event)
+    monkeypatch.setattr(vocab_mod, "_pinned_rows",
+                        lambda n, w: torch.empty((n, w), dtype=torch.bfloat16))
+    monkeypatch.setattr(vocab_mod.VocabStreamingRuntime, "_copy_first_chunk",
+                        lambda self, slot: released.append(slot))
+    plan = build_llama31_8b_plan("matrix_group", num_layers=1, stream_vocab=True)
+    table = torch.zeros(8, 4096, dtype=torch.bfloat16)
+    store = SimpleNamespace(mode=WeightStoreMode.FULL_PINNED, tensor=lambda key: table)
+    slots = [torch.empty(plan.slot_elements, dtype=torch.bfloat16, device="meta")
+             for _ in range(2)]
+    runtime = SimpleNamespace(device_slots=slots, device=torch.device("cpu"),
+                              copy_stream=None, compute_stream=None,
+                              coordinator=None, stage_call_ahead=lambda: None)
+    vocab = vocab_mod.VocabStreamingRuntime(plan, store, runtime)
+    assert runtime.release_hook(1) is None
+    assert released == [1]
+    alive = weakref.ref(vocab)
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        del vocab
+        assert alive() is None
+    finally:
+        if was_enabled:
+            gc.enable()
+    assert runtime.release_hook(0) is False
+    assert released == [1]
