@@ -66,6 +66,18 @@ def test_argument_checks_reject_without_launching():
     assert lib.cascade_topk_f32(16, 0, 10, 16, ws_bytes, 16, 16, None) == 1001
     assert lib.cascade_topk_f32(16, 1000, 10, 16, ws_bytes - 4, 16, 16, None) == 1004
     assert lib.cascade_topk_f32(16, 1000, 10, 20, ws_bytes, 16, 16, None) == 1002
+    # split-K GEMM forms, at a shape the plan splits (64 x 4096 x 14336):
+    # pointers, alignment and the workspace size are checked before launching
+    need = lib.cascade_gemm_workspace_bytes(64, 4096, 14336)
+    assert need >= 2 * 64 * 4096 * 4
+    assert lib.cascade_gemm_residual_ws_bf16(16, 16, 16, 16, 64, 4096, 14336,
+                                             None, need, None) == 1001
+    assert lib.cascade_gemm_residual_ws_bf16(16, 16, None, 16, 64, 4096, 14336,
+                                             16, need, None) == 1001
+    assert lib.cascade_gemm_residual_ws_bf16(16, 16, 16, 16, 64, 4096, 14336,
+                                             20, need, None) == 1002
+    assert lib.cascade_gemm_ws_bf16(16, 16, 16, 64, 4096, 14336, 16, need - 4,
+                                    None) == 1004
     # prefill attention: cache positions past + tokens are limited to 2^24,
     # head_dim to 128 and n_q_heads to 4 n_kv_heads
     pos = 1 << 24
